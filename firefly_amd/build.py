@@ -1,0 +1,93 @@
+"""Build the gfx950 shared library ``firefly_amd/libffkv.so`` (and the CPU checker under ``oracle/``).
+
+Every HIP and C++ source under ``firefly_amd/csrc`` is compiled with hipcc for gfx950 only and linked into one
+shared library whose exported C ABI is declared in ``include/ffkv.h``.  Objects go to ``firefly_amd/_build``;
+the library is written in-tree so it travels with the repository snapshot.
+
+Usage: ``python -m firefly_amd.build [--jobs N] [--no-oracle]``.
+"""
+
+from __future__ import annotations
+
+import argparse
+import concurrent.futures as cf
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+ROOT = PKG.parent
+CSRC = PKG / "csrc"
+BUILD = PKG / "_build"
+LIB = PKG / "libffkv.so"
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+ARCH = "gfx950"
+
+COMMON = [
+    "-O3",
+    "-std=c++20",
+    "-fPIC",
+    "-Wall",
+    "-Wno-unused-function",
+    f"-I{ROOT / 'include'}",
+    f"-I{CSRC}",
+]
+# Device code: gfx950 only; packed fp32 math stays off (hipcc's host pass warns that it does not know it).
+DEVICE = [f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+
+
+def _sources() -> list[Path]:
+    return sorted(list(CSRC.glob("*.hip")) + list(CSRC.glob("*.cpp")))
+
+
+def _compile(src: Path) -> Path:
+    obj = BUILD / (src.name + ".o")
+    cmd = [HIPCC, *COMMON, *DEVICE, "-c", str(src), "-o", str(obj)]
+    if src.suffix == ".hip":
+        cmd[1:1] = ["-x", "hip"]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"compile failed: {' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
+    return obj
+
+
+def build_library(jobs: int = 8) -> Path:
+    """Compile every source and link ``libffkv.so``.  Always rebuilds."""
+    BUILD.mkdir(exist_ok=True)
+    srcs = _sources()
+    with cf.ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
+        objs = list(ex.map(_compile, srcs))
+    tmp = LIB.with_suffix(".so.tmp")
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"link failed: {' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
+    os.replace(tmp, LIB)
+    return LIB
+
+
+def build_oracle() -> None:
+    """Build the CPU checker (and, where the reference sources exist, the compiled reference host code)."""
+    make = shutil.which("make") or "make"
+    subprocess.run([make, "-C", str(ROOT / "oracle"), "-j4"], check=True, capture_output=True, text=True)
+    if Path("/root/reference/src/scheduler.cc").exists():
+        subprocess.run([make, "-C", str(ROOT / "oracle"), "ref"], check=True, capture_output=True, text=True)
+
+
+def main(argv: list[str] | None = None) -> int:
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument("--jobs", type=int, default=8)
+    ap.add_argument("--no-oracle", action="store_true")
+    args = ap.parse_args(argv)
+    lib = build_library(args.jobs)
+    print(f"built {lib}")
+    if not args.no_oracle:
+        build_oracle()
+        print("built oracle")
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

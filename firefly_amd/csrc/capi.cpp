@@ -1,0 +1,242 @@
+// capi.cpp - the extern "C" boundary (include/ffkv.h): argument validation, split-K geometry, workspace
+// handling and error reporting around the HIP launchers.
+//
+// The reference launches without validating anything and reports launch errors on std::cerr
+// (src/kernels/attention.cu:487-491, src/model/qwen_model.cu:9-17); this layer returns a status code instead and
+// keeps a per-thread message for ffkv_last_error().
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <string>
+
+#include "ffkv.h"
+#include "ffkv_internal.h"
+
+namespace
+{
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...)
+{
+    char    buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+int ok()
+{
+    g_last_error.clear();
+    return FFKV_OK;
+}
+
+bool is_act(int dt) { return dt == FFKV_DTYPE_F32 || dt == FFKV_DTYPE_F16 || dt == FFKV_DTYPE_BF16; }
+bool is_cache(int dt) { return is_act(dt) || dt == FFKV_DTYPE_I8 || dt == FFKV_DTYPE_FP8_E4M3; }
+bool quantized(int dt) { return dt == FFKV_DTYPE_I8 || dt == FFKV_DTYPE_FP8_E4M3; }
+bool head_dim_ok(int d) { return d == 64 || d == 128 || d == 256; }
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+int hip_fail(hipError_t e, const char* what)
+{
+    return fail(FFKV_ERR_HIP, "%s: %s (%d)", what, hipGetErrorString(e), static_cast<int>(e));
+}
+
+int env_chunk()
+{
+    static const int v = []
+    {
+        const char* s = std::getenv("FFKV_DECODE_CHUNK");
+        return s ? std::atoi(s) : 0;
+    }();
+    return v;
+}
+
+}  // namespace
+
+namespace ffkv
+{
+
+int decode_cap_tokens(int max_blocks, int max_context_len)
+{
+    int64_t cap = static_cast<int64_t>(max_blocks) * kBlockSize;
+    if (max_context_len > 0 && cap > max_context_len) cap = max_context_len;
+    if (cap > (1 << 30)) cap = 1 << 30;
+    return cap < 0 ? 0 : static_cast<int>(cap);
+}
+
+// Smallest chunk the workspace is sized for: at least 256 tokens and at most 64 chunks per row.
+int decode_min_chunk(int cap_tokens)
+{
+    int64_t c = ceil_div(ceil_div(cap_tokens, 64), kBlockSize) * kBlockSize;
+    return static_cast<int>(c < 256 ? 256 : c);
+}
+
+// Grow the chunk while the grid still has >= 4096 work items at the row-length bound; long chunks cost fewer
+// partials, short chunks balance better.
+int decode_chunk(int batch, int num_kv_heads, int cap_tokens)
+{
+    const int min_chunk = decode_min_chunk(cap_tokens);
+    int       chunk = min_chunk;
+    if (env_chunk() > 0)
+    {
+        chunk = static_cast<int>(ceil_div(env_chunk(), kBlockSize) * kBlockSize);
+        return chunk < min_chunk ? min_chunk : chunk;
+    }
+    const int64_t pairs = static_cast<int64_t>(batch) * num_kv_heads;
+    while (chunk < 4096 && pairs * ceil_div(cap_tokens, 2 * chunk) >= 4096) chunk *= 2;
+    return chunk;
+}
+
+size_t decode_workspace_bytes(int batch, int num_heads, int head_dim, int cap_tokens)
+{
+    const int64_t chunks = ceil_div(cap_tokens, decode_min_chunk(cap_tokens));
+    if (chunks <= 1) return 0;
+    const int64_t parts = static_cast<int64_t>(batch) * num_heads * chunks;
+    const int64_t ml = ceil_div(parts * 2 * 4, 256) * 256;
+    return static_cast<size_t>(ml + parts * head_dim * 4);
+}
+
+}  // namespace ffkv
+
+extern "C" {
+
+const char* ffkv_last_error(void) { return g_last_error.c_str(); }
+
+const char* ffkv_version(void) { return "ffkv 0.1.0 gfx950"; }
+
+int ffkv_append(const void* k_src, const void* v_src, int src_dtype, void* k_cache, void* v_cache, int cache_dtype,
+                float* k_scale, float* v_scale, const int32_t* block_table, const int32_t* context_lens, int batch,
+                int seq_len, int num_kv_heads, int head_dim, int block_size, int max_blocks, int num_blocks,
+                void* stream)
+{
+    if (block_size != FFKV_BLOCK_SIZE) return fail(FFKV_ERR_UNSUPPORTED, "block_size must be 16, got %d", block_size);
+    if (!is_act(src_dtype)) return fail(FFKV_ERR_UNSUPPORTED, "unsupported source dtype %d", src_dtype);
+    if (!is_cache(cache_dtype)) return fail(FFKV_ERR_UNSUPPORTED, "unsupported cache dtype %d", cache_dtype);
+    if (!head_dim_ok(head_dim)) return fail(FFKV_ERR_UNSUPPORTED, "head_dim must be 64, 128 or 256, got %d", head_dim);
+    if (batch < 0 || seq_len < 0 || num_kv_heads <= 0 || max_blocks < 0 || num_blocks < 0)
+        return fail(FFKV_ERR_INVALID_ARGUMENT, "negative size (batch %d seq_len %d kv_heads %d max_blocks %d "
+                    "num_blocks %d)", batch, seq_len, num_kv_heads, max_blocks, num_blocks);
+    if (batch == 0 || seq_len == 0) return ok();
+    if (!k_src || !v_src || !k_cache || !v_cache || !block_table)
+        return fail(FFKV_ERR_INVALID_ARGUMENT, "null source, cache or block_table pointer");
+    if (quantized(cache_dtype) && (!k_scale || !v_scale))
+        return fail(FFKV_ERR_INVALID_ARGUMENT, "quantized cache needs k_scale and v_scale");
+    if (!aligned16(k_src) || !aligned16(v_src) || !aligned16(k_cache) || !aligned16(v_cache))
+        return fail(FFKV_ERR_INVALID_ARGUMENT, "source and cache pointers must be 16-byte aligned");
+
+    ffkv::AppendArgs a{k_src,      v_src,        k_cache,   v_cache,     k_scale,  v_scale,
+                       block_table, context_lens, src_dtype, cache_dtype, batch,    seq_len,
+                       num_kv_heads, head_dim,    max_blocks, num_blocks};
+    hipError_t e = ffkv::launch_append(a, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "append launch");
+    return ok();
+}
+
+size_t ffkv_decode_workspace_bytes(int batch, int num_heads, int head_dim, int max_blocks, int max_context_len)
+{
+    if (batch <= 0 || num_heads <= 0 || head_dim <= 0) return 0;
+    return ffkv::decode_workspace_bytes(batch, num_heads, head_dim,
+                                        ffkv::decode_cap_tokens(max_blocks, max_context_len));
+}
+
+int ffkv_paged_decode(const void* q, void* out, int qo_dtype, const void* k_cache, const void* v_cache,
+                      int cache_dtype, const float* k_scale, const float* v_scale, const int32_t* block_table,
+                      const int32_t* context_lens, int batch, int num_heads, int num_kv_heads, int head_dim,
+                      int block_size, int max_blocks, int num_blocks, int max_context_len, float scale,
+                      void* workspace, size_t workspace_bytes, void* stream)
+{
+    if (block_size != FFKV_BLOCK_SIZE) return fail(FFKV_ERR_UNSUPPORTED, "block_size must be 16, got %d", block_size);
+    if (!is_act(qo_dtype)) return fail(FFKV_ERR_UNSUPPORTED, "unsupported q/out dtype %d", qo_dtype);
+    if (!is_cache(cache_dtype)) return fail(FFKV_ERR_UNSUPPORTED, "unsupported cache dtype %d", cache_dtype);
+    if (!head_dim_ok(head_dim)) return fail(FFKV_ERR_UNSUPPORTED, "head_dim must be 64, 128 or 256, got %d", head_dim);
+    if (batch < 0 || num_heads <= 0 || num_kv_heads <= 0 || max_blocks < 0 || num_blocks < 0)
+        return fail(FFKV_ERR_INVALID_ARGUMENT, "bad size (batch %d heads %d kv_heads %d max_blocks %d num_blocks %d)",
+                    batch, num_heads, num_kv_heads, max_blocks, num_blocks);
+    if (num_heads % num_kv_heads != 0)
+        return fail(FFKV_ERR_INVALID_ARGUMENT, "num_heads %d is not a multiple of num_kv_heads %d", num_heads,
+                    num_kv_heads);
+    const int group = num_heads / num_kv_heads;
+    if (group > 16) return fail(FFKV_ERR_UNSUPPORTED, "GQA group size %d exceeds 16", group);
+    if (batch > 65535 || num_kv_heads > 65535)
+        return fail(FFKV_ERR_UNSUPPORTED, "batch and num_kv_heads must be <= 65535");
+    if (batch == 0) return ok();
+    if (!q || !out || !k_cache || !v_cache || !block_table || !context_lens)
+        return fail(FFKV_ERR_INVALID_ARGUMENT, "null q, out, cache, block_table or context_lens pointer");
+    if (quantized(cache_dtype) && (!k_scale || !v_scale))
+        return fail(FFKV_ERR_INVALID_ARGUMENT, "quantized cache needs k_scale and v_scale");
+    if (!aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache))
+        return fail(FFKV_ERR_INVALID_ARGUMENT, "q and cache pointers must be 16-byte aligned");
+
+    const int cap = ffkv::decode_cap_tokens(max_blocks, max_context_len);
+    const int chunk = ffkv::decode_chunk(batch, num_kv_heads, cap);
+    const int max_chunks = static_cast<int>(ceil_div(cap > 0 ? cap : 1, chunk));
+
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    void*       ws = workspace;
+    bool        owned = false;
+    size_t      need = 0;
+    float*      ws_ml = nullptr;
+    float*      ws_acc = nullptr;
+    if (max_chunks > 1)
+    {
+        const int64_t parts = static_cast<int64_t>(batch) * num_heads * max_chunks;
+        const int64_t ml = ceil_div(parts * 2 * 4, 256) * 256;
+        need = static_cast<size_t>(ml + parts * head_dim * 4);
+        if (ws == nullptr)
+        {
+            hipError_t e = hipMallocAsync(&ws, need, s);
+            if (e != hipSuccess) return hip_fail(e, "decode workspace hipMallocAsync");
+            owned = true;
+        }
+        else if (workspace_bytes < need)
+        {
+            return fail(FFKV_ERR_WORKSPACE, "workspace of %zu bytes is smaller than the %zu bytes needed", workspace_bytes,
+                        need);
+        }
+        ws_ml = static_cast<float*>(ws);
+        ws_acc = reinterpret_cast<float*>(static_cast<char*>(ws) + ml);
+    }
+
+    const float sm_scale = scale > 0.0f ? scale : 1.0f / sqrtf(static_cast<float>(head_dim));
+    ffkv::DecodeArgs a{q,
+                       out,
+                       k_cache,
+                       v_cache,
+                       k_scale,
+                       v_scale,
+                       block_table,
+                       context_lens,
+                       ws_ml,
+                       ws_acc,
+                       qo_dtype,
+                       cache_dtype,
+                       batch,
+                       num_heads,
+                       num_kv_heads,
+                       group,
+                       head_dim,
+                       max_blocks,
+                       num_blocks,
+                       cap,
+                       chunk,
+                       max_chunks,
+                       sm_scale * 1.4426950408889634f};
+    hipError_t e = ffkv::launch_decode(a, s);
+    if (owned)
+    {
+        hipError_t fe = hipFreeAsync(ws, s);
+        if (e == hipSuccess) e = fe;
+    }
+    if (e != hipSuccess) return hip_fail(e, "decode launch");
+    return ok();
+}
+
+}  // extern "C"

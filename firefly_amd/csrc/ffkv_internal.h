@@ -1,0 +1,69 @@
+// ffkv_internal.h - argument blocks and launchers shared by the C ABI layer and the HIP kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace ffkv
+{
+
+constexpr int kBlockSize = 16;  // tokens per KV page, fixed by the reference (include/firefly/scheduler.h:71)
+
+struct AppendArgs
+{
+    const void*    k_src;
+    const void*    v_src;
+    void*          k_cache;
+    void*          v_cache;
+    float*         k_scale;
+    float*         v_scale;
+    const int32_t* block_table;
+    const int32_t* context_lens;
+    int            src_dtype;
+    int            cache_dtype;
+    int            batch;
+    int            seq_len;
+    int            num_kv_heads;
+    int            head_dim;
+    int            max_blocks;
+    int            num_blocks;
+};
+
+struct DecodeArgs
+{
+    const void*    q;
+    void*          out;
+    const void*    k_cache;
+    const void*    v_cache;
+    const float*   k_scale;
+    const float*   v_scale;
+    const int32_t* block_table;
+    const int32_t* context_lens;
+    float*         ws_ml;   // [batch, num_heads, max_chunks, 2]: running max (log2 domain) and denominator
+    float*         ws_acc;  // [batch, num_heads, max_chunks, head_dim]: unnormalised output of each chunk
+    int            qo_dtype;
+    int            cache_dtype;
+    int            batch;
+    int            num_heads;
+    int            num_kv_heads;
+    int            group;  // num_heads / num_kv_heads
+    int            head_dim;
+    int            max_blocks;
+    int            num_blocks;
+    int            cap_tokens;  // attended tokens per row are clamped to this
+    int            chunk;       // tokens per split-K chunk (multiple of 16)
+    int            max_chunks;  // ceil(cap_tokens / chunk)
+    float          scale_log2;  // softmax scale * log2(e)
+};
+
+hipError_t launch_append(const AppendArgs& a, hipStream_t stream);
+hipError_t launch_decode(const DecodeArgs& a, hipStream_t stream);
+
+// Split-K geometry shared by the workspace query and the launcher.
+int    decode_cap_tokens(int max_blocks, int max_context_len);
+int    decode_min_chunk(int cap_tokens);
+int    decode_chunk(int batch, int num_kv_heads, int cap_tokens);
+size_t decode_workspace_bytes(int batch, int num_heads, int head_dim, int cap_tokens);
+
+}  // namespace ffkv

@@ -1,0 +1,333 @@
+// paged_decode.hip - PagedAttention decode for gfx950: GQA-shared KV reads, split-K over the context, online
+// softmax, and a merge pass.
+//
+// Reference semantics: paged_attention_kernel (src/kernels/attention.cu:291-447).  The reference runs one
+// 128-thread block per (query head, sequence), so every query head of a GQA group re-reads the same KV head, and
+// a long context is walked serially by one block.  Here one 256-thread workgroup owns a (chunk, kv_head,
+// sequence) work item: it loads the G = Hq/Hkv query vectors of the group once, reads each K/V page slice once
+// for all of them, and writes either the final output (rows that fit in one chunk) or an unnormalised partial
+// state (m, l, acc) that paged_decode_merge combines.
+//
+// Lane layout: head_dim/8 lanes per token (one 8-element, 16-byte chunk each for 16-bit KV), so a wave64 covers
+// 64/(D/8) tokens per step and the workgroup 256/(D/8).  Each token slot keeps its own online-softmax state in
+// registers; the slots are merged with cross-lane shuffles inside a wave and through LDS across waves.
+// The softmax runs in base 2 with log2(e) folded into the score scale.
+#include "ffkv_device.h"
+#include "ffkv_internal.h"
+
+namespace ffkv
+{
+
+namespace
+{
+
+constexpr float kNegBig = -1e30f;  // finite "minus infinity" seed, as in attention.cu:323
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ int row_tokens(const DecodeArgs& a, int b)
+{
+    int64_t L = static_cast<int64_t>(a.context_lens[b]) + 1;  // +1: the token appended this step (:320)
+    if (L > a.cap_tokens) L = a.cap_tokens;
+    return L < 0 ? 0 : static_cast<int>(L);
+}
+
+// Load 8 dequantized cache elements of row `row` (page*16 + slot)*Hkv + h at dims [d0, d0+8).
+template <int CT, int D>
+__device__ __forceinline__ void load_kv8(const void* cache, const float* scale, size_t row, int h, int d0, float* x)
+{
+    Raw8 raw;
+    load_raw8<CT>(cache, row * D + d0, raw);
+    unpack8<CT>(raw, x);
+    if constexpr (CT == I8)
+    {
+        const float s = scale[row];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) x[i] *= s;
+    }
+    else if constexpr (CT == FP8)
+    {
+        const float s = scale[h];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) x[i] *= s;
+    }
+}
+
+}  // namespace
+
+template <int CT, int D, int GP>
+__global__ __launch_bounds__(256) void paged_decode_generic(DecodeArgs a)
+{
+    constexpr int LPT = D / 8;     // lanes per token
+    constexpr int TPI = 256 / LPT; // token slots per workgroup
+    constexpr int WAVES = 4;
+
+    const int chunk_id = blockIdx.x;
+    const int kvh = blockIdx.y;
+    const int b = blockIdx.z;
+    const int tid = threadIdx.x;
+    const int lane = tid % LPT;
+    const int slot = tid / LPT;
+    const int wave = tid / 64;
+
+    const int L = row_tokens(a, b);
+    const int nch = (L + a.chunk - 1) / a.chunk;
+    if (chunk_id >= nch && !(chunk_id == 0 && nch == 0)) return;  // uniform over the workgroup
+    const int begin = chunk_id * a.chunk;
+    const int end = min(begin + a.chunk, L);
+    const int G = a.group;
+
+    float q[GP][8];
+#pragma unroll
+    for (int g = 0; g < GP; ++g)
+    {
+        if (g < G)
+            load_act8(a.q, a.qo_dtype, (static_cast<size_t>(b) * a.num_heads + kvh * G + g) * D + lane * 8, q[g]);
+        else
+#pragma unroll
+            for (int i = 0; i < 8; ++i) q[g][i] = 0.0f;
+    }
+
+    float m[GP], l[GP], acc[GP][8];
+#pragma unroll
+    for (int g = 0; g < GP; ++g)
+    {
+        m[g] = kNegBig;
+        l[g] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[g][i] = 0.0f;
+    }
+
+    const int32_t* table = a.block_table + static_cast<int64_t>(b) * a.max_blocks;
+    for (int base = begin; base < end; base += TPI)
+    {
+        const int j = base + slot;
+        bool      valid = j < end;
+        int       phys = -1;
+        if (valid)
+        {
+            phys = table[j >> 4];
+            valid = phys >= 0 && phys < a.num_blocks;
+        }
+        const size_t row = (static_cast<size_t>(valid ? phys : 0) * kBlockSize + (j & 15)) * a.num_kv_heads + kvh;
+
+        float s[GP];
+        float v[8];
+        if (valid)
+        {
+            float k[8];
+            load_kv8<CT, D>(a.k_cache, a.k_scale, row, kvh, lane * 8, k);
+            load_kv8<CT, D>(a.v_cache, a.v_scale, row, kvh, lane * 8, v);
+#pragma unroll
+            for (int g = 0; g < GP; ++g)
+            {
+                float d = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) d = __builtin_fmaf(q[g][i], k[i], d);
+                s[g] = d;
+            }
+        }
+        else
+        {
+#pragma unroll
+            for (int g = 0; g < GP; ++g) s[g] = 0.0f;
+        }
+        // every lane takes part in the shuffles; a token's lanes are a contiguous, aligned group
+#pragma unroll
+        for (int g = 0; g < GP; ++g)
+#pragma unroll
+            for (int off = LPT / 2; off > 0; off >>= 1) s[g] += shfl_xor(s[g], off);
+
+        if (valid)
+        {
+#pragma unroll
+            for (int g = 0; g < GP; ++g)
+            {
+                const float sg = s[g] * a.scale_log2;
+                const float mn = fmaxf(m[g], sg);
+                const float alpha = fast_exp2(m[g] - mn);
+                const float p = fast_exp2(sg - mn);
+                l[g] = __builtin_fmaf(l[g], alpha, p);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) acc[g][i] = __builtin_fmaf(acc[g][i], alpha, p * v[i]);
+                m[g] = mn;
+            }
+        }
+    }
+
+    // merge the token slots of this wave (lanes lane, lane+LPT, ... hold the same dims)
+#pragma unroll
+    for (int off = LPT; off < 64; off <<= 1)
+    {
+#pragma unroll
+        for (int g = 0; g < GP; ++g)
+        {
+            const float mo = shfl_xor(m[g], off);
+            const float lo = shfl_xor(l[g], off);
+            const float mn = fmaxf(m[g], mo);
+            const float a1 = fast_exp2(m[g] - mn);
+            const float a2 = fast_exp2(mo - mn);
+            l[g] = l[g] * a1 + lo * a2;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) acc[g][i] = acc[g][i] * a1 + shfl_xor(acc[g][i], off) * a2;
+            m[g] = mn;
+        }
+    }
+
+    // merge the waves through LDS, one wave at a time
+    __shared__ float s_acc[GP][D];
+    __shared__ float s_m[GP];
+    __shared__ float s_l[GP];
+    const bool holder = (tid % 64) < LPT;
+    for (int w = 0; w < WAVES; ++w)
+    {
+        if (wave == w && holder)
+        {
+#pragma unroll
+            for (int g = 0; g < GP; ++g)
+            {
+                if (w == 0)
+                {
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) s_acc[g][lane * 8 + i] = acc[g][i];
+                    if (lane == 0)
+                    {
+                        s_m[g] = m[g];
+                        s_l[g] = l[g];
+                    }
+                }
+                else
+                {
+                    const float mo = s_m[g];
+                    const float lo = s_l[g];
+                    const float mn = fmaxf(m[g], mo);
+                    const float a1 = fast_exp2(m[g] - mn);
+                    const float a2 = fast_exp2(mo - mn);
+#pragma unroll
+                    for (int i = 0; i < 8; ++i)
+                        s_acc[g][lane * 8 + i] = acc[g][i] * a1 + s_acc[g][lane * 8 + i] * a2;
+                    // all holder lanes read s_m/s_l before lane 0 overwrites them: same wave, lockstep
+                    __builtin_amdgcn_wave_barrier();
+                    if (lane == 0)
+                    {
+                        s_m[g] = mn;
+                        s_l[g] = l[g] * a1 + lo * a2;
+                    }
+                }
+            }
+        }
+        __syncthreads();
+    }
+
+    const int     hq0 = kvh * G;
+    const bool    single = nch <= 1;
+    const int64_t ml_base = (static_cast<int64_t>(b) * a.num_heads + hq0) * a.max_chunks + chunk_id;
+    for (int idx = tid; idx < G * D; idx += 256)
+    {
+        const int   g = idx / D;
+        const int   d = idx % D;
+        const float acc_v = s_acc[g][d];
+        if (single)
+        {
+            const float lsum = s_l[g];
+            store_act1(a.out, a.qo_dtype, (static_cast<size_t>(b) * a.num_heads + hq0 + g) * D + d,
+                       lsum > 0.0f ? acc_v / lsum : 0.0f);
+        }
+        else
+        {
+            const int64_t pi = ml_base + static_cast<int64_t>(g) * a.max_chunks;
+            a.ws_acc[pi * D + d] = acc_v;
+            if (d == 0)
+            {
+                a.ws_ml[2 * pi] = s_m[g];
+                a.ws_ml[2 * pi + 1] = s_l[g];
+            }
+        }
+    }
+}
+
+// Combine the chunk partials of rows that needed more than one chunk.  One workgroup per (query head, row).
+template <int D>
+__global__ __launch_bounds__(256) void paged_decode_merge(DecodeArgs a)
+{
+    const int hq = blockIdx.x;
+    const int b = blockIdx.y;
+    const int L = row_tokens(a, b);
+    const int nch = (L + a.chunk - 1) / a.chunk;
+    if (nch <= 1) return;
+
+    const int64_t base = (static_cast<int64_t>(b) * a.num_heads + hq) * a.max_chunks;
+    float         M = kNegBig;
+    for (int c = 0; c < nch; ++c) M = fmaxf(M, a.ws_ml[2 * (base + c)]);
+    float lsum = 0.0f;
+    for (int c = 0; c < nch; ++c) lsum += a.ws_ml[2 * (base + c) + 1] * fast_exp2(a.ws_ml[2 * (base + c)] - M);
+    const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
+    for (int d = threadIdx.x; d < D; d += 256)
+    {
+        float o = 0.0f;
+        for (int c = 0; c < nch; ++c)
+            o += a.ws_acc[(base + c) * D + d] * fast_exp2(a.ws_ml[2 * (base + c)] - M);
+        store_act1(a.out, a.qo_dtype, (static_cast<size_t>(b) * a.num_heads + hq) * D + d, o * inv);
+    }
+}
+
+namespace
+{
+
+template <int CT, int D, int GP>
+hipError_t launch3(const DecodeArgs& a, hipStream_t stream)
+{
+    dim3 grid(static_cast<unsigned>(a.max_chunks), static_cast<unsigned>(a.num_kv_heads),
+              static_cast<unsigned>(a.batch));
+    hipLaunchKernelGGL((paged_decode_generic<CT, D, GP>), grid, dim3(256), 0, stream, a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || a.max_chunks <= 1) return e;
+    hipLaunchKernelGGL((paged_decode_merge<D>), dim3(static_cast<unsigned>(a.num_heads), static_cast<unsigned>(a.batch)),
+                       dim3(D < 256 ? D : 256), 0, stream, a);
+    return hipGetLastError();
+}
+
+template <int CT, int D>
+hipError_t launch2(const DecodeArgs& a, hipStream_t stream)
+{
+    if (a.group <= 1) return launch3<CT, D, 1>(a, stream);
+    if (a.group <= 2) return launch3<CT, D, 2>(a, stream);
+    if (a.group <= 4) return launch3<CT, D, 4>(a, stream);
+    if (a.group <= 8) return launch3<CT, D, 8>(a, stream);
+    return launch3<CT, D, 16>(a, stream);
+}
+
+template <int CT>
+hipError_t launch1(const DecodeArgs& a, hipStream_t stream)
+{
+    switch (a.head_dim)
+    {
+        case 64:
+            return launch2<CT, 64>(a, stream);
+        case 128:
+            return launch2<CT, 128>(a, stream);
+        default:
+            return launch2<CT, 256>(a, stream);
+    }
+}
+
+}  // namespace
+
+hipError_t launch_decode(const DecodeArgs& a, hipStream_t stream)
+{
+    switch (a.cache_dtype)
+    {
+        case F32:
+            return launch1<F32>(a, stream);
+        case F16:
+            return launch1<F16>(a, stream);
+        case BF16:
+            return launch1<BF16>(a, stream);
+        case I8:
+            return launch1<I8>(a, stream);
+        default:
+            return launch1<FP8>(a, stream);
+    }
+}
+
+}  // namespace ffkv

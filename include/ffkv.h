@@ -1,0 +1,115 @@
+/*
+ * ffkv.h - C ABI of the MI355X (gfx950) paged KV-cache path.
+ *
+ * This is the drop-in boundary for Firefly's paged KV-cache hot path: appending new K/V tokens into
+ * block-table-addressed pages (optionally quantizing to int8 or OCP fp8 e4m3) and PagedAttention decode
+ * (GQA, split-K, online softmax).  Plain pointers and sizes only; no C++ or HIP types appear here, so
+ * ctypes / cgo / JNI / N-API callers can bind it directly.  `stream` is a hipStream_t passed as void*
+ * (NULL = the legacy default stream).
+ *
+ * Layout contract (identical to the reference):
+ *   K/V pages       [num_blocks, block_size=16, num_kv_heads, head_dim], element (p, o, h, d) at
+ *                   ((p*16 + o)*num_kv_heads + h)*head_dim + d        (src/model/qwen_model.cu:41-42,
+ *                                                                       src/kernels/attention.cu:347-348)
+ *   block_table     int32 [batch, max_blocks], row stride max_blocks  (src/kernels/attention.cu:334)
+ *   context_lens    int32 [batch], tokens already cached BEFORE this step's append
+ *                   (src/model/qwen_model.cu:32-33, src/kernels/attention.cu:320)
+ *   append source   [batch, seq_len, num_kv_heads, head_dim]          (src/model/qwen_model.cu:39)
+ *   q               [batch, 1, num_heads, head_dim]; out [batch, 1, num_heads*head_dim]
+ *   GQA head map    kv_head = q_head / (num_heads / num_kv_heads)     (src/kernels/attention.cu:304)
+ *
+ * Quantized caches (no counterpart in the reference, which is fp16-only):
+ *   FFKV_DTYPE_I8       symmetric int8, scale per (page, slot, kv_head): fp32 [num_blocks, 16, num_kv_heads],
+ *                       scale = absmax/127 (IEEE fp32 divide), q = clamp(rint_half_even(x/scale), -127, 127),
+ *                       absmax == 0 gives scale 0 and q 0.  Scales are WRITTEN by ffkv_append.
+ *   FFKV_DTYPE_FP8_E4M3 OCP e4m3 (bias 7, max 448, NaN = S.1111.111), scale per kv_head: fp32 [num_kv_heads],
+ *                       q = e4m3_round_half_even_satfinite(x/scale).  Scales are READ by ffkv_append.
+ *
+ * Invalid addressing is defined instead of undefined (the reference writes/reads block -1 for padded rows,
+ * src/engine.cc:298-300 with src/model/qwen_model.cu:37,41-45): a block-table entry < 0 or >= num_blocks,
+ * a logical block index >= max_blocks, or a negative position is skipped by append and masked out by decode;
+ * a decode row with no valid token produces zeros.
+ *
+ * All entry points are asynchronous on `stream`, never synchronize the host, and are safe to capture in a
+ * hipGraph as long as a workspace is passed to ffkv_paged_decode.  Return 0 on success or a negative
+ * FFKV_ERR_* code; ffkv_last_error() gives a message for the calling thread.
+ */
+#ifndef FFKV_H_
+#define FFKV_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FFKV_BLOCK_SIZE 16
+
+/* dtype codes: equal to the firefly::DType enumerators (include/firefly/types.h:16-26 in the reference,
+ * plus FP8_E4M3 which the reference lacks). */
+#define FFKV_DTYPE_F32 0
+#define FFKV_DTYPE_F16 1
+#define FFKV_DTYPE_BF16 2
+#define FFKV_DTYPE_I8 3
+#define FFKV_DTYPE_FP8_E4M3 7
+
+#define FFKV_OK 0
+#define FFKV_ERR_INVALID_ARGUMENT -1
+#define FFKV_ERR_UNSUPPORTED -2
+#define FFKV_ERR_WORKSPACE -3
+#define FFKV_ERR_HIP -4
+
+/*
+ * Scatter new K/V tokens into their pages.  Replaces the reference's unexported append kernel launch
+ * `append_kv_cache<<<(seq_len, Hkv, B), 128, 0, stream>>>(k, v, k_cache, v_cache, block_table, context_lens,
+ * max_blocks, Hkv, D)` (src/model/qwen_model.cu:21-47, launched at :138-143).
+ *
+ * Token t of row b goes to position pos = context_lens[b] + t (context_lens == NULL means 0), i.e. page
+ * block_table[b*max_blocks + pos/16], slot pos%16.  src_dtype is F32, F16 or BF16; cache_dtype is F32, F16,
+ * BF16 (copy, rounding to nearest even when narrowing), I8 or FP8_E4M3 (quantize, see above).
+ * k_scale / v_scale: I8 -> written, [num_blocks, 16, num_kv_heads]; FP8 -> read, [num_kv_heads]; else unused.
+ * head_dim must be 64, 128 or 256; block_size must be 16.  Source and cache pointers must be 16-byte aligned.
+ */
+int ffkv_append(const void* k_src, const void* v_src, int src_dtype, void* k_cache, void* v_cache, int cache_dtype,
+                float* k_scale, float* v_scale, const int32_t* block_table, const int32_t* context_lens, int batch,
+                int seq_len, int num_kv_heads, int head_dim, int block_size, int max_blocks, int num_blocks,
+                void* stream);
+
+/*
+ * Bytes of scratch ffkv_paged_decode needs for split-K partial results at these sizes.  max_context_len is
+ * an upper bound on context_lens[b] + 1 (<= 0 means max_blocks * 16).
+ */
+size_t ffkv_decode_workspace_bytes(int batch, int num_heads, int head_dim, int max_blocks, int max_context_len);
+
+/*
+ * PagedAttention decode: out[b, h, :] = softmax(scale * q[b,h] . K_j) V_j over the context_lens[b] + 1 cached
+ * tokens of row b (the +1 is the token appended this step).  Replaces `firefly::kernels::attention(q, k_cache,
+ * v_cache, out, block_table, kv_head_num, seq_len, max_context_blocks, context_lens)` on its decode branch
+ * (include/firefly/kernels.h:83-84, src/kernels/attention.cu:452-493 -> paged_attention_kernel :291-447).
+ *
+ * qo_dtype (q and out) is F32, F16 or BF16; cache_dtype as for ffkv_append.  scale <= 0 selects
+ * 1/sqrt(head_dim) (src/kernels/attention.cu:458).  num_heads must be a multiple of num_kv_heads with a group
+ * size of at most 16; head_dim 64, 128 or 256; q and cache pointers 16-byte aligned.  Long rows are split over
+ * the context and merged by a second pass; the partials live in `workspace` (ffkv_decode_workspace_bytes), or,
+ * when workspace is
+ * NULL, in stream-ordered memory the library allocates and frees on `stream`.  Rows whose context_lens[b] + 1
+ * exceeds max_context_len are truncated to it.
+ */
+int ffkv_paged_decode(const void* q, void* out, int qo_dtype, const void* k_cache, const void* v_cache,
+                      int cache_dtype, const float* k_scale, const float* v_scale, const int32_t* block_table,
+                      const int32_t* context_lens, int batch, int num_heads, int num_kv_heads, int head_dim,
+                      int block_size, int max_blocks, int num_blocks, int max_context_len, float scale,
+                      void* workspace, size_t workspace_bytes, void* stream);
+
+/* Message describing the last error returned on the calling thread ("" if none). */
+const char* ffkv_last_error(void);
+
+/* Library version string. */
+const char* ffkv_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FFKV_H_ */

@@ -1,0 +1,109 @@
+"""Parity of the HIP path against the CPU checker on identical seeded inputs.
+
+Bar: KV page bytes and int8/fp8 codes and scales bit-exact over the whole pool; decode outputs within max-abs
+2e-3 for 16-bit KV (bf16/fp16 in, fp32 accumulate), 2e-2 for quantized KV, 1e-4 for fp32 everything.  The
+GPU output (rounded to the activation dtype) is compared with the checker's fp32 value before rounding; the
+rounding to the output format itself (half a bf16/fp16 ulp at the value's magnitude, which exceeds 2e-2 once
+|O| >= 8 as with config 5's x8 outliers) is allowed on top of the tolerance.  fp32-output cases carry no
+rounding allowance.
+"""
+
+import math
+
+import numpy as np
+import pytest
+
+import cases
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+TOL = {("f32", "f32"): 1e-4, ("bf16", "bf16"): 2e-3, ("f16", "f16"): 2e-3, ("bf16", "i8"): 2e-2,
+       ("bf16", "fp8"): 2e-2, ("f16", "i8"): 2e-2, ("f16", "fp8"): 2e-2, ("f32", "i8"): 2e-2,
+       ("f32", "fp8"): 2e-2, ("bf16", "f32"): 2e-3, ("f32", "bf16"): 1e-4, ("f32", "f16"): 1e-4}
+
+
+def half_ulp(x: np.ndarray, act: int) -> np.ndarray:
+    """Half the spacing of the output format at |x| (0 for fp32)."""
+    if act == O.DTYPE_F32:
+        return np.zeros_like(x)
+    mant, emin = (7, -126) if act == O.DTYPE_BF16 else (10, -14)
+    e = np.floor(np.log2(np.maximum(np.abs(x), 2.0 ** emin)))
+    return 2.0 ** (e - mant - 1)
+
+
+def _check(ff, dev, c, tol, max_context_len=0, workspace=False):
+    import gpu_util as gu
+
+    print(f"case seed={c.seed} B={c.B} Hq={c.Hq} Hkv={c.Hkv} D={c.D} act={c.act} kv={c.kv} "
+          f"ctx_max={int(c.ctx.max())}", flush=True)
+    kp, vp, ks, vs, out, out32 = cases.oracle_step(c, max_context_len=max_context_len)
+    gk, gv, gks, gvs, gout = gu.run_step(ff, c, dev, max_context_len=max_context_len, workspace=workspace)
+    assert np.array_equal(gk.view(np.uint8), kp.view(np.uint8)), "K pages differ"
+    assert np.array_equal(gv.view(np.uint8), vp.view(np.uint8)), "V pages differ"
+    if ks is not None and c.kv == O.DTYPE_I8:
+        assert np.array_equal(gks.view(np.uint32), ks.view(np.uint32)), "K scales differ"
+        assert np.array_equal(gvs.view(np.uint32), vs.view(np.uint32)), "V scales differ"
+    got = gu.out_to_f32(gout, c.act).reshape(out32.shape)
+    diff = np.abs(got.astype(np.float64) - out32)
+    err = float(diff.max())
+    excess = float((diff - half_ulp(np.maximum(np.abs(got), np.abs(out32)), c.act)).max())
+    print(f"  max-abs err {err:.3e}, beyond output rounding {excess:.3e} (tol {tol})", flush=True)
+    assert excess <= tol
+
+
+@pytest.mark.parametrize("act,kv", [("bf16", "bf16"), ("f16", "f16"), ("f32", "f32"), ("bf16", "i8"),
+                                    ("bf16", "fp8"), ("f32", "bf16"), ("f16", "i8"), ("f32", "fp8")])
+def test_config1(ff, gpu, act, kv):
+    _check(ff, gpu, cases.config1(act=act, kv=kv), TOL[(act, kv)])
+
+
+@pytest.mark.parametrize("D", [64, 256])
+@pytest.mark.parametrize("G", [1, 2, 7, 16])
+def test_head_shapes(ff, gpu, D, G):
+    Hkv = 2
+    rng = np.random.default_rng(D * 100 + G)
+    ctx = rng.integers(0, 700, size=5)
+    c = cases.make_case(11 + G, 5, Hkv * G, Hkv, D, ctx, act="bf16", input_scale=1 / math.sqrt(D))
+    _check(ff, gpu, c, 2e-3)
+
+
+def test_config2_full(ff, gpu):
+    """BASELINE config 2 at full size: Qwen3-8B layer, B=64, contexts U[512, 4096]."""
+    rng = np.random.default_rng(2)
+    ctx = rng.integers(512, 4097, size=64)
+    c = cases.make_case(2, 64, 32, 8, 128, ctx, act="bf16")
+    _check(ff, gpu, c, 2e-3, max_context_len=4097, workspace=True)
+
+
+def test_split_k_long_context(ff, gpu):
+    """Config-3 shape (Hq28/Hkv4, G = 7) with 8k contexts so that rows span many split-K chunks."""
+    c = cases.make_case(3, 4, 28, 4, 128, [8191, 8000, 4100, 300], act="bf16")
+    _check(ff, gpu, c, 2e-3)
+
+
+def test_quantized_outliers(ff, gpu):
+    """Config-5 style inputs: N(0,1) with 1% outliers at x8, int8 and fp8 caches."""
+    rng = np.random.default_rng(5)
+    ctx = rng.integers(1024, 2048, size=8)
+    for act in ("bf16", "f32"):
+        for kv in ("i8", "fp8"):
+            c = cases.make_case(5, 8, 32, 8, 128, ctx, act=act, kv=kv, outlier_frac=0.01)
+            _check(ff, gpu, c, 2e-2)
+
+
+def test_invalid_pages_and_empty_rows(ff, gpu):
+    """Negative / out-of-pool block ids are skipped by append and masked by decode; a row with no valid token
+    gives zeros (the reference reads and writes block -1 here)."""
+    c = cases.make_case(9, 6, 8, 4, 128, [40, 0, 100, 31, 15, 64], act="bf16")
+    c.block_table[0, 1] = -1                 # hole in the middle of row 0
+    c.block_table[2, :] = -1                 # row 2 fully padded
+    c.block_table[3, 0] = c.num_blocks + 3   # out of the pool
+    c.ctx[4] = -1                            # no tokens at all: appends at position -1 is skipped
+    _check(ff, gpu, c, 2e-3)
+
+
+def test_multi_token_append_chunk(ff, gpu):
+    """Chunked-prefill style append of S=64 tokens per row, then decode."""
+    c = cases.make_case(4, 3, 32, 8, 128, [0, 37, 200], act="bf16", S=64)
+    _check(ff, gpu, c, 2e-3)
