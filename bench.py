@@ -1,0 +1,247 @@
+"""Benchmark of the paged KV-cache hot path on one MI355X.
+
+Workload: Qwen3-8B layer shape, bf16 KV, 32 query heads, 8 KV heads (GQA 4),
+head_dim 128, block size 16, batch 64, pre-append context lengths uniform in [512, 4096], block tables a
+seeded permutation of a pool sized to total blocks + 10 %, Q/K/V ~ N(0,1).  One step = append one new K/V
+token per sequence (ffkv_append) and run decode attention over context_lens + 1 tokens (ffkv_paged_decode),
+on one layer's pool.  Steps rotate over `--layers` independent pools (as a model's layers do), so the
+working set (~2.7 GB at 4 layers) is far beyond the 256 MB Infinity Cache and every step streams its KV from
+HBM.
+
+Printed JSON line (rank 0, N = 1):
+  value          algorithmic HBM bytes of (append + decode) per step / wall time per step, in TB/s
+  roofline       the decode call (split-K pass + merge pass) timed with HIP events on the launch stream;
+                 achieved = algorithmic decode bytes / mean call duration, peak 8 TB/s
+  cpu_baseline   the C restatement under oracle/ (the checker) timed on the host cores on the same layer-0
+                 inputs, same algorithmic-bytes formula
+  parity         max-abs error of the layer-0 GPU output against that CPU result (fp32, before rounding)
+
+Algorithmic bytes per decode call (L'_b = context_lens[b] + 1):
+  sum_b L'_b*Hkv*D*2*2 (K and V) + B*Hq*D*2*2 (q in, out) + sum_b ceil(L'_b/16)*4 (block table) + 4*B
+Algorithmic bytes per append call: T*Hkv*D*2*2 (read k, v) + T*Hkv*D*2*2 (write pages) + 4*B (context_lens)
+  + 4*T (one block-table entry per token).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_TBS = 8.0
+B, HQ, HKV, D, BLOCK = 64, 32, 8, 128, 16
+CTX_LO, CTX_HI = 512, 4096
+SEED = 0
+
+
+def workload(seed: int = SEED):
+    """Context lengths and block tables of config 2 (numpy, seeded)."""
+    import numpy as np
+
+    rng = np.random.default_rng(seed)
+    ctx = rng.integers(CTX_LO, CTX_HI + 1, size=B).astype(np.int32)
+    need = [math.ceil((int(c) + 1) / BLOCK) for c in ctx]
+    total = sum(need)
+    N = math.ceil(total * 1.1)
+    perm = rng.permutation(N).astype(np.int32)
+    mb = max(need)
+    table = np.full((B, mb), -1, dtype=np.int32)
+    pos = 0
+    for b in range(B):
+        table[b, :need[b]] = perm[pos:pos + need[b]]
+        pos += need[b]
+    return ctx, table, N
+
+
+def decode_bytes(ctx) -> int:
+    Lp = [int(c) + 1 for c in ctx]
+    return (sum(Lp) * HKV * D * 2 * 2 + len(ctx) * HQ * D * 2 * 2 + sum(math.ceil(x / BLOCK) for x in Lp) * 4
+            + 4 * len(ctx))
+
+
+def append_bytes(T: int, batch: int) -> int:
+    return T * HKV * D * 2 * 2 * 2 + 4 * batch + 4 * T
+
+
+def cpu_baseline(ctx, table, N, k_pool, v_pool, q, gpu_out, seconds: float = 10.0):
+    """Time the CPU restatement (oracle/) of the decode call on the host cores, on the same inputs as layer 0,
+    and return (baseline dict, max-abs error of the GPU output against it)."""
+    import numpy as np
+    import torch
+
+    import oracle as O
+
+    threads = min(16, os.cpu_count() or 1)
+    kp = k_pool.view(torch.int16).cpu().numpy().view(np.uint16)
+    vp = v_pool.view(torch.int16).cpu().numpy().view(np.uint16)
+    qn = q.view(torch.int16).cpu().numpy().view(np.uint16)
+    runs, t0 = [], time.perf_counter()
+    out32 = None
+    while True:
+        s = time.perf_counter()
+        _, out32 = O.paged_decode(qn, O.DTYPE_BF16, kp, vp, O.DTYPE_BF16, table, ctx, threads=threads)
+        runs.append(time.perf_counter() - s)
+        if time.perf_counter() - t0 > seconds and len(runs) >= 3:
+            break
+    t = float(np.median(runs))
+    got = gpu_out.float().cpu().numpy().reshape(out32.shape)
+    err = float(np.abs(got - out32).max())
+    tbs = decode_bytes(ctx) / t / 1e12
+    return ({"value": tbs, "unit": "TB/s", "cores": threads, "kind": "port",
+             "tokens_per_s": len(ctx) / t, "ms_per_call": t * 1e3,
+             "sample": f"full layer-0 decode call of the workload (B={len(ctx)}, {int(sum(ctx)) + len(ctx)} "
+                       f"context tokens), median of {len(runs)} runs"}, err)
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--layers", type=int, default=4, help="independent KV pools rotated over the steps")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline time budget (0 = skip)")
+    ap.add_argument("--no-bulk", action="store_true", help="skip the bulk-append measurement")
+    args = ap.parse_args(argv)
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: the paged KV-cache path shards by sequence or KV head with no "
+              "exchange, and every box in this build has one GPU; run with --gpus 1", file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+
+    import firefly_amd as ff
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    stream = torch.cuda.current_stream()
+
+    ctx_np, table_np, N = workload()
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(SEED)
+    ctx = torch.from_numpy(ctx_np).to(dev)
+    table = torch.from_numpy(table_np).to(dev)
+    shape = (N, BLOCK, HKV, D)
+    pools = [(torch.randn(shape, generator=gen, device=dev, dtype=torch.bfloat16),
+              torch.randn(shape, generator=gen, device=dev, dtype=torch.bfloat16)) for _ in range(args.layers)]
+    q = torch.randn((B, 1, HQ, D), generator=gen, device=dev, dtype=torch.bfloat16)
+    k_new = torch.randn((B, 1, HKV, D), generator=gen, device=dev, dtype=torch.bfloat16)
+    v_new = torch.randn((B, 1, HKV, D), generator=gen, device=dev, dtype=torch.bfloat16)
+    out = torch.empty((B, 1, HQ * D), device=dev, dtype=torch.bfloat16)
+    max_ctx = int(ctx_np.max()) + 1
+    ws_bytes = ff.decode_workspace_bytes(B, HQ, D, table_np.shape[1], max_ctx)
+    ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=dev)
+
+    def step(i):
+        kp, vp = pools[i % args.layers]
+        ff.append_kv_cache(k_new, v_new, kp, vp, table, ctx, stream=stream)
+        ff.paged_attention(q, kp, vp, table, ctx, out=out, max_context_len=max_ctx, workspace=ws, stream=stream)
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+
+    # Timed region: K steps, wall clock, synchronized on both sides.
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(i)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_per_step = wall / args.steps * 1e3
+
+    # Per-call durations with HIP events on the launch stream (same loop, events around each call).
+    n_ev = args.steps
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(n_ev)]
+    for i in range(n_ev):
+        kp, vp = pools[i % args.layers]
+        ev[i][0].record(stream)
+        ff.append_kv_cache(k_new, v_new, kp, vp, table, ctx, stream=stream)
+        ev[i][1].record(stream)
+        ff.paged_attention(q, kp, vp, table, ctx, out=out, max_context_len=max_ctx, workspace=ws, stream=stream)
+        ev[i][2].record(stream)
+    torch.cuda.synchronize()
+    app_ms = float(np.mean([e[0].elapsed_time(e[1]) for e in ev]))
+    dec_ms = float(np.mean([e[1].elapsed_time(e[2]) for e in ev]))
+
+    dbytes = decode_bytes(ctx_np)
+    abytes = append_bytes(B, B)
+    achieved = dbytes / (dec_ms * 1e-3) / 1e12
+
+    # Bulk append: 64 sequences x 2048 new tokens into fresh pages (the KV-append GB/s figure).
+    bulk = None
+    if not args.no_bulk:
+        S = 2048
+        nb = S // BLOCK
+        rng = np.random.default_rng(SEED + 1)
+        bt = torch.from_numpy(rng.permutation(B * nb).astype(np.int32).reshape(B, nb)).to(dev)
+        ks = torch.randn((B, S, HKV, D), generator=gen, device=dev, dtype=torch.bfloat16)
+        vs = torch.randn((B, S, HKV, D), generator=gen, device=dev, dtype=torch.bfloat16)
+        kc = torch.empty((B * nb, BLOCK, HKV, D), device=dev, dtype=torch.bfloat16)
+        vc = torch.empty_like(kc)
+        zero = torch.zeros(B, dtype=torch.int32, device=dev)
+        for _ in range(3):
+            ff.append_kv_cache(ks, vs, kc, vc, bt, zero, stream=stream)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        reps = 20
+        e0.record(stream)
+        for _ in range(reps):
+            ff.append_kv_cache(ks, vs, kc, vc, bt, zero, stream=stream)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        bms = e0.elapsed_time(e1) / reps
+        bulk = {"tokens": B * S, "bytes": append_bytes(B * S, B), "ms": bms,
+                "GB_per_s": append_bytes(B * S, B) / (bms * 1e-3) / 1e9}
+        del ks, vs, kc, vc
+
+    # Layer-0 output for the parity figure and the CPU baseline on the same inputs.
+    kp0, vp0 = pools[0]
+    ff.paged_attention(q, kp0, vp0, table, ctx, out=out, max_context_len=max_ctx, workspace=ws, stream=stream)
+    torch.cuda.synchronize()
+    cpu = None
+    err = None
+    if args.cpu_seconds > 0:
+        cpu, err = cpu_baseline(ctx_np, table_np, N, kp0, vp0, q, out, args.cpu_seconds)
+
+    line = {
+        "metric": "paged decode-attn HBM TB/s (% of peak) + tokens/s; KV-append GB/s, 1 GPU",
+        "value": (dbytes + abytes) / (ms_per_step * 1e-3) / 1e12,
+        "unit": "TB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) K/V/Q, seeded block-table permutation)",
+        "config": {"workload": "C2 Qwen3-8B layer: Hq32/Hkv8/D128 bf16, B=64, ctx U[512,4096], block 16, "
+                               "append 1 token + decode per step",
+                   "batch": B, "context_tokens": int(ctx_np.sum()) + B, "pool_blocks": N, "layers": args.layers},
+        "pct_of_peak": (dbytes + abytes) / (ms_per_step * 1e-3) / 1e12 / HBM_PEAK_TBS * 100,
+        "decode_tokens_per_s": B / (ms_per_step * 1e-3),
+        "decode_tokens_per_s_qwen3_8b_36_layers": B / (ms_per_step * 1e-3 * 36),
+        "decode_call_ms": dec_ms,
+        "append_call_us": app_ms * 1e3,
+        "append_bulk": bulk,
+        "roofline": {"kernel": "ffkv_paged_decode (paged_decode_generic + paged_decode_merge)", "bound": "hbm",
+                     "achieved": achieved * 1e3, "peak": HBM_PEAK_TBS * 1e3, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_TBS, "traffic": None, "algorithmic_bytes": dbytes},
+        "cpu_baseline": cpu,
+        "parity_max_abs_err_vs_cpu": err,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

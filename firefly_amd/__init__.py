@@ -40,7 +40,7 @@ class FFKVError(RuntimeError):
 
 def _load() -> ctypes.CDLL:
     if not LIB_PATH.exists():
-        raise ImportError(f"{LIB_PATH} is not built; run `python -m firefly_amd.build` (no CPU fallback exists)")
+        raise ImportError(f"{LIB_PATH} is not built; run `python firefly_amd/build.py` (no CPU fallback exists)")
     # torch wheels bundle their own HIP runtime under the same soname (libamdhip64.so.7).  Loading torch first
     # makes libffkv.so bind to that already-loaded runtime, so there is one runtime per process and torch's
     # device pointers and streams are valid here; loading ours first would put two runtimes in the process.

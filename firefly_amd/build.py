@@ -4,7 +4,8 @@ Every HIP and C++ source under ``firefly_amd/csrc`` is compiled with hipcc for g
 shared library whose exported C ABI is declared in ``include/ffkv.h``.  Objects go to ``firefly_amd/_build``;
 the library is written in-tree so it travels with the repository snapshot.
 
-Usage: ``python -m firefly_amd.build [--jobs N] [--no-oracle]``.
+Usage: ``python firefly_amd/build.py [--jobs N] [--no-oracle]`` (run as a script: importing the package needs
+the library this builds).
 """
 
 from __future__ import annotations
@@ -72,7 +73,7 @@ def build_oracle() -> None:
     """Build the CPU checker (and, where the reference sources exist, the compiled reference host code)."""
     make = shutil.which("make") or "make"
     subprocess.run([make, "-C", str(ROOT / "oracle"), "-j4"], check=True, capture_output=True, text=True)
-    if Path("/root/reference/src/scheduler.cc").exists():
+    if Path("/root/reference/src/scheduler.cc").exists() and (ROOT / "oracle" / "ref_sched_shim.cpp").exists():
         subprocess.run([make, "-C", str(ROOT / "oracle"), "ref"], check=True, capture_output=True, text=True)
 
 

@@ -1,0 +1,101 @@
+"""The C ABI without a GPU: the library loads, exports every function include/ffkv.h declares, and rejects
+invalid arguments with the documented status codes before it touches a device."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parent.parent
+
+
+def declared_functions() -> list[str]:
+    names = []
+    for h in sorted((ROOT / "include").glob("*.h")):
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        names += re.findall(r"\b(ffkv_[a-z0-9_]+)\s*\(", text)
+    return sorted(set(names))
+
+
+def test_exports_every_declared_symbol(ff):
+    names = declared_functions()
+    assert "ffkv_append" in names and "ffkv_paged_decode" in names
+    for n in names:
+        assert hasattr(ff.lib, n), f"{n} is declared in include/ but not exported by {ff.LIB_PATH}"
+
+
+def test_version(ff):
+    assert "gfx950" in ff.version()
+
+
+def _append(ff, **kw):
+    a = dict(k_src=16, v_src=16, src_dtype=ff.DTYPE_BF16, k_cache=16, v_cache=16, cache_dtype=ff.DTYPE_BF16,
+             k_scale=None, v_scale=None, block_table=16, context_lens=None, batch=1, seq_len=1, num_kv_heads=8,
+             head_dim=128, block_size=16, max_blocks=4, num_blocks=4, stream=None)
+    a.update(kw)
+    return ff.lib.ffkv_append(*a.values())
+
+
+def _decode(ff, **kw):
+    a = dict(q=16, out=16, qo_dtype=ff.DTYPE_BF16, k_cache=16, v_cache=16, cache_dtype=ff.DTYPE_BF16,
+             k_scale=None, v_scale=None, block_table=16, context_lens=16, batch=1, num_heads=32, num_kv_heads=8,
+             head_dim=128, block_size=16, max_blocks=4, num_blocks=4, max_context_len=0, scale=0.0,
+             workspace=None, workspace_bytes=0, stream=None)
+    a.update(kw)
+    return ff.lib.ffkv_paged_decode(*a.values())
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(block_size=32), -2),
+    (dict(head_dim=96), -2),
+    (dict(src_dtype=3), -2),          # int8 is not an activation dtype
+    (dict(cache_dtype=5), -2),
+    (dict(batch=-1), -1),
+    (dict(num_kv_heads=0), -1),
+    (dict(k_cache=None), -1),
+    (dict(block_table=None), -1),
+    (dict(cache_dtype=3), -1),        # int8 cache without scales
+    (dict(cache_dtype=7), -1),        # fp8 cache without scales
+    (dict(k_src=18), -1),             # misaligned
+])
+def test_append_rejects(ff, kw, code):
+    assert _append(ff, **kw) == code
+    assert ff.lib.ffkv_last_error().decode() != ""
+
+
+def test_append_empty_is_ok(ff):
+    assert _append(ff, batch=0, k_src=None, v_src=None) == 0
+    assert _append(ff, seq_len=0) == 0
+    assert ff.lib.ffkv_last_error().decode() == ""
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(block_size=8), -2),
+    (dict(head_dim=80), -2),
+    (dict(qo_dtype=3), -2),
+    (dict(num_heads=30), -1),         # not a multiple of num_kv_heads
+    (dict(num_heads=8 * 17), -2),     # GQA group above 16
+    (dict(context_lens=None), -1),
+    (dict(q=None), -1),
+    (dict(cache_dtype=3), -1),
+    (dict(q=20), -1),
+    (dict(batch=70000), -2),
+])
+def test_decode_rejects(ff, kw, code):
+    assert _decode(ff, **kw) == code
+    assert ff.lib.ffkv_last_error().decode() != ""
+
+
+def test_decode_workspace_too_small(ff):
+    need = ff.decode_workspace_bytes(4, 32, 128, 600, 0)
+    assert need > 0
+    assert _decode(ff, batch=4, max_blocks=600, workspace=256, workspace_bytes=need - 1) == ff.ERR_WORKSPACE
+
+
+def test_workspace_bytes_monotone(ff):
+    a = ff.decode_workspace_bytes(8, 28, 128, 2049, 0)
+    b = ff.decode_workspace_bytes(8, 28, 128, 2049, 8192)
+    assert a >= b > 0
+    assert ff.decode_workspace_bytes(8, 28, 128, 16, 0) == 0   # one chunk: no partials
+    assert ff.decode_workspace_bytes(0, 28, 128, 2049, 0) == 0
