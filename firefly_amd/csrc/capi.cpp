@@ -9,7 +9,11 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
+#include <cstring>
+#include <map>
+#include <mutex>
 #include <string>
+#include <utility>
 
 #include "ffkv.h"
 #include "ffkv_internal.h"
@@ -59,10 +63,63 @@ int env_chunk()
     return v;
 }
 
+// FFKV_DECODE_KERNEL=generic forces the generic decode kernel (for comparisons); anything else is automatic.
+bool env_force_generic()
+{
+    static const bool v = []
+    {
+        const char* s = std::getenv("FFKV_DECODE_KERNEL");
+        return s && std::strcmp(s, "generic") == 0;
+    }();
+    return v;
+}
+
+int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
+
 }  // namespace
 
 namespace ffkv
 {
+
+bool decode_use_mfma(int cache_dtype, int group)
+{
+    return !env_force_generic() && cache_dtype != FFKV_DTYPE_F32 && group <= 16;
+}
+
+size_t decode_mfma_workspace_bytes(int batch, int num_heads, int head_dim)
+{
+    const int64_t slots = static_cast<int64_t>(kMfmaMaxItems) + batch;
+    return static_cast<size_t>(align256(static_cast<int64_t>(batch) * 2 * 4) + align256(slots * num_heads * 2 * 4) +
+                               slots * num_heads * head_dim * 4);
+}
+
+int decode_mfma_items(const void* kernel, int threads, int grid_y)
+{
+    static std::mutex                               mu;
+    static std::map<std::pair<const void*, int>, int> cache;
+    int                                             dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+    std::lock_guard<std::mutex> lock(mu);
+    auto                        key = std::make_pair(kernel, dev * 4096 + threads);
+    auto                        it = cache.find(key);
+    int                         resident;
+    if (it != cache.end())
+    {
+        resident = it->second;
+    }
+    else
+    {
+        int cus = 0, per_cu = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0) != hipSuccess || per_cu <= 0)
+            per_cu = 1;
+        resident = cus * per_cu;
+        cache.emplace(key, resident);
+    }
+    int items = resident / (grid_y > 0 ? grid_y : 1);
+    if (items < 1) items = 1;
+    return items > kMfmaMaxItems ? kMfmaMaxItems : items;
+}
 
 int decode_cap_tokens(int max_blocks, int max_context_len)
 {
@@ -143,8 +200,10 @@ int ffkv_append(const void* k_src, const void* v_src, int src_dtype, void* k_cac
 size_t ffkv_decode_workspace_bytes(int batch, int num_heads, int head_dim, int max_blocks, int max_context_len)
 {
     if (batch <= 0 || num_heads <= 0 || head_dim <= 0) return 0;
-    return ffkv::decode_workspace_bytes(batch, num_heads, head_dim,
-                                        ffkv::decode_cap_tokens(max_blocks, max_context_len));
+    const size_t generic = ffkv::decode_workspace_bytes(batch, num_heads, head_dim,
+                                                        ffkv::decode_cap_tokens(max_blocks, max_context_len));
+    const size_t mfma = ffkv::decode_mfma_workspace_bytes(batch, num_heads, head_dim);
+    return generic > mfma ? generic : mfma;
 }
 
 int ffkv_paged_decode(const void* q, void* out, int qo_dtype, const void* k_cache, const void* v_cache,
@@ -172,64 +231,80 @@ int ffkv_paged_decode(const void* q, void* out, int qo_dtype, const void* k_cach
         return fail(FFKV_ERR_INVALID_ARGUMENT, "null q, out, cache, block_table or context_lens pointer");
     if (quantized(cache_dtype) && (!k_scale || !v_scale))
         return fail(FFKV_ERR_INVALID_ARGUMENT, "quantized cache needs k_scale and v_scale");
-    if (!aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache))
-        return fail(FFKV_ERR_INVALID_ARGUMENT, "q and cache pointers must be 16-byte aligned");
+    if (!aligned16(q) || !aligned16(out) || !aligned16(k_cache) || !aligned16(v_cache))
+        return fail(FFKV_ERR_INVALID_ARGUMENT, "q, out and cache pointers must be 16-byte aligned");
 
-    const int cap = ffkv::decode_cap_tokens(max_blocks, max_context_len);
-    const int chunk = ffkv::decode_chunk(batch, num_kv_heads, cap);
-    const int max_chunks = static_cast<int>(ceil_div(cap > 0 ? cap : 1, chunk));
+    const int  cap = ffkv::decode_cap_tokens(max_blocks, max_context_len);
+    const bool mfma = ffkv::decode_use_mfma(cache_dtype, group);
+    const int  chunk = ffkv::decode_chunk(batch, num_kv_heads, cap);
+    const int  max_chunks = static_cast<int>(ceil_div(cap > 0 ? cap : 1, chunk));
+
+    // workspace layout: MFMA kernel [meta | ml | acc], generic kernel [ml | acc] (none for single-chunk rows)
+    int64_t meta_bytes = 0, ml_bytes = 0, need = 0;
+    if (mfma)
+    {
+        const int64_t slots = static_cast<int64_t>(ffkv::kMfmaMaxItems) + batch;
+        meta_bytes = align256(static_cast<int64_t>(batch) * 2 * 4);
+        ml_bytes = align256(slots * num_heads * 2 * 4);
+        need = meta_bytes + ml_bytes + slots * num_heads * head_dim * 4;
+    }
+    else if (max_chunks > 1)
+    {
+        const int64_t parts = static_cast<int64_t>(batch) * num_heads * max_chunks;
+        ml_bytes = align256(parts * 2 * 4);
+        need = ml_bytes + parts * head_dim * 4;
+    }
 
     hipStream_t s = static_cast<hipStream_t>(stream);
     void*       ws = workspace;
     bool        owned = false;
-    size_t      need = 0;
-    float*      ws_ml = nullptr;
-    float*      ws_acc = nullptr;
-    if (max_chunks > 1)
+    if (need > 0)
     {
-        const int64_t parts = static_cast<int64_t>(batch) * num_heads * max_chunks;
-        const int64_t ml = ceil_div(parts * 2 * 4, 256) * 256;
-        need = static_cast<size_t>(ml + parts * head_dim * 4);
         if (ws == nullptr)
         {
-            hipError_t e = hipMallocAsync(&ws, need, s);
+            hipError_t e = hipMallocAsync(&ws, static_cast<size_t>(need), s);
             if (e != hipSuccess) return hip_fail(e, "decode workspace hipMallocAsync");
             owned = true;
         }
-        else if (workspace_bytes < need)
+        else if (workspace_bytes < static_cast<size_t>(need))
         {
-            return fail(FFKV_ERR_WORKSPACE, "workspace of %zu bytes is smaller than the %zu bytes needed", workspace_bytes,
-                        need);
+            return fail(FFKV_ERR_WORKSPACE, "workspace of %zu bytes is smaller than the %lld bytes needed",
+                        workspace_bytes, static_cast<long long>(need));
         }
-        ws_ml = static_cast<float*>(ws);
-        ws_acc = reinterpret_cast<float*>(static_cast<char*>(ws) + ml);
+        else if (!aligned16(ws))
+        {
+            return fail(FFKV_ERR_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
+        }
     }
+    char* wsb = static_cast<char*>(ws);
 
-    const float sm_scale = scale > 0.0f ? scale : 1.0f / sqrtf(static_cast<float>(head_dim));
-    ffkv::DecodeArgs a{q,
-                       out,
-                       k_cache,
-                       v_cache,
-                       k_scale,
-                       v_scale,
-                       block_table,
-                       context_lens,
-                       ws_ml,
-                       ws_acc,
-                       qo_dtype,
-                       cache_dtype,
-                       batch,
-                       num_heads,
-                       num_kv_heads,
-                       group,
-                       head_dim,
-                       max_blocks,
-                       num_blocks,
-                       cap,
-                       chunk,
-                       max_chunks,
-                       sm_scale * 1.4426950408889634f};
-    hipError_t e = ffkv::launch_decode(a, s);
+    const float      sm_scale = scale > 0.0f ? scale : 1.0f / sqrtf(static_cast<float>(head_dim));
+    ffkv::DecodeArgs a{};
+    a.q = q;
+    a.out = out;
+    a.k_cache = k_cache;
+    a.v_cache = v_cache;
+    a.k_scale = k_scale;
+    a.v_scale = v_scale;
+    a.block_table = block_table;
+    a.context_lens = context_lens;
+    a.ws_meta = need > 0 && mfma ? reinterpret_cast<int32_t*>(wsb) : nullptr;
+    a.ws_ml = need > 0 ? reinterpret_cast<float*>(wsb + meta_bytes) : nullptr;
+    a.ws_acc = need > 0 ? reinterpret_cast<float*>(wsb + meta_bytes + ml_bytes) : nullptr;
+    a.qo_dtype = qo_dtype;
+    a.cache_dtype = cache_dtype;
+    a.batch = batch;
+    a.num_heads = num_heads;
+    a.num_kv_heads = num_kv_heads;
+    a.group = group;
+    a.head_dim = head_dim;
+    a.max_blocks = max_blocks;
+    a.num_blocks = num_blocks;
+    a.cap_tokens = cap;
+    a.chunk = chunk;
+    a.max_chunks = max_chunks;
+    a.scale_log2 = sm_scale * 1.4426950408889634f;
+    hipError_t e = mfma ? ffkv::launch_decode_mfma(a, s) : ffkv::launch_decode(a, s);
     if (owned)
     {
         hipError_t fe = hipFreeAsync(ws, s);

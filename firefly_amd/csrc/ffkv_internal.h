@@ -40,8 +40,11 @@ struct DecodeArgs
     const float*   v_scale;
     const int32_t* block_table;
     const int32_t* context_lens;
-    float*         ws_ml;   // [batch, num_heads, max_chunks, 2]: running max (log2 domain) and denominator
-    float*         ws_acc;  // [batch, num_heads, max_chunks, head_dim]: unnormalised output of each chunk
+    // Partial results.  Generic kernel: [batch, num_heads, max_chunks] entries.  MFMA kernel: slot = work item +
+    // row, [kMfmaMaxItems + batch, num_heads] entries.
+    float*         ws_ml;   // [.., 2]: running max (log2 domain) and denominator
+    float*         ws_acc;  // [.., head_dim]: unnormalised output
+    int32_t*       ws_meta; // MFMA kernel: [batch, 2] first and last work item covering each row
     int            qo_dtype;
     int            cache_dtype;
     int            batch;
@@ -58,7 +61,16 @@ struct DecodeArgs
 };
 
 hipError_t launch_append(const AppendArgs& a, hipStream_t stream);
-hipError_t launch_decode(const DecodeArgs& a, hipStream_t stream);
+hipError_t launch_decode(const DecodeArgs& a, hipStream_t stream);       // generic kernel (any cache dtype)
+hipError_t launch_decode_mfma(const DecodeArgs& a, hipStream_t stream);  // matrix-core kernel (16-bit/8-bit caches)
+
+// Upper bound on the MFMA kernel's work items (sizes its partial-result slots).
+constexpr int kMfmaMaxItems = 2048;
+// Work items for one MFMA decode launch: as many workgroups as the device keeps resident at once (CUs times
+// occupancy of `kernel` at `threads` threads), divided over `grid_y` head groups, capped at kMfmaMaxItems.
+int decode_mfma_items(const void* kernel, int threads, int grid_y);
+bool decode_use_mfma(int cache_dtype, int group);
+size_t decode_mfma_workspace_bytes(int batch, int num_heads, int head_dim);
 
 // Split-K geometry shared by the workspace query and the launcher.
 int    decode_cap_tokens(int max_blocks, int max_context_len);

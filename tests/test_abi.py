@@ -97,5 +97,6 @@ def test_workspace_bytes_monotone(ff):
     a = ff.decode_workspace_bytes(8, 28, 128, 2049, 0)
     b = ff.decode_workspace_bytes(8, 28, 128, 2049, 8192)
     assert a >= b > 0
-    assert ff.decode_workspace_bytes(8, 28, 128, 16, 0) == 0   # one chunk: no partials
+    # the matrix-core kernel splits any row over work items, so even one-chunk rows need partial slots
+    assert ff.decode_workspace_bytes(8, 28, 128, 16, 0) > 0
     assert ff.decode_workspace_bytes(0, 28, 128, 2049, 0) == 0

@@ -107,3 +107,57 @@ def test_multi_token_append_chunk(ff, gpu):
     """Chunked-prefill style append of S=64 tokens per row, then decode."""
     c = cases.make_case(4, 3, 32, 8, 128, [0, 37, 200], act="bf16", S=64)
     _check(ff, gpu, c, 2e-3)
+
+
+def test_many_short_rows(ff, gpu):
+    """700 rows (more rows than scan threads per workgroup), contexts 0..40, some rows without tokens."""
+    rng = np.random.default_rng(21)
+    ctx = rng.integers(0, 41, size=700)
+    ctx[::97] = -1                           # rows with no token at all: zeros
+    c = cases.make_case(21, 700, 8, 2, 128, ctx, act="bf16", input_scale=1 / math.sqrt(128))
+    _check(ff, gpu, c, 2e-3)
+
+
+@pytest.mark.parametrize("Hq,Hkv", [(16, 1), (12, 6), (40, 5)])
+def test_kv_head_groupings(ff, gpu, Hq, Hkv):
+    """One KV head (64-thread workgroups), and KV-head counts that leave idle waves in the last group."""
+    rng = np.random.default_rng(Hq * 10 + Hkv)
+    ctx = rng.integers(100, 1500, size=6)
+    c = cases.make_case(30 + Hkv, 6, Hq, Hkv, 128, ctx, act="bf16")
+    _check(ff, gpu, c, 2e-3)
+
+
+def test_truncated_context(ff, gpu):
+    """max_context_len below context_lens + 1 clamps the attended tokens on both sides."""
+    c = cases.make_case(22, 3, 32, 8, 128, [700, 100, 1000], act="bf16")
+    _check(ff, gpu, c, 2e-3, max_context_len=513)
+
+
+@pytest.mark.parametrize("act,kv", [("f16", "fp8"), ("bf16", "f16"), ("f16", "bf16")])
+def test_mixed_dtypes(ff, gpu, act, kv):
+    """q/out in another type than the cache (q is split into hi + lo MFMA parts)."""
+    rng = np.random.default_rng(23)
+    ctx = rng.integers(10, 900, size=5)
+    c = cases.make_case(23, 5, 16, 4, 128, ctx, act=act, kv=kv)
+    _check(ff, gpu, c, 2e-2 if kv in ("i8", "fp8") else 2e-3)
+
+
+def test_generic_and_mfma_kernels_agree(ff, gpu):
+    """The generic fp32-cache kernel and the matrix-core kernel on the same bf16 data (cache widened to fp32
+    for the generic one) agree within the bf16 tolerance."""
+    import torch
+
+    import gpu_util as gu
+
+    c = cases.make_case(24, 4, 32, 8, 128, [300, 1200, 47, 2050], act="f32", kv="bf16")
+    kp, vp, _, _, _, out32 = cases.oracle_step(c)
+    _, _, _, _, gout = gu.run_step(ff, c, gpu)
+    kf = torch.from_numpy(O.bf16_to_f32(kp)).to(gpu)
+    vf = torch.from_numpy(O.bf16_to_f32(vp)).to(gpu)
+    q = torch.from_numpy(c.q).to(gpu)
+    bt = torch.from_numpy(c.block_table).to(gpu)
+    ctx = torch.from_numpy(c.ctx).to(gpu)
+    gen = ff.paged_attention(q, kf, vf, bt, ctx).cpu().numpy().reshape(out32.shape)
+    mf = gout.reshape(out32.shape)
+    assert np.abs(gen - out32).max() <= 1e-4
+    assert np.abs(mf - out32).max() <= 2e-3
