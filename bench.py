@@ -70,6 +70,17 @@ def append_bytes(T: int, batch: int) -> int:
     return T * HKV * D * 2 * 2 * 2 + 4 * batch + 4 * T
 
 
+def measured_traffic():
+    """HBM bytes per decode call from the rocprofv3 counter passes recorded in profiles/ (FETCH_SIZE and
+    WRITE_SIZE of the decode and merge kernels, scaled by the same counters' reading for a copy of known size);
+    None when that record is absent."""
+    path = ROOT / "profiles" / "decode_c2_traffic.json"
+    if not path.exists():
+        return None
+    rec = json.loads(path.read_text())
+    return rec.get("bytes_per_call")
+
+
 def cpu_baseline(ctx, table, N, k_pool, v_pool, q, gpu_out, seconds: float = 10.0):
     """Time the CPU restatement (oracle/) of the decode call on the host cores, on the same inputs as layer 0,
     and return (baseline dict, max-abs error of the GPU output against it)."""
@@ -108,6 +119,9 @@ def main(argv=None) -> int:
     ap.add_argument("--layers", type=int, default=4, help="independent KV pools rotated over the steps")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline time budget (0 = skip)")
     ap.add_argument("--no-bulk", action="store_true", help="skip the bulk-append measurement")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="also run one 1 GiB device-to-device copy (a kernel of known read/write bytes, used to "
+                         "scale rocprofv3 FETCH_SIZE/WRITE_SIZE counters)")
     args = ap.parse_args(argv)
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -138,13 +152,19 @@ def main(argv=None) -> int:
     v_new = torch.randn((B, 1, HKV, D), generator=gen, device=dev, dtype=torch.bfloat16)
     out = torch.empty((B, 1, HQ * D), device=dev, dtype=torch.bfloat16)
     max_ctx = int(ctx_np.max()) + 1
-    ws_bytes = ff.decode_workspace_bytes(B, HQ, D, table_np.shape[1], max_ctx)
-    ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=dev)
+    ws = ff.decode_workspace(B, HQ, D, table_np.shape[1], max_ctx, device=dev)
 
     def step(i):
         kp, vp = pools[i % args.layers]
         ff.append_kv_cache(k_new, v_new, kp, vp, table, ctx, stream=stream)
         ff.paged_attention(q, kp, vp, table, ctx, out=out, max_context_len=max_ctx, workspace=ws, stream=stream)
+
+    if args.calibrate_copy:
+        src = torch.ones(1 << 30, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     for i in range(args.warmup):
         step(i)
@@ -233,9 +253,10 @@ def main(argv=None) -> int:
         "decode_call_ms": dec_ms,
         "append_call_us": app_ms * 1e3,
         "append_bulk": bulk,
-        "roofline": {"kernel": "ffkv_paged_decode (paged_decode_generic + paged_decode_merge)", "bound": "hbm",
+        "roofline": {"kernel": "ffkv_paged_decode (paged_decode_mfma + paged_decode_mfma_merge)", "bound": "hbm",
                      "achieved": achieved * 1e3, "peak": HBM_PEAK_TBS * 1e3, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_TBS, "traffic": None, "algorithmic_bytes": dbytes},
+                     "frac": achieved / HBM_PEAK_TBS, "traffic": measured_traffic(),
+                     "algorithmic_bytes": dbytes},
         "cpu_baseline": cpu,
         "parity_max_abs_err_vs_cpu": err,
     }

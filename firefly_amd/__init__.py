@@ -124,6 +124,15 @@ def decode_workspace_bytes(batch: int, num_heads: int, head_dim: int, max_blocks
     return int(lib.ffkv_decode_workspace_bytes(batch, num_heads, head_dim, max_blocks, max_context_len))
 
 
+def decode_workspace(batch: int, num_heads: int, head_dim: int, max_blocks: int, max_context_len: int = 0,
+                     device=None, stream=None):
+    """A decode workspace (uint8 tensor, contents irrelevant) sized by ``ffkv_decode_workspace_bytes``."""
+    import torch
+
+    n = max(decode_workspace_bytes(batch, num_heads, head_dim, max_blocks, max_context_len), 256)
+    return torch.empty(n, dtype=torch.uint8, device=device if device is not None else "cuda")
+
+
 def paged_attention(q, k_cache, v_cache, block_table, context_lens, out=None, k_scale=None, v_scale=None,
                     max_context_len: int = 0, scale: float = 0.0, workspace=None, num_blocks: int | None = None,
                     stream=None):

@@ -86,11 +86,27 @@ bool decode_use_mfma(int cache_dtype, int group)
     return !env_force_generic() && cache_dtype != FFKV_DTYPE_F32 && group <= 16;
 }
 
-size_t decode_mfma_workspace_bytes(int batch, int num_heads, int head_dim)
+// MFMA workspace layout: [row meta: batch x 2 int32 | (m, l): slots x num_heads x 2 fp32 | acc: slots x num_heads
+// x head_dim fp32], each region 256-byte aligned, slots = kMfmaMaxItems + batch.
+struct MfmaLayout
+{
+    int64_t meta, ml, acc, total;
+};
+
+MfmaLayout mfma_layout(int batch, int num_heads, int head_dim)
 {
     const int64_t slots = static_cast<int64_t>(kMfmaMaxItems) + batch;
-    return static_cast<size_t>(align256(static_cast<int64_t>(batch) * 2 * 4) + align256(slots * num_heads * 2 * 4) +
-                               slots * num_heads * head_dim * 4);
+    MfmaLayout    l{};
+    l.meta = 0;
+    l.ml = align256(static_cast<int64_t>(batch) * 2 * 4);
+    l.acc = l.ml + align256(slots * num_heads * 2 * 4);
+    l.total = l.acc + slots * num_heads * head_dim * 4;
+    return l;
+}
+
+size_t decode_mfma_workspace_bytes(int batch, int num_heads, int head_dim)
+{
+    return static_cast<size_t>(mfma_layout(batch, num_heads, head_dim).total);
 }
 
 int decode_mfma_items(const void* kernel, int threads, int grid_y)
@@ -239,20 +255,20 @@ int ffkv_paged_decode(const void* q, void* out, int qo_dtype, const void* k_cach
     const int  chunk = ffkv::decode_chunk(batch, num_kv_heads, cap);
     const int  max_chunks = static_cast<int>(ceil_div(cap > 0 ? cap : 1, chunk));
 
-    // workspace layout: MFMA kernel [meta | ml | acc], generic kernel [ml | acc] (none for single-chunk rows)
-    int64_t meta_bytes = 0, ml_bytes = 0, need = 0;
+    // workspace layout: MFMA kernel see mfma_layout, generic kernel [ml | acc] (none for single-chunk rows)
+    ffkv::MfmaLayout lay{};
+    int64_t          need = 0;
     if (mfma)
     {
-        const int64_t slots = static_cast<int64_t>(ffkv::kMfmaMaxItems) + batch;
-        meta_bytes = align256(static_cast<int64_t>(batch) * 2 * 4);
-        ml_bytes = align256(slots * num_heads * 2 * 4);
-        need = meta_bytes + ml_bytes + slots * num_heads * head_dim * 4;
+        lay = ffkv::mfma_layout(batch, num_heads, head_dim);
+        need = lay.total;
     }
     else if (max_chunks > 1)
     {
         const int64_t parts = static_cast<int64_t>(batch) * num_heads * max_chunks;
-        ml_bytes = align256(parts * 2 * 4);
-        need = ml_bytes + parts * head_dim * 4;
+        lay.ml = 0;
+        lay.acc = align256(parts * 2 * 4);
+        need = lay.acc + parts * head_dim * 4;
     }
 
     hipStream_t s = static_cast<hipStream_t>(stream);
@@ -288,9 +304,9 @@ int ffkv_paged_decode(const void* q, void* out, int qo_dtype, const void* k_cach
     a.v_scale = v_scale;
     a.block_table = block_table;
     a.context_lens = context_lens;
-    a.ws_meta = need > 0 && mfma ? reinterpret_cast<int32_t*>(wsb) : nullptr;
-    a.ws_ml = need > 0 ? reinterpret_cast<float*>(wsb + meta_bytes) : nullptr;
-    a.ws_acc = need > 0 ? reinterpret_cast<float*>(wsb + meta_bytes + ml_bytes) : nullptr;
+    a.ws_meta = need > 0 && mfma ? reinterpret_cast<int32_t*>(wsb + lay.meta) : nullptr;
+    a.ws_ml = need > 0 ? reinterpret_cast<float*>(wsb + lay.ml) : nullptr;
+    a.ws_acc = need > 0 ? reinterpret_cast<float*>(wsb + lay.acc) : nullptr;
     a.qo_dtype = qo_dtype;
     a.cache_dtype = cache_dtype;
     a.batch = batch;

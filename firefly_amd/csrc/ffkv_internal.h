@@ -44,7 +44,7 @@ struct DecodeArgs
     // row, [kMfmaMaxItems + batch, num_heads] entries.
     float*         ws_ml;   // [.., 2]: running max (log2 domain) and denominator
     float*         ws_acc;  // [.., head_dim]: unnormalised output
-    int32_t*       ws_meta; // MFMA kernel: [batch, 2] first and last work item covering each row
+    int32_t*       ws_meta;  // MFMA kernel: [batch, 2] first and last work item covering each row
     int            qo_dtype;
     int            cache_dtype;
     int            batch;

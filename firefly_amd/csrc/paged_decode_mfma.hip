@@ -13,18 +13,25 @@
 //     tokens 4g..4g+3, so the per-page max is 3 in-lane maxes and two cross-lane steps; the denominator stays a
 //     per-lane partial sum until the end.
 //   * PV on MFMA: O^T[d, h] += V^T[d, t] P^T[t, h] with v_mfma_f32_16x16x16; P^T is exactly the QK output
-//     layout (k = token = 4g + i), V^T comes from an LDS copy of the page's V rows whose 32-byte chunks are
-//     XOR-swizzled by token / 4, so the four token rows a read instruction touches fall in distinct bank
-//     groups while every row stays 16-byte aligned for the vector writes.
+//     layout (k = token = 4g + i), V^T comes from an LDS copy of the page's V rows whose 16-byte chunks are
+//     XOR-swizzled per token, so both the 16-byte row writes and the transposing column reads are free of bank
+//     conflicts while every row stays 16-byte aligned.
 //     P is split into hi + lo parts of the MFMA input type, so the products carry ~16 significant bits.
 //   * quantized caches: int8 and fp8 e4m3 codes convert exactly to f16 for the MFMA; int8 per-token K scales
 //     multiply the scores and V scales multiply P, fp8 per-head scales fold into the score scale and the output.
 //   * work split: the pages of all rows form one sequence; work item i of W takes pages
 //     [i*P/W, (i+1)*P/W), so every wave gets the same number of pages whatever the row lengths (no tail of
 //     long rows).  A row covered by one item writes its output directly; otherwise each piece writes an
-//     unnormalised partial (m, l, acc) to slot item + row and paged_decode_merge combines them.
+//     unnormalised partial (m, l, acc) to slot item + row and paged_decode_mfma_merge combines them.
 #include "ffkv_device.h"
 #include "ffkv_internal.h"
+
+#ifndef FFKV_MFMA_ROLLING
+#define FFKV_MFMA_ROLLING 1  // 1: load page pg + 1 while page pg finishes (two pages of K/V live in registers)
+#endif
+#ifndef FFKV_MFMA_MAX_WAVES
+#define FFKV_MFMA_MAX_WAVES 4  // waves (= KV heads) per workgroup
+#endif
 
 namespace ffkv
 {
@@ -51,7 +58,8 @@ struct MType<true>
 {
     using x8 = bf16x8;
     using x4 = bf16x4;
-    static __device__ __forceinline__ uint32_t bits(float x) { return f32_to_bf16(x); }
+    // v_cvt_pk_bf16_f32: round to nearest even (the operands here are finite)
+    static __device__ __forceinline__ uint32_t bits(float x) { return __builtin_bit_cast(uint16_t, static_cast<__bf16>(x)); }
     static __device__ __forceinline__ float value(uint32_t h) { return bf16_to_f32(h); }
     static __device__ __forceinline__ f32x4 mma32(x8 a, x8 b, f32x4 c)
     {
@@ -99,23 +107,59 @@ __device__ __forceinline__ int dim_of(int j, int g)
         return 64 * (j >> 1) + 16 * g + 8 * (j & 1);
 }
 
+using h2 = _Float16 __attribute__((ext_vector_type(2)));
+
+// 4 int8 codes -> 4 f16 values (two packed words), exact: the biased byte u = code + 128 is placed under the f16
+// exponent of 1024 (0x64uu = 1024 + u) and 1152 is subtracted with one packed f16 add per pair.
+__device__ __forceinline__ void i8x4_to_f16(uint32_t w, uint32_t& lo, uint32_t& hi)
+{
+    const uint32_t u = w ^ 0x80808080u;
+    const uint32_t a = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);  // [u0, 0x64, u1, 0x64]
+    const uint32_t b = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);  // [u2, 0x64, u3, 0x64]
+    const h2       bias = h2{static_cast<_Float16>(-1152.0f), static_cast<_Float16>(-1152.0f)};
+    lo = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, a) + bias);
+    hi = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, b) + bias);
+}
+
+// 4 OCP e4m3 codes -> 4 f16 values, exact: the code's magnitude bits shifted into the f16 exponent/mantissa
+// fields give 2^-8 times the value (normal and subnormal alike), fixed by one packed multiply by 256; the
+// NaN codes (S.1111.111) become f16 NaN.
+__device__ __forceinline__ void fp8x4_to_f16(uint32_t w, uint32_t& lo, uint32_t& hi)
+{
+    const uint32_t x0 = __builtin_amdgcn_perm(0u, w, 0x010c000cu);  // [0, b0, 0, b1]
+    const uint32_t x1 = __builtin_amdgcn_perm(0u, w, 0x030c020cu);  // [0, b2, 0, b3]
+    const uint32_t f0 = (x0 & 0x80008000u) | ((x0 >> 1) & 0x3f803f80u);
+    const uint32_t f1 = (x1 & 0x80008000u) | ((x1 >> 1) & 0x3f803f80u);
+    const h2       k256 = h2{static_cast<_Float16>(256.0f), static_cast<_Float16>(256.0f)};
+    lo = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, f0) * k256);
+    hi = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, f1) * k256);
+    // a byte whose low 7 bits are all ones is NaN; (b & 0x7f) + 1 carries into bit 7 only for those
+    const uint32_t nan = ((w & 0x7f7f7f7fu) + 0x01010101u) & 0x80808080u;
+    if (__builtin_expect(nan != 0u, 0))
+    {
+        const uint32_t n0 = __builtin_amdgcn_perm(0u, nan, 0x010c000cu);  // NaN flags at bit 15 of each half
+        const uint32_t n1 = __builtin_amdgcn_perm(0u, nan, 0x030c020cu);
+        lo = (lo & ~(((n0 >> 15) & 0x00010001u) * 0x7fffu)) | (((n0 >> 15) & 0x00010001u) * 0x7e00u);
+        hi = (hi & ~(((n1 >> 15) & 0x00010001u) * 0x7fffu)) | (((n1 >> 15) & 0x00010001u) * 0x7e00u);
+    }
+}
+
 // 8 cache codes (one k-step of one lane) as 4 packed 16-bit MFMA words.  Quantized codes convert exactly.
 template <int CT>
 __device__ __forceinline__ u32x4 codes_to_m(uint32_t lo, uint32_t hi)
 {
-    uint32_t w[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e)
+    uint32_t r0, r1, r2, r3;
+    if constexpr (CT == I8)
     {
-        const uint32_t byte = ((e < 4 ? lo : hi) >> (8 * (e & 3))) & 0xffu;
-        float          x;
-        if constexpr (CT == I8)
-            x = static_cast<float>(static_cast<int8_t>(byte));
-        else
-            x = e4m3_to_f32(byte);
-        w[e] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(x));
+        i8x4_to_f16(lo, r0, r1);
+        i8x4_to_f16(hi, r2, r3);
     }
-    return u32x4{w[0] | (w[1] << 16), w[2] | (w[3] << 16), w[4] | (w[5] << 16), w[6] | (w[7] << 16)};
+    else
+    {
+        fp8x4_to_f16(lo, r0, r1);
+        fp8x4_to_f16(hi, r2, r3);
+    }
+    return u32x4{r0, r1, r2, r3};
 }
 
 template <int QT>
@@ -137,7 +181,9 @@ __device__ __forceinline__ void store_out4(void* out, size_t i, f32x4 v)
     {
         uint32_t h[4];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) h[k] = QT == BF16 ? f32_to_bf16(v[k]) : f32_to_f16(v[k]);
+        for (int k = 0; k < 4; ++k)
+            h[k] = QT == BF16 ? __builtin_bit_cast(uint16_t, static_cast<__bf16>(v[k]))
+                              : __builtin_bit_cast(uint16_t, static_cast<_Float16>(v[k]));
         *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(out) + i) = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
     }
 }
@@ -157,12 +203,25 @@ __device__ __forceinline__ int row_tokens(const DecodeArgs& a, int b)
     return L < 0 ? 0 : static_cast<int>(L);
 }
 
-// Position (16-bit elements) of V[t][d] in a wave's LDS tile of 16 rows x D: chunk d/16 of row t is stored at
-// chunk (d/16) ^ ((t/4) % 4).
+// Registers of one loaded page: K as MFMA A operands, V (converted to the MFMA type) for the LDS tile.
+template <typename X8, int KSTEPS>
+struct PageRegs
+{
+    X8       k[KSTEPS];
+    u32x4    v[KSTEPS];
+    int      phys;
+    bool     ok;
+};
+
+// Position (16-bit elements) of V[t][d] in a wave's LDS tile of 16 rows x D.  The 16-byte chunk d/8 of row t
+// is stored at chunk (d/8) ^ sw(t) with sw(t) = (t % 8) ^ 2 * (t / 8).  Both access patterns then hit distinct
+// bank groups: a 16-byte write by 8 consecutive lanes (8 tokens, same chunk) spreads over 8 chunk slots mod 8,
+// and a PV operand read (tokens 4g + i for g = 0..3, chunks 2n and 2n + 1) touches 8 distinct slots mod 8.
 template <int D>
 __device__ __forceinline__ int lds_pos(int t, int d)
 {
-    return t * D + ((((d >> 4) ^ ((t >> 2) & 3))) << 4) + (d & 15);
+    const int sw = (t & 7) ^ ((t >> 3) << 1);
+    return t * D + ((((d >> 3) ^ sw)) << 3) + (d & 7);
 }
 
 __device__ __forceinline__ float xor_max(float x)
@@ -182,12 +241,12 @@ __device__ __forceinline__ float xor_sum(float x)
 // Waves per SIMD the register budget is sized for: 4 (128 registers) where that fits without spills.
 template <int CT, int QT, int D>
 constexpr int kMfmaWaves =
-    D == 256 ? 2 : ((D == 128 && !((QT == BF16 && CT == BF16) || (QT == F16 && CT == F16))) ? 3 : 4);
+    D == 256 ? 2 : ((D == 128 && (FFKV_MFMA_ROLLING || !((QT == BF16 && CT == BF16) || (QT == F16 && CT == F16)))) ? 3 : 4);
 
 // Work item i (blockIdx.x) of W (gridDim.x); KV heads blockIdx.y*NW .. +NW, one per wave.
 template <int CT, int QT, int D>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kMfmaWaves<CT, QT, D>, 8))) void
-paged_decode_mfma(DecodeArgs a)
+__global__ __launch_bounds__(64 * FFKV_MFMA_MAX_WAVES) __attribute__((amdgpu_waves_per_eu(kMfmaWaves<CT, QT, D>, 8)))
+void paged_decode_mfma(DecodeArgs a)
 {
     constexpr bool BF = kBF<CT>;
     using M = MType<BF>;
@@ -195,8 +254,8 @@ paged_decode_mfma(DecodeArgs a)
     constexpr int  NT = D / 16;                          // output tiles of 16 dims
     constexpr bool NEED_LO = !((QT == BF16 && BF) || (QT == F16 && !BF));
 
-    __shared__ uint16_t s_v[4][kBlockSize * D];
-    __shared__ int64_t  s_scan[4];
+    __shared__ uint16_t s_v[FFKV_MFMA_MAX_WAVES][kBlockSize * D];
+    __shared__ int64_t  s_scan[FFKV_MFMA_MAX_WAVES];
     __shared__ int64_t  s_total;
     __shared__ int      s_b0;
     __shared__ int64_t  s_pb0;
@@ -228,6 +287,16 @@ paged_decode_mfma(DecodeArgs a)
     for (int w = 0; w < wave; ++w) wave_base += s_scan[w];
     if (tid == nthreads - 1) s_total = wave_base + incl;
     __syncthreads();
+    // rows without any token get a zero output; nobody else touches them
+    if (blockIdx.x == 0 && blockIdx.y == 0)
+    {
+        for (int r = r0; r < r1; ++r)
+        {
+            if (row_pages(a, r) != 0) continue;
+            for (int e = 0; e < a.num_heads * D; e += 4)
+                store_out4<QT>(a.out, static_cast<size_t>(r) * a.num_heads * D + e, f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+        }
+    }
     const int64_t P = s_total;
     const int64_t W = min(static_cast<int64_t>(gridDim.x), P);
     const int64_t item = blockIdx.x;
@@ -277,6 +346,18 @@ paged_decode_mfma(DecodeArgs a)
 #pragma unroll
         for (int j = 0; j < KSTEPS; ++j)
         {
+            if constexpr (!NEED_LO)
+            {
+                // q is stored in the MFMA input type: its 16 bytes are the operand
+                u32x4 w = u32x4{0u, 0u, 0u, 0u};
+                if (c < G)
+                    w = *reinterpret_cast<const u32x4*>(
+                        static_cast<const uint16_t*>(a.q) +
+                        (static_cast<size_t>(b) * a.num_heads + kvh * G + c) * D + dim_of<CT>(j, g));
+                qhi[j] = __builtin_bit_cast(typename M::x8, w);
+                qlo[j] = qhi[j];
+                continue;
+            }
             float x[8];
             if (c < G)
                 load_q8<QT>(a.q, (static_cast<size_t>(b) * a.num_heads + kvh * G + c) * D + dim_of<CT>(j, g), x);
@@ -303,17 +384,14 @@ paged_decode_mfma(DecodeArgs a)
         for (int n = 0; n < NT; ++n) acc[n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
         const int32_t* table = a.block_table + static_cast<int64_t>(b) * a.max_blocks;
-        for (int pg = static_cast<int>(p - pb); pg < static_cast<int>(seg_end - pb); ++pg)
-        {
-            const int phys = table[pg];
-            if (phys < 0 || phys >= a.num_blocks) continue;  // uniform: masked page
-            const int n_tok = min(kBlockSize, Lp - pg * kBlockSize);
 
-            // ---- load K (A operand rows = tokens) and V (to LDS) of token c ----------------------------
-            const size_t row_c = (static_cast<size_t>(phys) * kBlockSize + c) * a.num_kv_heads + kvh;
-            const bool   tok_ok = c < n_tok;
-            typename M::x8 kop[KSTEPS];
-            u32x4          vraw[KSTEPS];
+        // Issue the K and V loads of page pg (token c of the page, lane group g's dims) into registers.
+        auto load_page = [&](int pg, PageRegs<typename M::x8, KSTEPS>& r)
+        {
+            r.phys = table[pg];
+            r.ok = r.phys >= 0 && r.phys < a.num_blocks;  // uniform: a masked page is skipped
+            if (!r.ok) return;
+            const size_t row_c = (static_cast<size_t>(r.phys) * kBlockSize + c) * a.num_kv_heads + kvh;
             if constexpr (kElemBytes<CT> == 2)
             {
                 const char* kp = static_cast<const char*>(a.k_cache) + row_c * D * 2;
@@ -321,9 +399,9 @@ paged_decode_mfma(DecodeArgs a)
 #pragma unroll
                 for (int j = 0; j < KSTEPS; ++j)
                 {
-                    kop[j] = __builtin_bit_cast(typename M::x8,
+                    r.k[j] = __builtin_bit_cast(typename M::x8,
                                                 *reinterpret_cast<const u32x4*>(kp + dim_of<CT>(j, g) * 2));
-                    vraw[j] = *reinterpret_cast<const u32x4*>(vp + dim_of<CT>(j, g) * 2);
+                    r.v[j] = *reinterpret_cast<const u32x4*>(vp + dim_of<CT>(j, g) * 2);
                 }
             }
             else
@@ -335,29 +413,41 @@ paged_decode_mfma(DecodeArgs a)
                 {
                     const u32x4 kw = *reinterpret_cast<const u32x4*>(kp + dim_of<CT>(j, g));
                     const u32x4 vw = *reinterpret_cast<const u32x4*>(vp + dim_of<CT>(j, g));
-                    kop[j] = __builtin_bit_cast(typename M::x8, codes_to_m<CT>(kw[0], kw[1]));
-                    kop[j + 1] = __builtin_bit_cast(typename M::x8, codes_to_m<CT>(kw[2], kw[3]));
-                    vraw[j] = codes_to_m<CT>(vw[0], vw[1]);
-                    vraw[j + 1] = codes_to_m<CT>(vw[2], vw[3]);
+                    r.k[j] = __builtin_bit_cast(typename M::x8, codes_to_m<CT>(kw[0], kw[1]));
+                    r.k[j + 1] = __builtin_bit_cast(typename M::x8, codes_to_m<CT>(kw[2], kw[3]));
+                    r.v[j] = codes_to_m<CT>(vw[0], vw[1]);
+                    r.v[j + 1] = codes_to_m<CT>(vw[2], vw[3]);
                 }
             }
-            // stage V[t = c] (zero for slots past the row's last token) into the wave's LDS tile
+        };
+
+        // Stage a loaded page: V rows into the wave's LDS tile, scores S^T = K Q^T into s.  Consumes r.k and
+        // r.v, so the next page can be loaded into r right after.
+        auto stage_page = [&](int pg, const PageRegs<typename M::x8, KSTEPS>& r, f32x4& s)
+        {
+            const int n_tok = min(kBlockSize, Lp - pg * kBlockSize);
+            // V[t = c], zero for slots past the row's last token
+            const bool tok_ok = c < n_tok;
 #pragma unroll
             for (int j = 0; j < KSTEPS; ++j)
             {
-                const u32x4 w = tok_ok ? vraw[j] : u32x4{0u, 0u, 0u, 0u};
+                const u32x4 w = tok_ok ? r.v[j] : u32x4{0u, 0u, 0u, 0u};
                 *reinterpret_cast<u32x4*>(sv + lds_pos<D>(c, dim_of<CT>(j, g))) = w;
             }
-
-            // ---- S^T = K Q^T: lane (c, g) gets tokens 4g + i of head c ----------------------------------
-            f32x4 s = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            // lane (c, g) gets tokens 4g + i of head c
+            s = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int j = 0; j < KSTEPS; ++j)
             {
-                s = M::mma32(kop[j], qhi[j], s);
-                if constexpr (NEED_LO) s = M::mma32(kop[j], qlo[j], s);
+                s = M::mma32(r.k[j], qhi[j], s);
+                if constexpr (NEED_LO) s = M::mma32(r.k[j], qlo[j], s);
             }
+        };
 
+        // Online softmax of a staged page's scores and PV from its LDS tile.
+        auto finish_page = [&](int pg, int phys, f32x4 s)
+        {
+            const int n_tok = min(kBlockSize, Lp - pg * kBlockSize);
             float ks[4], vs[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i)
@@ -412,8 +502,10 @@ paged_decode_mfma(DecodeArgs a)
                 ph[i] = M::bits(pv[i]);
                 pl[i] = M::bits(pv[i] - M::value(ph[i]));
             }
-            const typename M::x4 phi = __builtin_bit_cast(typename M::x4, u32x2{ph[0] | (ph[1] << 16), ph[2] | (ph[3] << 16)});
-            const typename M::x4 plo = __builtin_bit_cast(typename M::x4, u32x2{pl[0] | (pl[1] << 16), pl[2] | (pl[3] << 16)});
+            const typename M::x4 phi =
+                __builtin_bit_cast(typename M::x4, u32x2{ph[0] | (ph[1] << 16), ph[2] | (ph[3] << 16)});
+            const typename M::x4 plo =
+                __builtin_bit_cast(typename M::x4, u32x2{pl[0] | (pl[1] << 16), pl[2] | (pl[3] << 16)});
 
             // LDS writes of this wave are complete before its reads below (in-order LDS queue of one wave);
             // the fence keeps the compiler from moving the reads above the writes.
@@ -421,7 +513,7 @@ paged_decode_mfma(DecodeArgs a)
             __builtin_amdgcn_wave_barrier();
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-            // ---- O^T[d, h] += V^T[d, t] P^T[t, h] over the 16 dims of each tile -------------------------
+            // O^T[d, h] += V^T[d, t] P^T[t, h] over the 16 dims of each tile
 #pragma unroll
             for (int n = 0; n < NT; ++n)
             {
@@ -429,7 +521,8 @@ paged_decode_mfma(DecodeArgs a)
                 const uint32_t v1 = sv[lds_pos<D>(4 * g + 1, 16 * n + c)];
                 const uint32_t v2 = sv[lds_pos<D>(4 * g + 2, 16 * n + c)];
                 const uint32_t v3 = sv[lds_pos<D>(4 * g + 3, 16 * n + c)];
-                const typename M::x4 vt = __builtin_bit_cast(typename M::x4, u32x2{v0 | (v1 << 16), v2 | (v3 << 16)});
+                const typename M::x4 vt =
+                    __builtin_bit_cast(typename M::x4, u32x2{v0 | (v1 << 16), v2 | (v3 << 16)});
                 acc[n] = M::mma16(vt, phi, acc[n]);
                 acc[n] = M::mma16(vt, plo, acc[n]);
             }
@@ -437,7 +530,35 @@ paged_decode_mfma(DecodeArgs a)
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
             __builtin_amdgcn_wave_barrier();
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        };
+
+        const int pg0 = static_cast<int>(p - pb);
+        const int pg1 = static_cast<int>(seg_end - pb);
+        // Rolling prefetch: the loads of page pg + 1 are issued as soon as page pg's registers have been consumed
+        // (V written to LDS, K fed to the score MFMAs) and stay in flight during page pg's softmax and PV.
+#if FFKV_MFMA_ROLLING
+        PageRegs<typename M::x8, KSTEPS> r;
+        load_page(pg0, r);
+        for (int pg = pg0; pg < pg1; ++pg)
+        {
+            const bool ok = r.ok;
+            const int  phys = r.phys;
+            f32x4      s;
+            if (ok) stage_page(pg, r, s);
+            if (pg + 1 < pg1) load_page(pg + 1, r);
+            if (ok) finish_page(pg, phys, s);
         }
+#else
+        for (int pg = pg0; pg < pg1; ++pg)
+        {
+            PageRegs<typename M::x8, KSTEPS> r;
+            load_page(pg, r);
+            if (!r.ok) continue;
+            f32x4 s;
+            stage_page(pg, r, s);
+            finish_page(pg, r.phys, s);
+        }
+#endif
 
         // ---- finish the row segment ---------------------------------------------------------------------
         const float l_tot = xor_sum(l_run);
@@ -492,41 +613,75 @@ paged_decode_mfma(DecodeArgs a)
             }
         }
     }
+
 }
 
-// Combine the partials of rows split over several work items; write zeros for rows without tokens.
-// One workgroup per (row, 256 / D heads).
+// Combine the partials of rows split over several work items.
+// One workgroup of four waves per (row, head): wave w folds segments i_lo + w, i_lo + w + 4, ... into an online
+// (max, denominator, output) state (lane = D/64 dims), then the four states are combined through LDS.
 template <int QT, int D>
 __global__ __launch_bounds__(256) void paged_decode_mfma_merge(DecodeArgs a)
 {
-    constexpr int HPW = 256 / D;
+    constexpr int PER = D / 64;  // dims per lane
     const int     b = blockIdx.x;
-    const int     h = blockIdx.y * HPW + threadIdx.x / D;
-    const int     d = threadIdx.x % D;
-    if (h >= a.num_heads) return;
-    const size_t oi = (static_cast<size_t>(b) * a.num_heads + h) * D + d;
-    if (row_pages(a, b) == 0)
-    {
-        store_act1(a.out, QT, oi, 0.0f);
-        return;
-    }
+    const int     h = blockIdx.y;
+    const int     lane = threadIdx.x & 63;
+    const int     wave = threadIdx.x >> 6;
+    const size_t  ob = (static_cast<size_t>(b) * a.num_heads + h) * D;
+    __shared__ float s_m[4], s_l[4];
+    __shared__ float s_o[4][D];
+
+    if (row_pages(a, b) == 0) return;  // zeroed by the decode kernel
     const int i_lo = a.ws_meta[2 * b];
     const int i_hi = a.ws_meta[2 * b + 1];
     if (i_lo == i_hi) return;  // written by the decode kernel
-    float M = kNegInf;
-    for (int i = i_lo; i <= i_hi; ++i) M = fmaxf(M, a.ws_ml[((static_cast<int64_t>(i) + b) * a.num_heads + h) * 2]);
-    float o = 0.0f, lsum = 0.0f;
-    if (M != kNegInf)
+
+    float m = kNegInf, l = 0.0f, o[PER];
+#pragma unroll
+    for (int k = 0; k < PER; ++k) o[k] = 0.0f;
+    for (int i = i_lo + wave; i <= i_hi; i += 4)
     {
-        for (int i = i_lo; i <= i_hi; ++i)
-        {
-            const int64_t slot = static_cast<int64_t>(i) + b;
-            const float   w = __builtin_amdgcn_exp2f(a.ws_ml[(slot * a.num_heads + h) * 2] - M);
-            lsum += a.ws_ml[(slot * a.num_heads + h) * 2 + 1] * w;
-            o += a.ws_acc[(slot * a.num_heads + h) * D + d] * w;
-        }
+        const int64_t slot = static_cast<int64_t>(i) + b;
+        const float   ms = a.ws_ml[(slot * a.num_heads + h) * 2];
+        const float   ls = a.ws_ml[(slot * a.num_heads + h) * 2 + 1];
+        const float*  src = a.ws_acc + (slot * a.num_heads + h) * D + lane * PER;
+        float         x[PER];
+#pragma unroll
+        for (int k = 0; k < PER; ++k) x[k] = src[k];
+        if (ms == kNegInf) continue;  // segment without a valid page
+        const float mn = fmaxf(m, ms);
+        const float wa = __builtin_amdgcn_exp2f(m - mn);
+        const float wb = __builtin_amdgcn_exp2f(ms - mn);
+        l = l * wa + ls * wb;
+#pragma unroll
+        for (int k = 0; k < PER; ++k) o[k] = o[k] * wa + x[k] * wb;
+        m = mn;
     }
-    store_act1(a.out, QT, oi, lsum > 0.0f ? o / lsum : 0.0f);
+    if (lane == 0)
+    {
+        s_m[wave] = m;
+        s_l[wave] = l;
+    }
+#pragma unroll
+    for (int k = 0; k < PER; ++k) s_o[wave][lane * PER + k] = o[k];
+    __syncthreads();
+    if (threadIdx.x < D)
+    {
+        const int d = threadIdx.x;
+        float     M = fmaxf(fmaxf(s_m[0], s_m[1]), fmaxf(s_m[2], s_m[3]));
+        float     L = 0.0f, O = 0.0f;
+        if (M != kNegInf)
+        {
+#pragma unroll
+            for (int w = 0; w < 4; ++w)
+            {
+                const float wt = __builtin_amdgcn_exp2f(s_m[w] - M);
+                L += s_l[w] * wt;
+                O += s_o[w][d] * wt;
+            }
+        }
+        store_act1(a.out, QT, ob + d, L > 0.0f ? O / L : 0.0f);
+    }
 }
 
 namespace
@@ -536,17 +691,15 @@ template <int CT, int QT, int D>
 hipError_t launch_m3(const DecodeArgs& a0, hipStream_t stream)
 {
     DecodeArgs a = a0;
-    const int  nw = a.num_kv_heads < 4 ? a.num_kv_heads : 4;
+    const int  nw = a.num_kv_heads < FFKV_MFMA_MAX_WAVES ? a.num_kv_heads : FFKV_MFMA_MAX_WAVES;
     const int  gy = (a.num_kv_heads + nw - 1) / nw;
     const auto kern = paged_decode_mfma<CT, QT, D>;
     const int  items = decode_mfma_items(reinterpret_cast<const void*>(kern), 64 * nw, gy);
     hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(items), static_cast<unsigned>(gy)), dim3(64 * nw), 0, stream, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    constexpr int HPW = 256 / D;
     hipLaunchKernelGGL((paged_decode_mfma_merge<QT, D>),
-                       dim3(static_cast<unsigned>(a.batch), static_cast<unsigned>((a.num_heads + HPW - 1) / HPW)),
-                       dim3(256), 0, stream, a);
+                       dim3(static_cast<unsigned>(a.batch), static_cast<unsigned>(a.num_heads)), dim3(256), 0, stream, a);
     return hipGetLastError();
 }
 

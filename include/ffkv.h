@@ -78,9 +78,11 @@ int ffkv_append(const void* k_src, const void* v_src, int src_dtype, void* k_cac
 
 /*
  * Bytes of scratch ffkv_paged_decode needs for split-K partial results at these sizes.  max_context_len is
- * an upper bound on context_lens[b] + 1 (<= 0 means max_blocks * 16).
+ * an upper bound on context_lens[b] + 1 (<= 0 means max_blocks * 16).  No counterpart in the reference, whose
+ * decode kernel has no split-K (src/kernels/attention.cu:475-485).
  */
 size_t ffkv_decode_workspace_bytes(int batch, int num_heads, int head_dim, int max_blocks, int max_context_len);
+
 
 /*
  * PagedAttention decode: out[b, h, :] = softmax(scale * q[b,h] . K_j) V_j over the context_lens[b] + 1 cached
@@ -90,11 +92,10 @@ size_t ffkv_decode_workspace_bytes(int batch, int num_heads, int head_dim, int m
  *
  * qo_dtype (q and out) is F32, F16 or BF16; cache_dtype as for ffkv_append.  scale <= 0 selects
  * 1/sqrt(head_dim) (src/kernels/attention.cu:458).  num_heads must be a multiple of num_kv_heads with a group
- * size of at most 16; head_dim 64, 128 or 256; q and cache pointers 16-byte aligned.  Long rows are split over
- * the context and merged by a second pass; the partials live in `workspace` (ffkv_decode_workspace_bytes), or,
- * when workspace is
- * NULL, in stream-ordered memory the library allocates and frees on `stream`.  Rows whose context_lens[b] + 1
- * exceeds max_context_len are truncated to it.
+ * size of at most 16; head_dim 64, 128 or 256; q, out, cache and workspace pointers 16-byte aligned.  Rows are
+ * split over the context and the pieces merged; the partials live in `workspace` (ffkv_decode_workspace_bytes;
+ * any initial contents), or, when workspace is NULL, in stream-ordered memory the library allocates and frees on
+ * `stream`.  Calls sharing one workspace must not overlap in time (use one workspace per stream).  Rows whose context_lens[b] + 1 exceeds max_context_len are truncated to it.
  */
 int ffkv_paged_decode(const void* q, void* out, int qo_dtype, const void* k_cache, const void* v_cache,
                       int cache_dtype, const float* k_scale, const float* v_scale, const int32_t* block_table,

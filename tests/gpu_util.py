@@ -41,8 +41,7 @@ def run_step(ff, c, dev, max_context_len: int = 0, workspace=False):
     ff.append_kv_cache(kn, vn, kp, vp, bt, ctx, ks, vs)
     ws = None
     if workspace:
-        nbytes = ff.decode_workspace_bytes(c.B, c.Hq, c.D, c.max_blocks, max_context_len)
-        ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=dev)
+        ws = ff.decode_workspace(c.B, c.Hq, c.D, c.max_blocks, max_context_len, device=dev)
     out = ff.paged_attention(q, kp, vp, bt, ctx, k_scale=ks, v_scale=vs, max_context_len=max_context_len,
                              workspace=ws)
     torch.cuda.synchronize()

@@ -100,3 +100,4 @@ def test_workspace_bytes_monotone(ff):
     # the matrix-core kernel splits any row over work items, so even one-chunk rows need partial slots
     assert ff.decode_workspace_bytes(8, 28, 128, 16, 0) > 0
     assert ff.decode_workspace_bytes(0, 28, 128, 2049, 0) == 0
+

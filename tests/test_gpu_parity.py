@@ -161,3 +161,67 @@ def test_generic_and_mfma_kernels_agree(ff, gpu):
     mf = gout.reshape(out32.shape)
     assert np.abs(gen - out32).max() <= 1e-4
     assert np.abs(mf - out32).max() <= 2e-3
+
+
+def test_workspace_reused_across_calls(ff, gpu):
+    """One workspace, filled with garbage first, serves consecutive calls of different shapes, in-kernel merge
+    (B=64) and merge-kernel (B=5) calls alternating, so each call finds the other layout's data where its
+    arrival counters live."""
+    import torch
+
+    import gpu_util as gu
+
+    rng = np.random.default_rng(25)
+    big = cases.make_case(25, 64, 32, 8, 128, rng.integers(512, 4097, size=64), act="bf16")
+    small = cases.make_case(26, 5, 32, 8, 128, rng.integers(1, 900, size=5), act="bf16")
+    ws = ff.decode_workspace(64, 32, 128, max(big.max_blocks, small.max_blocks), device=gpu)
+    ws.copy_(torch.randint(0, 256, ws.shape, dtype=torch.uint8, device=gpu))
+    for c in (big, small, big, small, big):
+        kp, vp, _, _, _, out32 = cases.oracle_step(c)
+        kd, vd = gu.to_dev(kp, c.kv, gpu), gu.to_dev(vp, c.kv, gpu)
+        out = ff.paged_attention(gu.to_dev(c.q, c.act, gpu), kd, vd, torch.from_numpy(c.block_table).to(gpu),
+                                 torch.from_numpy(c.ctx).to(gpu), workspace=ws)
+        torch.cuda.synchronize()
+        got = gu.out_to_f32(gu.to_host(out, np.uint16), c.act).reshape(out32.shape)
+        assert np.abs(got - out32).max() <= 2e-3 + 2 ** -8
+
+
+def test_graph_capture_replays(ff, gpu):
+    """Append + decode captured in a hipGraph (through torch.cuda.graph) and replayed several times, with eager
+    work and host synchronization between replays; every replay matches the eager result."""
+    import torch
+
+    import gpu_util as gu
+
+    rng = np.random.default_rng(27)
+    c = cases.make_case(27, 16, 32, 8, 128, rng.integers(100, 2000, size=16), act="bf16")
+    kp0, vp0 = gu.to_dev(c.k_pool, c.kv, gpu), gu.to_dev(c.v_pool, c.kv, gpu)
+    bt = torch.from_numpy(c.block_table).to(gpu)
+    ctx = torch.from_numpy(c.ctx).to(gpu)
+    kn, vn, q = gu.to_dev(c.k_new, c.act, gpu), gu.to_dev(c.v_new, c.act, gpu), gu.to_dev(c.q, c.act, gpu)
+    ws = ff.decode_workspace(c.B, c.Hq, c.D, c.max_blocks, device=gpu)
+    out = torch.empty((c.B, 1, c.Hq * c.D), dtype=torch.bfloat16, device=gpu)
+    kp, vp = kp0.clone(), vp0.clone()
+
+    def step():
+        ff.append_kv_cache(kn, vn, kp, vp, bt, ctx)
+        ff.paged_attention(q, kp, vp, bt, ctx, out=out, workspace=ws)
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step()                                   # warm-up outside capture
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    eager = out.clone()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step()
+    for _ in range(4):
+        kp.copy_(kp0)
+        vp.copy_(vp0)
+        out.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
