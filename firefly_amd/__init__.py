@@ -19,7 +19,7 @@ DTYPE_F32 = 0
 DTYPE_F16 = 1
 DTYPE_BF16 = 2
 DTYPE_I8 = 3
-DTYPE_FP8_E4M3 = 7
+DTYPE_FP8_E4M3 = 8
 
 OK = 0
 ERR_INVALID_ARGUMENT = -1

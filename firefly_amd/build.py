@@ -40,7 +40,7 @@ DEVICE = [f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang", "-p
 
 
 def _sources() -> list[Path]:
-    return sorted(list(CSRC.glob("*.hip")) + list(CSRC.glob("*.cpp")))
+    return sorted(list(CSRC.glob("*.hip")) + list(CSRC.glob("*.cpp")) + list((CSRC / "host").glob("*.cpp")))
 
 
 def _compile(src: Path) -> Path:
@@ -48,6 +48,9 @@ def _compile(src: Path) -> Path:
     cmd = [HIPCC, *COMMON, *DEVICE, "-c", str(src), "-o", str(obj)]
     if src.suffix == ".hip":
         cmd[1:1] = ["-x", "hip"]
+    else:
+        # host C++: only the C ABI (ffkv.h) and the firefly:: API (include/firefly) are exported
+        cmd[1:1] = ["-fvisibility=hidden", "-fvisibility-inlines-hidden"]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"compile failed: {' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
@@ -69,11 +72,24 @@ def build_library(jobs: int = 8) -> Path:
     return LIB
 
 
+def build_test_shims() -> None:
+    """Test-only helpers linked against libffkv.so: the C++-API shim used by tests/test_gpu_cxx_api.py."""
+    src = ROOT / "tests" / "cpp" / "kernels_api_shim.cpp"
+    if not src.exists():
+        return
+    out = ROOT / "tests" / "cpp" / "libkernels_api_shim.so"
+    cmd = [HIPCC, "-O2", "-std=c++20", "-fPIC", "-shared", f"-I{ROOT / 'include'}", str(src), "-o", str(out),
+           f"-L{PKG}", "-lffkv", "-Wl,-rpath,$ORIGIN/../../firefly_amd"]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"test shim build failed: {' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
+
+
 def build_oracle() -> None:
     """Build the CPU checker (and, where the reference sources exist, the compiled reference host code)."""
     make = shutil.which("make") or "make"
     subprocess.run([make, "-C", str(ROOT / "oracle"), "-j4"], check=True, capture_output=True, text=True)
-    if Path("/root/reference/src/scheduler.cc").exists() and (ROOT / "oracle" / "ref_sched_shim.cpp").exists():
+    if Path("/root/reference/src/scheduler.cc").exists():
         subprocess.run([make, "-C", str(ROOT / "oracle"), "ref"], check=True, capture_output=True, text=True)
 
 
@@ -83,6 +99,7 @@ def main(argv: list[str] | None = None) -> int:
     ap.add_argument("--no-oracle", action="store_true")
     args = ap.parse_args(argv)
     lib = build_library(args.jobs)
+    build_test_shims()
     print(f"built {lib}")
     if not args.no_oracle:
         build_oracle()

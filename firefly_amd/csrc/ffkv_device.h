@@ -17,7 +17,7 @@ enum DType : int
     F16 = 1,
     BF16 = 2,
     I8 = 3,
-    FP8 = 7,
+    FP8 = 8,
 };
 
 __device__ __forceinline__ uint32_t f2u(float x) { return __builtin_bit_cast(uint32_t, x); }

@@ -1,0 +1,166 @@
+// kernels.cpp - firefly::kernels entry points over the C ABI (ffkv.h).
+//
+// Shapes and conventions follow the reference dispatcher (src/kernels/attention.cu:452-493): batch = q.shape[0],
+// num_heads = q.shape[2], head_dim = q.shape[3], scale = 1/sqrt(head_dim), the block-table row stride is the
+// max_context_blocks argument, and the launch goes to the thread's default stream.  The decode workspace (split
+// partial results) is cached per thread and grown outside of stream capture; while a stream is being captured a
+// missing or too-small workspace makes the library allocate stream-ordered memory inside the graph instead.
+#include <hip/hip_runtime_api.h>
+
+#include <iostream>
+
+#include "ffkv.h"
+#include "firefly/kernels.h"
+
+namespace firefly::kernels
+{
+
+namespace
+{
+
+thread_local hipStream_t t_stream = nullptr;
+thread_local std::string t_error;
+
+struct Workspace
+{
+    void*  ptr = nullptr;
+    size_t bytes = 0;
+    int    device = -1;
+};
+thread_local Workspace t_ws;
+
+void report(int rc, const char* what)
+{
+    if (rc == FFKV_OK)
+    {
+        t_error.clear();
+        return;
+    }
+    t_error = std::string(what) + ": " + ffkv_last_error();
+    std::cerr << t_error << std::endl;
+}
+
+void fail(const std::string& msg)
+{
+    t_error = msg;
+    std::cerr << msg << std::endl;
+}
+
+// A workspace of at least `bytes` for the current device, or nullptr while the default stream is capturing and
+// the cached one is too small.
+void* workspace(size_t bytes, size_t& have)
+{
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    if (t_ws.ptr != nullptr && t_ws.device == dev && t_ws.bytes >= bytes)
+    {
+        have = t_ws.bytes;
+        return t_ws.ptr;
+    }
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(t_stream, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone)
+    {
+        have = 0;
+        return nullptr;
+    }
+    if (t_ws.ptr != nullptr)
+    {
+        int cur = 0;
+        (void)hipGetDevice(&cur);
+        (void)hipSetDevice(t_ws.device);
+        (void)hipDeviceSynchronize();
+        (void)hipFree(t_ws.ptr);
+        (void)hipSetDevice(cur);
+        t_ws = Workspace{};
+    }
+    void* p = nullptr;
+    if (hipMalloc(&p, bytes) != hipSuccess)
+    {
+        have = 0;
+        return nullptr;
+    }
+    t_ws = Workspace{p, bytes, dev};
+    have = bytes;
+    return p;
+}
+
+bool is_gpu(const Tensor& t) { return t.device() == Device::GPU; }
+
+int code(DType d) { return static_cast<int>(d); }
+
+void decode(Tensor& q, Tensor& k, Tensor& v, const float* k_scale, const float* v_scale, Tensor& out,
+            void* block_table, int kv_head_num, int max_context_blocks, const int* context_lens)
+{
+    if (q.shape().size() != 4 || k.shape().size() != 4 || !is_gpu(q) || !is_gpu(k) || !is_gpu(v) || !is_gpu(out))
+        return fail("PagedAttention: q must be [B, S, Hq, D] and all tensors on the GPU");
+    const int B = static_cast<int>(q.shape()[0]);
+    const int Hq = static_cast<int>(q.shape()[2]);
+    const int D = static_cast<int>(q.shape()[3]);
+    if (out.numel() < static_cast<int64_t>(B) * Hq * D || out.dtype() != q.dtype())
+        return fail("PagedAttention: output must hold B*Hq*D elements of q's dtype");
+    if (k.shape()[2] != kv_head_num || k.shape()[3] != D || v.shape() != k.shape() || v.dtype() != k.dtype())
+        return fail("PagedAttention: k/v caches must both be [num_blocks, 16, kv_head_num, head_dim]");
+    const size_t need = ffkv_decode_workspace_bytes(B, Hq, D, max_context_blocks, 0);
+    size_t       have = 0;
+    void*        ws = workspace(need, have);
+    const int rc = ffkv_paged_decode(q.data(), out.data(), code(q.dtype()), k.data(), v.data(), code(k.dtype()),
+                                     k_scale, v_scale, reinterpret_cast<const int32_t*>(block_table), context_lens, B,
+                                     Hq, kv_head_num, D, FFKV_BLOCK_SIZE, max_context_blocks,
+                                     static_cast<int>(k.shape()[0]), 0, 0.0f, ws, have, t_stream);
+    report(rc, "PagedAttention failed");
+}
+
+void append(const Tensor& k, const Tensor& v, Tensor& kc, Tensor& vc, float* ks, float* vs, const int* block_table,
+            const int* context_lens, int max_blocks)
+{
+    if (k.shape().size() != 4 || kc.shape().size() != 4 || v.shape() != k.shape() || vc.shape() != kc.shape() ||
+        k.shape()[2] != kc.shape()[2] || k.shape()[3] != kc.shape()[3])
+        return fail("append_kv_cache: k/v must be [B, S, Hkv, D] and the caches [num_blocks, 16, Hkv, D]");
+    const int rc =
+        ffkv_append(k.data(), v.data(), code(k.dtype()), kc.data(), vc.data(), code(kc.dtype()), ks, vs,
+                    reinterpret_cast<const int32_t*>(block_table), reinterpret_cast<const int32_t*>(context_lens),
+                    static_cast<int>(k.shape()[0]), static_cast<int>(k.shape()[1]), static_cast<int>(k.shape()[2]),
+                    static_cast<int>(k.shape()[3]), static_cast<int>(kc.shape()[1]), max_blocks,
+                    static_cast<int>(kc.shape()[0]), t_stream);
+    report(rc, "append_kv_cache failed");
+}
+
+}  // namespace
+
+void        set_default_stream(hipStream_t stream) { t_stream = stream; }
+hipStream_t get_default_stream() { return t_stream; }
+std::string last_error() { return t_error; }
+
+void attention(Tensor& q, Tensor& k, Tensor& v, Tensor& output, void* kv_cache_block_table, int kv_head_num,
+               int seq_len, int max_context_blocks, const int* context_lens)
+{
+    (void)seq_len;  // the decode branch attends context_lens[b] + 1 tokens whatever seq_len says
+    if (kv_cache_block_table == nullptr)
+        return fail("attention: contiguous (block-table-free) prefill attention is not part of this library");
+    decode(q, k, v, nullptr, nullptr, output, kv_cache_block_table, kv_head_num, max_context_blocks, context_lens);
+}
+
+void attention(Tensor& q, Tensor& k_cache, Tensor& v_cache, const Tensor& k_scale, const Tensor& v_scale,
+               Tensor& output, void* kv_cache_block_table, int kv_head_num, int seq_len, int max_context_blocks,
+               const int* context_lens)
+{
+    (void)seq_len;
+    if (kv_cache_block_table == nullptr) return fail("attention: a quantized cache needs a block table");
+    decode(q, k_cache, v_cache, k_scale.data_as<const float>(), v_scale.data_as<const float>(), output,
+           kv_cache_block_table, kv_head_num, max_context_blocks, context_lens);
+}
+
+void append_kv_cache(const Tensor& k, const Tensor& v, Tensor& k_cache, Tensor& v_cache, const int* block_table,
+                     const int* context_lens, int max_blocks)
+{
+    append(k, v, k_cache, v_cache, nullptr, nullptr, block_table, context_lens, max_blocks);
+}
+
+void append_kv_cache(const Tensor& k, const Tensor& v, Tensor& k_cache, Tensor& v_cache, Tensor& k_scale,
+                     Tensor& v_scale, const int* block_table, const int* context_lens, int max_blocks)
+{
+    append(k, v, k_cache, v_cache, k_scale.data_as<float>(), v_scale.data_as<float>(), block_table, context_lens,
+           max_blocks);
+}
+
+}  // namespace firefly::kernels

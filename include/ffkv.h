@@ -40,19 +40,23 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#ifndef FFKV_API
+#define FFKV_API __attribute__((visibility("default")))
+#endif
+
 #ifdef __cplusplus
 extern "C" {
 #endif
 
 #define FFKV_BLOCK_SIZE 16
 
-/* dtype codes: equal to the firefly::DType enumerators (include/firefly/types.h:16-26 in the reference,
- * plus FP8_E4M3 which the reference lacks). */
+/* dtype codes: equal to the firefly::DType enumerators F32, F16, BF16, I8 (include/firefly/types.h:16-26 in
+ * the reference, whose enum continues I32, I64, U8, UNKNOWN = 7), plus FP8_E4M3 = 8, which the reference lacks. */
 #define FFKV_DTYPE_F32 0
 #define FFKV_DTYPE_F16 1
 #define FFKV_DTYPE_BF16 2
 #define FFKV_DTYPE_I8 3
-#define FFKV_DTYPE_FP8_E4M3 7
+#define FFKV_DTYPE_FP8_E4M3 8
 
 #define FFKV_OK 0
 #define FFKV_ERR_INVALID_ARGUMENT -1
@@ -71,7 +75,7 @@ extern "C" {
  * k_scale / v_scale: I8 -> written, [num_blocks, 16, num_kv_heads]; FP8 -> read, [num_kv_heads]; else unused.
  * head_dim must be 64, 128 or 256; block_size must be 16.  Source and cache pointers must be 16-byte aligned.
  */
-int ffkv_append(const void* k_src, const void* v_src, int src_dtype, void* k_cache, void* v_cache, int cache_dtype,
+FFKV_API int ffkv_append(const void* k_src, const void* v_src, int src_dtype, void* k_cache, void* v_cache, int cache_dtype,
                 float* k_scale, float* v_scale, const int32_t* block_table, const int32_t* context_lens, int batch,
                 int seq_len, int num_kv_heads, int head_dim, int block_size, int max_blocks, int num_blocks,
                 void* stream);
@@ -81,7 +85,7 @@ int ffkv_append(const void* k_src, const void* v_src, int src_dtype, void* k_cac
  * an upper bound on context_lens[b] + 1 (<= 0 means max_blocks * 16).  No counterpart in the reference, whose
  * decode kernel has no split-K (src/kernels/attention.cu:475-485).
  */
-size_t ffkv_decode_workspace_bytes(int batch, int num_heads, int head_dim, int max_blocks, int max_context_len);
+FFKV_API size_t ffkv_decode_workspace_bytes(int batch, int num_heads, int head_dim, int max_blocks, int max_context_len);
 
 
 /*
@@ -97,17 +101,17 @@ size_t ffkv_decode_workspace_bytes(int batch, int num_heads, int head_dim, int m
  * any initial contents), or, when workspace is NULL, in stream-ordered memory the library allocates and frees on
  * `stream`.  Calls sharing one workspace must not overlap in time (use one workspace per stream).  Rows whose context_lens[b] + 1 exceeds max_context_len are truncated to it.
  */
-int ffkv_paged_decode(const void* q, void* out, int qo_dtype, const void* k_cache, const void* v_cache,
+FFKV_API int ffkv_paged_decode(const void* q, void* out, int qo_dtype, const void* k_cache, const void* v_cache,
                       int cache_dtype, const float* k_scale, const float* v_scale, const int32_t* block_table,
                       const int32_t* context_lens, int batch, int num_heads, int num_kv_heads, int head_dim,
                       int block_size, int max_blocks, int num_blocks, int max_context_len, float scale,
                       void* workspace, size_t workspace_bytes, void* stream);
 
 /* Message describing the last error returned on the calling thread ("" if none). */
-const char* ffkv_last_error(void);
+FFKV_API const char* ffkv_last_error(void);
 
 /* Library version string. */
-const char* ffkv_version(void);
+FFKV_API const char* ffkv_version(void);
 
 #ifdef __cplusplus
 }

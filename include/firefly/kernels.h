@@ -1,0 +1,60 @@
+// kernels.h - the paged KV-cache operators with the reference's call signatures.
+//
+// Drop-in for the KV-cache part of include/firefly/kernels.h (reference, :8-9 and :70-84):
+//   set_default_stream / get_default_stream   thread-local stream every launch below uses
+//   attention(...)                            paged decode when kv_cache_block_table != nullptr
+// plus the append the reference keeps private to its model (src/model/qwen_model.cu:21-47, launched at
+// :138-143), exported here, and quantized-cache overloads of both.  Each forwards to the C ABI in ffkv.h.
+//
+// Like the reference, the functions return void and report failures on std::cerr
+// (src/kernels/attention.cu:487-491); last_error() additionally returns the message of the calling thread's
+// last failure ("" if none).  Everything is asynchronous on the default stream and may be captured in a hipGraph.
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+
+#include <string>
+
+#include "firefly/tensor.h"
+
+namespace firefly::kernels
+{
+
+FIREFLY_API void        set_default_stream(hipStream_t stream);
+FIREFLY_API hipStream_t get_default_stream();
+FIREFLY_API std::string last_error();
+
+/**
+ * @brief Scaled dot-product attention (reference include/firefly/kernels.h:83-84).
+ *
+ * Paged decode when kv_cache_block_table != nullptr: q [B, 1, Hq, D]; k / v the page pools
+ * [num_blocks, 16, kv_head_num, D]; output [B, 1, Hq*D] (or any tensor of B*Hq*D elements) in q's dtype;
+ * kv_cache_block_table int32 [B, max_context_blocks] on the device; context_lens int32 [B] on the device, tokens
+ * cached before this step (context_lens[b] + 1 tokens are attended).  seq_len is ignored, as in the reference's
+ * decode branch.  The reference's other branch (kv_cache_block_table == nullptr: contiguous causal prefill
+ * attention, src/kernels/attention.cu:460-474) is not part of this library and is reported as an error.
+ */
+FIREFLY_API void attention(Tensor& q, Tensor& k, Tensor& v, Tensor& output, void* kv_cache_block_table,
+                           int kv_head_num, int seq_len, int max_context_blocks, const int* context_lens);
+
+// Paged decode over an int8 (k_scale/v_scale fp32 [num_blocks, 16, Hkv]) or fp8 e4m3 (fp32 [Hkv]) cache.
+FIREFLY_API void attention(Tensor& q, Tensor& k_cache, Tensor& v_cache, const Tensor& k_scale, const Tensor& v_scale,
+                           Tensor& output, void* kv_cache_block_table, int kv_head_num, int seq_len,
+                           int max_context_blocks, const int* context_lens);
+
+/**
+ * @brief Write new K/V tokens into their pages (the reference's append_kv_cache kernel).
+ *
+ * k, v [B, S, Hkv, D] (F32/F16/BF16); k_cache, v_cache [num_blocks, 16, Hkv, D]; token t of row b goes to
+ * position context_lens[b] + t (context_lens == nullptr means 0) of the row's block table
+ * (block_table[b*max_blocks + pos/16], slot pos%16).  A narrower cache type rounds to nearest even.
+ */
+FIREFLY_API void append_kv_cache(const Tensor& k, const Tensor& v, Tensor& k_cache, Tensor& v_cache,
+                                 const int* block_table, const int* context_lens, int max_blocks);
+
+// Quantizing append: int8 cache (k_scale/v_scale written, fp32 [num_blocks, 16, Hkv]: absmax/127 per token and
+// head) or fp8 e4m3 cache (k_scale/v_scale read, fp32 [Hkv] per head).
+FIREFLY_API void append_kv_cache(const Tensor& k, const Tensor& v, Tensor& k_cache, Tensor& v_cache, Tensor& k_scale,
+                                 Tensor& v_scale, const int* block_table, const int* context_lens, int max_blocks);
+
+}  // namespace firefly::kernels

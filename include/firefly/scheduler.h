@@ -1,0 +1,75 @@
+// scheduler.h - KV block allocator and the continuous-batching scheduler that builds block tables.
+//
+// Same interfaces and behaviour as the reference (include/firefly/scheduler.h:13-74, src/scheduler.cc):
+//   BlockAllocator  LIFO free list of physical block ids 0..N-1 (the first allocations return N-1, N-2, ...);
+//                   on shortage it asks the radix tree to evict first.  Not internally locked (the scheduler
+//                   holds its mutex around every use).
+//   Scheduler       add_request() matches the prompt against the prefix cache (shared blocks, context_len);
+//                   step() gives active requests a new block when their tokens fill the last one and admits
+//                   pending requests (longest cached prefix first) with blocks for their next prefill chunk;
+//                   finish_request() returns the sequence and its blocks to the prefix cache.
+#pragma once
+
+#include <list>
+#include <memory>
+#include <mutex>
+#include <vector>
+
+#include "firefly/radix_tree.h"
+#include "firefly/request.h"
+
+namespace firefly
+{
+
+class FIREFLY_API BlockAllocator
+{
+public:
+    BlockAllocator();
+    void init(int total_blocks, RadixTree* tree = nullptr);
+    void set_radix_tree(RadixTree* tree);
+
+    // Appends num_blocks ids to out_blocks; false (nothing appended) if they cannot be had even after eviction.
+    bool allocate(int num_blocks, std::vector<int>& out_blocks);
+    void free(const std::vector<int>& blocks);
+    int  get_free_blocks() const;
+
+private:
+    std::vector<int> free_list_;  // back = next id handed out
+    int              total_blocks_ = 0;
+    RadixTree*       tree_ = nullptr;
+};
+
+struct SchedulerBatch
+{
+    std::vector<RequestPtr> requests;
+};
+
+class FIREFLY_API Scheduler
+{
+public:
+    Scheduler();
+    // max_context_blocks: pool size in blocks; max_batch_size_limit: cap on active requests;
+    // max_prefill_chunk_size: tokens a pending request may prefill in one step.
+    void init(int max_context_blocks, int max_batch_size_limit, int max_prefill_chunk_size);
+
+    void add_request(RequestPtr req);
+    SchedulerBatch step();
+    void finish_request(RequestPtr req);
+    bool has_unfinished_requests();
+
+    // Free blocks right now (diagnostics and tests).
+    int free_blocks();
+
+private:
+    std::mutex            mutex_;
+    std::list<RequestPtr> pending_;
+    std::list<RequestPtr> active_;
+
+    BlockAllocator             allocator_;
+    std::unique_ptr<RadixTree> tree_;
+    int                        block_size_ = 16;
+    int                        max_batch_ = 64;
+    int                        max_chunk_ = 256;
+};
+
+}  // namespace firefly

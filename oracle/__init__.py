@@ -16,7 +16,7 @@ _DIR = Path(__file__).resolve().parent
 LIB_PATH = _DIR / "libffkv_oracle.so"
 REF_SCHED_PATH = _DIR / "_ref" / "libref_sched.so"
 
-DTYPE_F32, DTYPE_F16, DTYPE_BF16, DTYPE_I8, DTYPE_FP8 = 0, 1, 2, 3, 7
+DTYPE_F32, DTYPE_F16, DTYPE_BF16, DTYPE_I8, DTYPE_FP8 = 0, 1, 2, 3, 8
 _NP_STORAGE = {DTYPE_F32: np.float32, DTYPE_F16: np.uint16, DTYPE_BF16: np.uint16, DTYPE_I8: np.int8,
                DTYPE_FP8: np.uint8}
 

@@ -44,7 +44,7 @@
 #define DT_F16 1
 #define DT_BF16 2
 #define DT_I8 3
-#define DT_FP8 7
+#define DT_FP8 8
 
 #define ERR_ARG -1
 #define ERR_UNSUPPORTED -2

@@ -1,0 +1,62 @@
+// kernels_api_shim.cpp - C entry points over the firefly:: C++ API, for tests/test_gpu_cxx_api.py.
+//
+// Wraps caller device buffers in non-owning firefly::Tensor views and calls the drop-in operators exactly as the
+// reference's model does (src/model/qwen_model.cu:138-156): kernels::append_kv_cache, then kernels::attention on
+// the paged caches with the block table and context_lens device pointers.  Returns 0 or -1 with the error text
+// from kernels::last_error().
+#include <cstring>
+#include <string>
+
+#include "firefly/kernels.h"
+
+using namespace firefly;
+
+extern "C" {
+
+static thread_local std::string g_err;
+
+const char* kas_last_error() { return g_err.c_str(); }
+
+// q [B,1,Hq,D], k_new/v_new [B,S,Hkv,D] in dtype qd; caches [N,16,Hkv,D] in dtype cd; out [B,1,Hq*D] in dtype qd.
+int kas_append_then_decode(void* q, void* k_new, void* v_new, void* k_cache, void* v_cache, void* k_scale,
+                           void* v_scale, int scale_rows, void* out, const int* block_table, const int* context_lens,
+                           int B, int S, int Hq, int Hkv, int D, int N, int max_blocks, int qd, int cd, void* stream)
+{
+    kernels::set_default_stream(static_cast<hipStream_t>(stream));
+    const DType qt = static_cast<DType>(qd), ct = static_cast<DType>(cd);
+    Tensor      tq = Tensor::from_external(q, {B, 1, Hq, D}, qt, Device::GPU);
+    Tensor      tk = Tensor::from_external(k_new, {B, S, Hkv, D}, qt, Device::GPU);
+    Tensor      tv = Tensor::from_external(v_new, {B, S, Hkv, D}, qt, Device::GPU);
+    Tensor      kc = Tensor::from_external(k_cache, {N, 16, Hkv, D}, ct, Device::GPU);
+    Tensor      vc = Tensor::from_external(v_cache, {N, 16, Hkv, D}, ct, Device::GPU);
+    Tensor      to = Tensor::from_external(out, {B, 1, Hq * D}, qt, Device::GPU);
+    const bool  quant = ct == DType::I8 || ct == DType::FP8_E4M3;
+    if (quant)
+    {
+        std::vector<int64_t> sshape = ct == DType::I8 ? std::vector<int64_t>{N, 16, Hkv} : std::vector<int64_t>{Hkv};
+        (void)scale_rows;
+        Tensor ks = Tensor::from_external(k_scale, sshape, DType::F32, Device::GPU);
+        Tensor vs = Tensor::from_external(v_scale, sshape, DType::F32, Device::GPU);
+        kernels::append_kv_cache(tk, tv, kc, vc, ks, vs, block_table, context_lens, max_blocks);
+        if (!kernels::last_error().empty()) return g_err = kernels::last_error(), -1;
+        kernels::attention(tq, kc, vc, ks, vs, to, const_cast<int*>(block_table), Hkv, 1, max_blocks, context_lens);
+    }
+    else
+    {
+        kernels::append_kv_cache(tk, tv, kc, vc, block_table, context_lens, max_blocks);
+        if (!kernels::last_error().empty()) return g_err = kernels::last_error(), -1;
+        kernels::attention(tq, kc, vc, to, const_cast<int*>(block_table), Hkv, 1, max_blocks, context_lens);
+    }
+    if (!kernels::last_error().empty()) return g_err = kernels::last_error(), -1;
+    return 0;
+}
+
+// The reference's prefill branch (no block table) is reported as an error by this library.
+int kas_prefill_branch_rejected()
+{
+    Tensor q = Tensor::from_external(nullptr, {1, 4, 2, 128}, DType::BF16, Device::GPU);
+    kernels::attention(q, q, q, q, nullptr, 2, 4, 0, nullptr);
+    return kernels::last_error().empty() ? 0 : 1;
+}
+
+}  // extern "C"

@@ -50,13 +50,13 @@ def _decode(ff, **kw):
     (dict(block_size=32), -2),
     (dict(head_dim=96), -2),
     (dict(src_dtype=3), -2),          # int8 is not an activation dtype
-    (dict(cache_dtype=5), -2),
+    (dict(cache_dtype=7), -2),        # the reference's UNKNOWN
     (dict(batch=-1), -1),
     (dict(num_kv_heads=0), -1),
     (dict(k_cache=None), -1),
     (dict(block_table=None), -1),
     (dict(cache_dtype=3), -1),        # int8 cache without scales
-    (dict(cache_dtype=7), -1),        # fp8 cache without scales
+    (dict(cache_dtype=8), -1),        # fp8 cache without scales
     (dict(k_src=18), -1),             # misaligned
 ])
 def test_append_rejects(ff, kw, code):

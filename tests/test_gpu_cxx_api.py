@@ -1,0 +1,72 @@
+"""The firefly:: C++ drop-in API (include/firefly/kernels.h, tensor.h) on the GPU, called the way the
+reference's model calls its operators: Tensor::from_external views over device buffers, kernels::append_kv_cache
+then kernels::attention with the block table and context_lens device pointers (tests/cpp/kernels_api_shim.cpp).
+Same bar as the C-ABI parity tests: pages bit-exact, outputs within tolerance of the CPU checker."""
+
+import ctypes
+import math
+import os
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import cases
+import oracle as O
+
+SHIM = Path(__file__).resolve().parent / "cpp" / "libkernels_api_shim.so"
+
+
+@pytest.fixture(scope="module")
+def shim(ff):
+    if not SHIM.exists():
+        pytest.skip("tests/cpp/libkernels_api_shim.so not built")
+    lib = ctypes.CDLL(str(SHIM), mode=os.RTLD_NOW)
+    vp, i = ctypes.c_void_p, ctypes.c_int
+    lib.kas_append_then_decode.restype = i
+    lib.kas_append_then_decode.argtypes = [vp] * 7 + [i, vp, vp, vp] + [i] * 9 + [vp]
+    lib.kas_last_error.restype = ctypes.c_char_p
+    lib.kas_prefill_branch_rejected.restype = i
+    return lib
+
+
+def test_shim_links_against_exported_cxx_api(shim):
+    """Loading with RTLD_NOW resolves every firefly:: symbol the shim uses from libffkv.so."""
+    assert shim.kas_last_error() == b""
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("act,kv,tol", [("bf16", "bf16", 2e-3), ("f16", "f16", 2e-3), ("bf16", "i8", 2e-2),
+                                        ("f32", "fp8", 2e-2), ("f32", "f32", 1e-4)])
+def test_cxx_api_append_then_decode(shim, gpu, act, kv, tol):
+    import torch
+
+    import gpu_util as gu
+
+    c = cases.config1(act=act, kv=kv)
+    kp, vp, ks, vs, _, out32 = cases.oracle_step(c)
+    dk, dv = gu.to_dev(c.k_pool, c.kv, gpu), gu.to_dev(c.v_pool, c.kv, gpu)
+    dks = None if c.k_scale is None else torch.from_numpy(c.k_scale.copy()).to(gpu)
+    dvs = None if c.v_scale is None else torch.from_numpy(c.v_scale.copy()).to(gpu)
+    q, kn, vn = gu.to_dev(c.q, c.act, gpu), gu.to_dev(c.k_new, c.act, gpu), gu.to_dev(c.v_new, c.act, gpu)
+    bt, ctx = torch.from_numpy(c.block_table).to(gpu), torch.from_numpy(c.ctx).to(gpu)
+    out = torch.empty((c.B, 1, c.Hq * c.D), dtype=q.dtype, device=gpu)
+    p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+    rc = shim.kas_append_then_decode(p(q), p(kn), p(vn), p(dk), p(dv), p(dks), p(dvs), 0, p(out), p(bt), p(ctx),
+                                     c.B, c.S, c.Hq, c.Hkv, c.D, c.num_blocks, c.max_blocks, c.act, c.kv,
+                                     torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert rc == 0, shim.kas_last_error()
+    conv = (lambda t: gu.to_host(t, np.uint16)) if dk.dtype in (torch.float16, torch.bfloat16) else \
+        (lambda t: t.cpu().numpy())
+    assert np.array_equal(conv(dk).view(np.uint8), kp.view(np.uint8))
+    assert np.array_equal(conv(dv).view(np.uint8), vp.view(np.uint8))
+    if c.kv == O.DTYPE_I8:
+        assert np.array_equal(dks.cpu().numpy().view(np.uint32), ks.view(np.uint32))
+    got = out.float().cpu().numpy().reshape(out32.shape)
+    assert np.abs(got - out32).max() <= tol + (0 if c.act == O.DTYPE_F32 else 2.0 ** -9)
+
+
+@pytest.mark.gpu
+def test_cxx_api_prefill_branch_reports_error(shim, gpu):
+    assert shim.kas_prefill_branch_rejected() == 1

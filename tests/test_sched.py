@@ -1,0 +1,124 @@
+"""Block-table producers (BlockAllocator, RadixTree, Scheduler) against the reference's own implementation.
+
+This repository's C++ (include/firefly, firefly_amd/csrc/host) and the reference's sources (src/scheduler.cc,
+src/radix_tree.cc) are driven through the same oracle/sched_driver.cpp.  Pins:
+  * golden results recorded from the reference build (tests/golden/sched_golden.json: pool scripts in full,
+    serving traces as digests of every scheduled block table / context length / generated count),
+  * the live reference build when it exists (oracle/_ref, only where /root/reference is mounted) on further
+    seeded workloads,
+  * closed forms: LIFO allocation order and block-aligned prefix matches.
+"""
+
+import hashlib
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import sched_util as su
+
+GOLDEN = json.loads((Path(__file__).resolve().parent / "golden" / "sched_golden.json").read_text())
+
+
+@pytest.fixture(scope="module")
+def mine():
+    if not su.MINE.exists():
+        pytest.skip(f"{su.MINE} not built (python __graft_entry__.py)")
+    return su.load(su.MINE)
+
+
+@pytest.fixture(scope="module")
+def ref():
+    if not su.REF.exists():
+        pytest.skip("reference scheduler build absent (oracle/_ref needs /root/reference at build time)")
+    return su.load(su.REF)
+
+
+def _digest(obj):
+    return hashlib.sha256(json.dumps(obj, separators=(",", ":")).encode()).hexdigest()
+
+
+def _jsonable(x):
+    return json.loads(json.dumps(x))
+
+
+@pytest.mark.parametrize("name", sorted(GOLDEN["pool"]))
+def test_pool_scripts_match_reference_golden(mine, name):
+    g = GOLDEN["pool"][name]
+    ops = [tuple(op) for op in g["ops"]]
+    assert _jsonable(su.run_pool_script(mine, g["total_blocks"], ops)) == g["results"]
+
+
+@pytest.mark.parametrize("name", sorted(GOLDEN["serving"]))
+def test_serving_trace_matches_reference_golden(mine, name):
+    g = GOLDEN["serving"][name]
+    arrivals = {int(k): [tuple(r) for r in v] for k, v in g["arrivals"].items()}
+    trace = su.run_serving(mine, g["total_blocks"], g["max_batch"], g["chunk"], arrivals)
+    assert len(trace) == g["steps"]
+    assert sum(len(s) for s in trace) == g["scheduled_requests"]
+    assert _digest(_jsonable(trace)) == g["trace_sha256"]
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_serving_matches_live_reference(mine, ref, seed):
+    rng = np.random.default_rng(100 + seed)
+    total = int(rng.integers(48, 400))
+    arrivals = su.shared_prefix_workload(200 + seed, int(rng.integers(6, 24)), int(rng.integers(16, 200)),
+                                         1, int(rng.integers(8, 120)), 1, int(rng.integers(2, 20)),
+                                         n_prefixes=int(rng.integers(1, 4)))
+    args = (total, int(rng.integers(2, 12)), int(rng.choice([16, 32, 48, 256])), arrivals)
+    assert su.run_serving(mine, *args, max_steps=600) == su.run_serving(ref, *args, max_steps=600)
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_random_pool_ops_match_live_reference(mine, ref, seed):
+    """Random inserts / matches / releases / evictions / allocations, including eviction-order ties."""
+    rng = np.random.default_rng(seed)
+    base = [list(rng.integers(0, 4, size=int(rng.integers(8, 90)))) for _ in range(6)]
+    ops, live, next_block = [], [], 0
+    for _ in range(80):
+        r = rng.random()
+        seq = [int(t) for t in base[int(rng.integers(0, len(base)))][:int(rng.integers(1, 90))]]
+        if r < 0.3:
+            nb = (len(seq) + 15) // 16
+            ops.append(("insert", seq, list(range(next_block, next_block + nb))))
+            next_block += nb
+        elif r < 0.6:
+            ops.append(("match", seq))
+            live.append(len([o for o in ops if o[0] == "match"]) - 1)
+        elif r < 0.75 and live:
+            ops.append(("release", live.pop(int(rng.integers(0, len(live))))))
+        elif r < 0.9:
+            ops.append(("evict", int(rng.integers(1, 6))))
+        else:
+            ops.append(("alloc", int(rng.integers(1, 8))))
+    assert su.run_pool_script(mine, 64, ops) == su.run_pool_script(ref, 64, ops)
+
+
+def test_lifo_closed_form(mine):
+    p = su.Pool(mine, 100)
+    try:
+        assert p.alloc(5) == [99, 98, 97, 96, 95]
+        p.free([97, 42])
+        assert p.alloc(3) == [42, 97, 94]
+        assert p.alloc(100) is None and p.free_count() == 94
+    finally:
+        p.close()
+
+
+def test_prefix_matches_are_block_aligned(mine):
+    rng = np.random.default_rng(7)
+    p = su.Pool(mine, 1000)
+    try:
+        seqs = []
+        for i in range(20):
+            s = [int(t) for t in rng.integers(0, 3, size=int(rng.integers(1, 120)))]
+            p.insert(s, list(range(i * 10, i * 10 + (len(s) + 15) // 16)))
+            seqs.append(s)
+        for s in seqs:
+            _, blocks, mt = p.match(s + [7, 7])
+            assert mt % 16 == 0 and mt <= len(s)
+            assert len(blocks) == mt // 16
+    finally:
+        p.close()
