@@ -6,6 +6,7 @@
 // keeps a per-thread message for ffkv_last_error().
 #include <hip/hip_runtime.h>
 
+#include <climits>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -250,7 +251,10 @@ int ffkv_paged_decode(const void* q, void* out, int qo_dtype, const void* k_cach
     if (!aligned16(q) || !aligned16(out) || !aligned16(k_cache) || !aligned16(v_cache))
         return fail(FFKV_ERR_INVALID_ARGUMENT, "q, out and cache pointers must be 16-byte aligned");
 
-    const int  cap = ffkv::decode_cap_tokens(max_blocks, max_context_len);
+    const int cap = ffkv::decode_cap_tokens(max_blocks, max_context_len);
+    if (static_cast<int64_t>(batch) * ceil_div(cap, FFKV_BLOCK_SIZE) > INT32_MAX)
+        return fail(FFKV_ERR_UNSUPPORTED, "batch * pages per row exceeds 2^31 - 1 (batch %d, %d tokens per row)",
+                    batch, cap);
     const bool mfma = ffkv::decode_use_mfma(cache_dtype, group);
     const int  chunk = ffkv::decode_chunk(batch, num_kv_heads, cap);
     const int  max_chunks = static_cast<int>(ceil_div(cap > 0 ? cap : 1, chunk));

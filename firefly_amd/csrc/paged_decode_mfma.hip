@@ -26,9 +26,6 @@
 #include "ffkv_device.h"
 #include "ffkv_internal.h"
 
-#ifndef FFKV_MFMA_ROLLING
-#define FFKV_MFMA_ROLLING 1  // 1: load page pg + 1 while page pg finishes (two pages of K/V live in registers)
-#endif
 #ifndef FFKV_MFMA_MAX_WAVES
 #define FFKV_MFMA_MAX_WAVES 4  // waves (= KV heads) per workgroup
 #endif
@@ -203,14 +200,15 @@ __device__ __forceinline__ int row_tokens(const DecodeArgs& a, int b)
     return L < 0 ? 0 : static_cast<int>(L);
 }
 
-// Registers of one loaded page: K as MFMA A operands, V (converted to the MFMA type) for the LDS tile.
-template <typename X8, int KSTEPS>
+// Registers of one loaded page, as loaded: NW 16-byte words of K and of V per lane (one k-step each for 16-bit
+// caches, two for 8-bit codes, which convert when the page is staged so the loads stay in flight until then).
+template <int NW>
 struct PageRegs
 {
-    X8       k[KSTEPS];
-    u32x4    v[KSTEPS];
-    int      phys;
-    bool     ok;
+    u32x4 k[NW];
+    u32x4 v[NW];
+    int   phys;
+    bool  ok;
 };
 
 // Position (16-bit elements) of V[t][d] in a wave's LDS tile of 16 rows x D.  The 16-byte chunk d/8 of row t
@@ -223,6 +221,16 @@ __device__ __forceinline__ int lds_pos(int t, int d)
     const int sw = (t & 7) ^ ((t >> 3) << 1);
     return t * D + ((((d >> 3) ^ sw)) << 3) + (d & 7);
 }
+
+__device__ __forceinline__ int wave_sum(int x)
+{
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) x += __shfl_xor(x, off, 64);
+    return x;
+}
+
+// A value equal in all lanes, moved to a scalar register.
+__device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
 
 __device__ __forceinline__ float xor_max(float x)
 {
@@ -238,10 +246,10 @@ __device__ __forceinline__ float xor_sum(float x)
 
 }  // namespace
 
-// Waves per SIMD the register budget is sized for: 4 (128 registers) where that fits without spills.
+// Waves per SIMD the register budget is sized for, with one page's K/V in flight beside the page being finished:
+// 3 (168 registers) at D = 128, 4 (128) at D = 64, 2 at D = 256.
 template <int CT, int QT, int D>
-constexpr int kMfmaWaves =
-    D == 256 ? 2 : ((D == 128 && (FFKV_MFMA_ROLLING || !((QT == BF16 && CT == BF16) || (QT == F16 && CT == F16)))) ? 3 : 4);
+constexpr int kMfmaWaves = D == 256 ? 2 : (D == 128 ? 3 : 4);
 
 // Work item i (blockIdx.x) of W (gridDim.x); KV heads blockIdx.y*NW .. +NW, one per wave.
 template <int CT, int QT, int D>
@@ -250,76 +258,69 @@ void paged_decode_mfma(DecodeArgs a)
 {
     constexpr bool BF = kBF<CT>;
     using M = MType<BF>;
+    using X8 = typename M::x8;
     constexpr int  KSTEPS = D / 32;
-    constexpr int  NT = D / 16;                          // output tiles of 16 dims
+    constexpr int  NT = D / 16;  // output tiles of 16 dims
     constexpr bool NEED_LO = !((QT == BF16 && BF) || (QT == F16 && !BF));
 
     __shared__ uint16_t s_v[FFKV_MFMA_MAX_WAVES][kBlockSize * D];
-    __shared__ int64_t  s_scan[FFKV_MFMA_MAX_WAVES];
-    __shared__ int64_t  s_total;
-    __shared__ int      s_b0;
-    __shared__ int64_t  s_pb0;
 
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
     const int c = lane & 15;  // MFMA column / row-in-tile index
     const int g = lane >> 4;  // lane group
-    const int nthreads = blockDim.x;
     const int B = a.batch;
+    const bool first_wg = blockIdx.x == 0 && blockIdx.y == 0 && wave == 0;
 
-    // ---- pages per row, block-wide exclusive scan (each thread owns a contiguous run of rows) ------------
-    const int per = (B + nthreads - 1) / nthreads;
-    const int r0 = min(B, tid * per);
-    const int r1 = min(B, r0 + per);
-    int64_t   local = 0;
-    for (int r = r0; r < r1; ++r) local += row_pages(a, r);
-    int64_t incl = local;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1)
+    // ---- total pages P, each wave on its own (64 rows per pass, no barriers) -----------------------------
+    // Rows without any token get a zero output and "no pieces" meta here; nothing else touches them.
+    // Page counts fit in 32 bits: the host bounds batch * pages per row.
+    int P = 0;
+    for (int r0 = 0; r0 < B; r0 += 64)
     {
-        const int64_t o = __shfl_up(incl, off, 64);
-        if (lane >= off) incl += o;
-    }
-    if (lane == 63) s_scan[wave] = incl;
-    __syncthreads();
-    int64_t wave_base = 0;
-    for (int w = 0; w < wave; ++w) wave_base += s_scan[w];
-    if (tid == nthreads - 1) s_total = wave_base + incl;
-    __syncthreads();
-    // rows without any token get a zero output; nobody else touches them
-    if (blockIdx.x == 0 && blockIdx.y == 0)
-    {
-        for (int r = r0; r < r1; ++r)
+        const int r = r0 + lane;
+        const int n = r < B ? row_pages(a, r) : 0;
+        P += uniform(wave_sum(n));
+        if (first_wg && r < B && n == 0)
         {
-            if (row_pages(a, r) != 0) continue;
             for (int e = 0; e < a.num_heads * D; e += 4)
                 store_out4<QT>(a.out, static_cast<size_t>(r) * a.num_heads * D + e, f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+            a.ws_meta[2 * r] = -1;
+            a.ws_meta[2 * r + 1] = -1;
         }
     }
-    const int64_t P = s_total;
-    const int64_t W = min(static_cast<int64_t>(gridDim.x), P);
-    const int64_t item = blockIdx.x;
-    if (item >= W) return;  // uniform over the workgroup; no barrier follows for returned threads' waves
-    const int64_t start = item * P / W;
-    const int64_t end = (item + 1) * P / W;
-    const int64_t excl = wave_base + incl - local;
-    if (excl <= start && start < excl + local)
-    {
-        int64_t pb = excl;
-        int     r = r0;
-        for (;; ++r)
-        {
-            const int n = row_pages(a, r);
-            if (start < pb + n) break;
-            pb += n;
-        }
-        s_b0 = r;
-        s_pb0 = pb;
-    }
-    __syncthreads();
+    const int W = min(static_cast<int>(gridDim.x), P);
+    const int item = blockIdx.x;
+    if (item >= W) return;
+    const int start = static_cast<int>(static_cast<int64_t>(item) * P / W);
+    const int end = static_cast<int>(static_cast<int64_t>(item + 1) * P / W);
 
-    const int kvh = blockIdx.y * (nthreads >> 6) + wave;
+    // ---- row holding page `start`: second pass with an inclusive wave scan ------------------------------
+    int b0 = 0;
+    int pb0 = 0;
+    for (int r0 = 0; r0 < B; r0 += 64)
+    {
+        const int r = r0 + lane;
+        const int n = r < B ? row_pages(a, r) : 0;
+        int       incl = n;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1)
+        {
+            const int o = __shfl_up(incl, off, 64);
+            if (lane >= off) incl += o;
+        }
+        const uint64_t hit = __ballot(pb0 + incl - n <= start && start < pb0 + incl);
+        if (hit != 0)
+        {
+            const int l = __ffsll(static_cast<long long>(hit)) - 1;
+            b0 = r0 + l;
+            pb0 += uniform(__shfl(incl - n, l, 64));
+            break;
+        }
+        pb0 += uniform(__shfl(incl, 63, 64));
+    }
+
+    const int kvh = blockIdx.y * (static_cast<int>(blockDim.x) >> 6) + wave;
     if (kvh >= a.num_kv_heads) return;
     const int G = a.group;
     uint16_t* sv = s_v[wave];
@@ -332,17 +333,30 @@ void paged_decode_mfma(DecodeArgs a)
         v_head_scale = a.v_scale[kvh];
     }
 
-    int     b = s_b0;
-    int64_t pb = s_pb0;
-    int     nb = row_pages(a, b);
-    int64_t p = start;
-    while (p < end)
+    // ---- per-row state ------------------------------------------------------------------------------------
+    struct Row
     {
-        const int64_t seg_end = min(end, pb + nb);
-        const int     Lp = row_tokens(a, b);
+        int            b;
+        int            pb;  // global index of the row's first page
+        int            nb;  // pages in the row
+        int            Lp;  // attended tokens
+        const int32_t* table;
+    };
+    auto make_row = [&](int b, int pb)
+    {
+        return Row{b, pb, row_pages(a, b), row_tokens(a, b), a.block_table + static_cast<int64_t>(b) * a.max_blocks};
+    };
+    auto next_row = [&](const Row& r)
+    {
+        const int pb = r.pb + r.nb;
+        int       b = r.b + 1;
+        while (row_pages(a, b) == 0) ++b;
+        return make_row(b, pb);
+    };
 
-        // ---- Q of this row's group as MFMA B operands (column c = head, zero beyond the group) ----------
-        typename M::x8 qhi[KSTEPS], qlo[KSTEPS];
+    X8   qhi[KSTEPS], qlo[KSTEPS];
+    auto load_q = [&](int b)  // Q of row b's group as MFMA B operands (column c = head, zero beyond the group)
+    {
 #pragma unroll
         for (int j = 0; j < KSTEPS; ++j)
         {
@@ -351,269 +365,275 @@ void paged_decode_mfma(DecodeArgs a)
                 // q is stored in the MFMA input type: its 16 bytes are the operand
                 u32x4 w = u32x4{0u, 0u, 0u, 0u};
                 if (c < G)
-                    w = *reinterpret_cast<const u32x4*>(
-                        static_cast<const uint16_t*>(a.q) +
-                        (static_cast<size_t>(b) * a.num_heads + kvh * G + c) * D + dim_of<CT>(j, g));
-                qhi[j] = __builtin_bit_cast(typename M::x8, w);
+                    w = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.q) +
+                                                        (static_cast<size_t>(b) * a.num_heads + kvh * G + c) * D +
+                                                        dim_of<CT>(j, g));
+                qhi[j] = __builtin_bit_cast(X8, w);
                 qlo[j] = qhi[j];
-                continue;
-            }
-            float x[8];
-            if (c < G)
-                load_q8<QT>(a.q, (static_cast<size_t>(b) * a.num_heads + kvh * G + c) * D + dim_of<CT>(j, g), x);
-            else
-#pragma unroll
-                for (int e = 0; e < 8; ++e) x[e] = 0.0f;
-            uint32_t hi[8], lo[8];
-#pragma unroll
-            for (int e = 0; e < 8; ++e)
-            {
-                hi[e] = M::bits(x[e]);
-                lo[e] = NEED_LO ? M::bits(x[e] - M::value(hi[e])) : 0u;
-            }
-            qhi[j] = __builtin_bit_cast(typename M::x8, u32x4{hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16),
-                                                             hi[4] | (hi[5] << 16), hi[6] | (hi[7] << 16)});
-            qlo[j] = __builtin_bit_cast(typename M::x8, u32x4{lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16),
-                                                             lo[4] | (lo[5] << 16), lo[6] | (lo[7] << 16)});
-        }
-
-        float m_run = kNegInf;  // running max of head c (log2 domain), equal in the four lane groups
-        float l_run = 0.0f;     // this lane's share of the denominator (tokens 4g..4g+3 of each page)
-        f32x4 acc[NT];
-#pragma unroll
-        for (int n = 0; n < NT; ++n) acc[n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-
-        const int32_t* table = a.block_table + static_cast<int64_t>(b) * a.max_blocks;
-
-        // Issue the K and V loads of page pg (token c of the page, lane group g's dims) into registers.
-        auto load_page = [&](int pg, PageRegs<typename M::x8, KSTEPS>& r)
-        {
-            r.phys = table[pg];
-            r.ok = r.phys >= 0 && r.phys < a.num_blocks;  // uniform: a masked page is skipped
-            if (!r.ok) return;
-            const size_t row_c = (static_cast<size_t>(r.phys) * kBlockSize + c) * a.num_kv_heads + kvh;
-            if constexpr (kElemBytes<CT> == 2)
-            {
-                const char* kp = static_cast<const char*>(a.k_cache) + row_c * D * 2;
-                const char* vp = static_cast<const char*>(a.v_cache) + row_c * D * 2;
-#pragma unroll
-                for (int j = 0; j < KSTEPS; ++j)
-                {
-                    r.k[j] = __builtin_bit_cast(typename M::x8,
-                                                *reinterpret_cast<const u32x4*>(kp + dim_of<CT>(j, g) * 2));
-                    r.v[j] = *reinterpret_cast<const u32x4*>(vp + dim_of<CT>(j, g) * 2);
-                }
             }
             else
             {
-                const char* kp = static_cast<const char*>(a.k_cache) + row_c * D;
-                const char* vp = static_cast<const char*>(a.v_cache) + row_c * D;
+                float x[8];
+                if (c < G)
+                    load_q8<QT>(a.q, (static_cast<size_t>(b) * a.num_heads + kvh * G + c) * D + dim_of<CT>(j, g), x);
+                else
 #pragma unroll
-                for (int j = 0; j < KSTEPS; j += 2)
+                    for (int e = 0; e < 8; ++e) x[e] = 0.0f;
+                uint32_t hi[8], lo[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
                 {
-                    const u32x4 kw = *reinterpret_cast<const u32x4*>(kp + dim_of<CT>(j, g));
-                    const u32x4 vw = *reinterpret_cast<const u32x4*>(vp + dim_of<CT>(j, g));
-                    r.k[j] = __builtin_bit_cast(typename M::x8, codes_to_m<CT>(kw[0], kw[1]));
-                    r.k[j + 1] = __builtin_bit_cast(typename M::x8, codes_to_m<CT>(kw[2], kw[3]));
-                    r.v[j] = codes_to_m<CT>(vw[0], vw[1]);
-                    r.v[j + 1] = codes_to_m<CT>(vw[2], vw[3]);
+                    hi[e] = M::bits(x[e]);
+                    lo[e] = M::bits(x[e] - M::value(hi[e]));
                 }
+                qhi[j] = __builtin_bit_cast(X8, u32x4{hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16),
+                                                      hi[4] | (hi[5] << 16), hi[6] | (hi[7] << 16)});
+                qlo[j] = __builtin_bit_cast(X8, u32x4{lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16),
+                                                      lo[4] | (lo[5] << 16), lo[6] | (lo[7] << 16)});
             }
-        };
+        }
+    };
 
-        // Stage a loaded page: V rows into the wave's LDS tile, scores S^T = K Q^T into s.  Consumes r.k and
-        // r.v, so the next page can be loaded into r right after.
-        auto stage_page = [&](int pg, const PageRegs<typename M::x8, KSTEPS>& r, f32x4& s)
+    float m_run = kNegInf;  // running max of head c (log2 domain), equal in the four lane groups
+    float l_run = 0.0f;     // this lane's share of the denominator (tokens 4g..4g+3 of each page)
+    f32x4 acc[NT];
+
+    // Issue the K and V loads of physical page `phys` (token c of the page, lane group g's dims) into registers.
+    constexpr int NW = kElemBytes<CT> == 2 ? KSTEPS : KSTEPS / 2;
+    auto          load_page = [&](int phys, PageRegs<NW>& r)
+    {
+        r.phys = phys;
+        r.ok = phys >= 0 && phys < a.num_blocks;  // uniform: a masked page is skipped
+        if (!r.ok) return;
+        const size_t row_c = (static_cast<size_t>(phys) * kBlockSize + c) * a.num_kv_heads + kvh;
+        if constexpr (kElemBytes<CT> == 2)
         {
-            const int n_tok = min(kBlockSize, Lp - pg * kBlockSize);
-            // V[t = c], zero for slots past the row's last token
-            const bool tok_ok = c < n_tok;
+            const char* kp = static_cast<const char*>(a.k_cache) + row_c * D * 2;
+            const char* vp = static_cast<const char*>(a.v_cache) + row_c * D * 2;
 #pragma unroll
             for (int j = 0; j < KSTEPS; ++j)
             {
-                const u32x4 w = tok_ok ? r.v[j] : u32x4{0u, 0u, 0u, 0u};
-                *reinterpret_cast<u32x4*>(sv + lds_pos<D>(c, dim_of<CT>(j, g))) = w;
+                r.k[j] = *reinterpret_cast<const u32x4*>(kp + dim_of<CT>(j, g) * 2);
+                r.v[j] = *reinterpret_cast<const u32x4*>(vp + dim_of<CT>(j, g) * 2);
             }
-            // lane (c, g) gets tokens 4g + i of head c
-            s = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int j = 0; j < KSTEPS; ++j)
-            {
-                s = M::mma32(r.k[j], qhi[j], s);
-                if constexpr (NEED_LO) s = M::mma32(r.k[j], qlo[j], s);
-            }
-        };
-
-        // Online softmax of a staged page's scores and PV from its LDS tile.
-        auto finish_page = [&](int pg, int phys, f32x4 s)
-        {
-            const int n_tok = min(kBlockSize, Lp - pg * kBlockSize);
-            float ks[4], vs[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-            {
-                ks[i] = 1.0f;
-                vs[i] = 1.0f;
-            }
-            if constexpr (CT == I8)
-            {
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                {
-                    const size_t srow = (static_cast<size_t>(phys) * kBlockSize + 4 * g + i) * a.num_kv_heads + kvh;
-                    ks[i] = a.k_scale[srow];
-                    vs[i] = a.v_scale[srow];
-                }
-            }
-            float sc[4];
-            float mt = kNegInf;
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-            {
-                const bool ok = 4 * g + i < n_tok;
-                sc[i] = ok ? s[i] * ks[i] * kv_scale_log2 : kNegInf;
-                mt = fmaxf(mt, sc[i]);
-            }
-            mt = xor_max(mt);
-            const float m_new = fmaxf(m_run, mt);
-            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-            float       pv[4];
-            float       psum = 0.0f;
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-            {
-                const float pr = __builtin_amdgcn_exp2f(sc[i] - m_new);
-                psum += pr;
-                pv[i] = 4 * g + i < n_tok ? pr * vs[i] : 0.0f;
-            }
-            l_run = l_run * alpha + psum;
-            if (__any(m_new > m_run))
-            {
-#pragma unroll
-                for (int n = 0; n < NT; ++n) acc[n] *= alpha;
-            }
-            m_run = m_new;
-
-            // P^T as MFMA B operands (k = token 4g + i, column c = head), hi + lo parts
-            uint32_t ph[4], pl[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-            {
-                ph[i] = M::bits(pv[i]);
-                pl[i] = M::bits(pv[i] - M::value(ph[i]));
-            }
-            const typename M::x4 phi =
-                __builtin_bit_cast(typename M::x4, u32x2{ph[0] | (ph[1] << 16), ph[2] | (ph[3] << 16)});
-            const typename M::x4 plo =
-                __builtin_bit_cast(typename M::x4, u32x2{pl[0] | (pl[1] << 16), pl[2] | (pl[3] << 16)});
-
-            // LDS writes of this wave are complete before its reads below (in-order LDS queue of one wave);
-            // the fence keeps the compiler from moving the reads above the writes.
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-
-            // O^T[d, h] += V^T[d, t] P^T[t, h] over the 16 dims of each tile
-#pragma unroll
-            for (int n = 0; n < NT; ++n)
-            {
-                const uint32_t v0 = sv[lds_pos<D>(4 * g + 0, 16 * n + c)];
-                const uint32_t v1 = sv[lds_pos<D>(4 * g + 1, 16 * n + c)];
-                const uint32_t v2 = sv[lds_pos<D>(4 * g + 2, 16 * n + c)];
-                const uint32_t v3 = sv[lds_pos<D>(4 * g + 3, 16 * n + c)];
-                const typename M::x4 vt =
-                    __builtin_bit_cast(typename M::x4, u32x2{v0 | (v1 << 16), v2 | (v3 << 16)});
-                acc[n] = M::mma16(vt, phi, acc[n]);
-                acc[n] = M::mma16(vt, plo, acc[n]);
-            }
-            // the next page's LDS writes must not overtake these reads
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        };
-
-        const int pg0 = static_cast<int>(p - pb);
-        const int pg1 = static_cast<int>(seg_end - pb);
-        // Rolling prefetch: the loads of page pg + 1 are issued as soon as page pg's registers have been consumed
-        // (V written to LDS, K fed to the score MFMAs) and stay in flight during page pg's softmax and PV.
-#if FFKV_MFMA_ROLLING
-        PageRegs<typename M::x8, KSTEPS> r;
-        load_page(pg0, r);
-        for (int pg = pg0; pg < pg1; ++pg)
-        {
-            const bool ok = r.ok;
-            const int  phys = r.phys;
-            f32x4      s;
-            if (ok) stage_page(pg, r, s);
-            if (pg + 1 < pg1) load_page(pg + 1, r);
-            if (ok) finish_page(pg, phys, s);
         }
-#else
-        for (int pg = pg0; pg < pg1; ++pg)
+        else
         {
-            PageRegs<typename M::x8, KSTEPS> r;
-            load_page(pg, r);
-            if (!r.ok) continue;
-            f32x4 s;
-            stage_page(pg, r, s);
-            finish_page(pg, r.phys, s);
+            const char* kp = static_cast<const char*>(a.k_cache) + row_c * D;
+            const char* vp = static_cast<const char*>(a.v_cache) + row_c * D;
+#pragma unroll
+            for (int j = 0; j < KSTEPS; j += 2)
+            {
+                r.k[j / 2] = *reinterpret_cast<const u32x4*>(kp + dim_of<CT>(j, g));
+                r.v[j / 2] = *reinterpret_cast<const u32x4*>(vp + dim_of<CT>(j, g));
+            }
         }
-#endif
+    };
 
-        // ---- finish the row segment ---------------------------------------------------------------------
+    // Stage a loaded page: V rows into the wave's LDS tile, scores S^T = K Q^T into s.  Consumes r.k and r.v,
+    // so the next page can be loaded into r right after.
+    // K or V words of k-step j in the MFMA input type.
+    auto mword = [&](const u32x4* w, int j) -> u32x4
+    {
+        if constexpr (kElemBytes<CT> == 2)
+            return w[j];
+        else
+            return (j & 1) ? codes_to_m<CT>(w[j / 2][2], w[j / 2][3]) : codes_to_m<CT>(w[j / 2][0], w[j / 2][1]);
+    };
+    auto stage_page = [&](int n_tok, const PageRegs<NW>& r, f32x4& s)
+    {
+        const bool tok_ok = c < n_tok;  // V[t = c], zero for slots past the row's last token
+#pragma unroll
+        for (int j = 0; j < KSTEPS; ++j)
+        {
+            const u32x4 w = tok_ok ? mword(r.v, j) : u32x4{0u, 0u, 0u, 0u};
+            *reinterpret_cast<u32x4*>(sv + lds_pos<D>(c, dim_of<CT>(j, g))) = w;
+        }
+        s = f32x4{0.0f, 0.0f, 0.0f, 0.0f};  // lane (c, g) gets tokens 4g + i of head c
+#pragma unroll
+        for (int j = 0; j < KSTEPS; ++j)
+        {
+            const X8 kj = __builtin_bit_cast(X8, mword(r.k, j));
+            s = M::mma32(kj, qhi[j], s);
+            if constexpr (NEED_LO) s = M::mma32(kj, qlo[j], s);
+        }
+    };
+
+    // Online softmax of a staged page's scores and PV from its LDS tile.
+    auto finish_page = [&](int n_tok, int phys, f32x4 s)
+    {
+        float ks[4], vs[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+        {
+            ks[i] = 1.0f;
+            vs[i] = 1.0f;
+        }
+        if constexpr (CT == I8)
+        {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+            {
+                const size_t srow = (static_cast<size_t>(phys) * kBlockSize + 4 * g + i) * a.num_kv_heads + kvh;
+                ks[i] = a.k_scale[srow];
+                vs[i] = a.v_scale[srow];
+            }
+        }
+        float sc[4];
+        float mt = kNegInf;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+        {
+            const bool ok = 4 * g + i < n_tok;
+            sc[i] = ok ? s[i] * ks[i] * kv_scale_log2 : kNegInf;
+            mt = fmaxf(mt, sc[i]);
+        }
+        mt = xor_max(mt);
+        const float m_new = fmaxf(m_run, mt);
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+        float       pv[4];
+        float       psum = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+        {
+            const float pr = __builtin_amdgcn_exp2f(sc[i] - m_new);
+            psum += pr;
+            pv[i] = 4 * g + i < n_tok ? pr * vs[i] : 0.0f;
+        }
+        l_run = l_run * alpha + psum;
+        if (__any(m_new > m_run))
+        {
+#pragma unroll
+            for (int n = 0; n < NT; ++n) acc[n] *= alpha;
+        }
+        m_run = m_new;
+
+        // P^T as MFMA B operands (k = token 4g + i, column c = head), hi + lo parts
+        uint32_t ph[4], pl[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+        {
+            ph[i] = M::bits(pv[i]);
+            pl[i] = M::bits(pv[i] - M::value(ph[i]));
+        }
+        const typename M::x4 phi =
+            __builtin_bit_cast(typename M::x4, u32x2{ph[0] | (ph[1] << 16), ph[2] | (ph[3] << 16)});
+        const typename M::x4 plo =
+            __builtin_bit_cast(typename M::x4, u32x2{pl[0] | (pl[1] << 16), pl[2] | (pl[3] << 16)});
+
+        // LDS writes of this wave are complete before its reads below (in-order LDS queue of one wave);
+        // the fence keeps the compiler from moving the reads above the writes.
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+        // O^T[d, h] += V^T[d, t] P^T[t, h] over the 16 dims of each tile
+#pragma unroll
+        for (int n = 0; n < NT; ++n)
+        {
+            const uint32_t v0 = sv[lds_pos<D>(4 * g + 0, 16 * n + c)];
+            const uint32_t v1 = sv[lds_pos<D>(4 * g + 1, 16 * n + c)];
+            const uint32_t v2 = sv[lds_pos<D>(4 * g + 2, 16 * n + c)];
+            const uint32_t v3 = sv[lds_pos<D>(4 * g + 3, 16 * n + c)];
+            const typename M::x4 vt = __builtin_bit_cast(typename M::x4, u32x2{v0 | (v1 << 16), v2 | (v3 << 16)});
+            acc[n] = M::mma16(vt, phi, acc[n]);
+            acc[n] = M::mma16(vt, plo, acc[n]);
+        }
+        // the next page's LDS writes must not overtake these reads
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    };
+
+    // Write the segment [seg_start, seg_end) of row `row`: the output if it is the whole row, else a partial.
+    auto finish_segment = [&](const Row& row, int seg_start, int seg_end)
+    {
         const float l_tot = xor_sum(l_run);
         const int   h = kvh * G + c;
-        const bool  whole = p == pb && seg_end == pb + nb;
-        if (whole)
+        if (seg_start == row.pb && seg_end == row.pb + row.nb)
         {
             if (c < G)
             {
                 const float inv = l_tot > 0.0f ? v_head_scale / l_tot : 0.0f;
 #pragma unroll
                 for (int n = 0; n < NT; ++n)
-                    store_out4<QT>(a.out, (static_cast<size_t>(b) * a.num_heads + h) * D + 16 * n + 4 * g,
+                    store_out4<QT>(a.out, (static_cast<size_t>(row.b) * a.num_heads + h) * D + 16 * n + 4 * g,
                                    acc[n] * inv);
             }
         }
-        else
+        else if (c < G)
         {
-            const int64_t slot = item + b;
-            if (c < G)
-            {
-                float* dst = a.ws_acc + (slot * a.num_heads + h) * D;
+            const int64_t slot = static_cast<int64_t>(item) + row.b;
+            float*        dst = a.ws_acc + (slot * a.num_heads + h) * D;
 #pragma unroll
-                for (int n = 0; n < NT; ++n)
-                    *reinterpret_cast<f32x4*>(dst + 16 * n + 4 * g) = acc[n] * v_head_scale;
-                if (g == 0)
-                {
-                    a.ws_ml[(slot * a.num_heads + h) * 2] = m_run;
-                    a.ws_ml[(slot * a.num_heads + h) * 2 + 1] = l_tot;
-                }
+            for (int n = 0; n < NT; ++n)
+                *reinterpret_cast<f32x4*>(dst + 16 * n + 4 * g) = acc[n] * v_head_scale;
+            if (g == 0)
+            {
+                a.ws_ml[(slot * a.num_heads + h) * 2] = m_run;
+                a.ws_ml[(slot * a.num_heads + h) * 2 + 1] = l_tot;
             }
         }
         // the item holding a row's first page records which items cover the row
-        if (p == pb && blockIdx.y == 0 && wave == 0 && lane == 0)
+        if (seg_start == row.pb && blockIdx.y == 0 && wave == 0 && lane == 0)
         {
-            const int64_t last = pb + nb - 1;
+            const int64_t last = row.pb + row.nb - 1;
             const int64_t i_hi = ((last + 1) * W + P - 1) / P - 1;  // largest i with i*P/W <= last
-            a.ws_meta[2 * b] = static_cast<int32_t>(item);
-            a.ws_meta[2 * b + 1] = static_cast<int32_t>(i_hi);
+            a.ws_meta[2 * row.b] = item;
+            a.ws_meta[2 * row.b + 1] = static_cast<int32_t>(i_hi);
         }
+    };
 
-        p = seg_end;
-        if (p < end)
+    // ---- one flat pass over the item's pages ------------------------------------------------------------
+    // The loads of page p + 1 are issued as soon as page p's registers are consumed and stay in flight during
+    // page p's softmax and PV - across row boundaries too: the next row, its first block-table entry and its Q
+    // are fetched ahead, so a row change costs no extra memory round trip.
+    Row     cur = make_row(b0, pb0);
+    Row     nxt = cur;
+    int     nxt_phys0 = -1;
+    int     seg_start = start;
+    auto    begin_segment = [&]()
+    {
+        m_run = kNegInf;
+        l_run = 0.0f;
+#pragma unroll
+        for (int n = 0; n < NT; ++n) acc[n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        if (cur.pb + cur.nb < end)
         {
-            pb += nb;
-            ++b;
-            nb = row_pages(a, b);
-            while (nb == 0)
+            nxt = next_row(cur);
+            nxt_phys0 = nxt.table[0];
+        }
+    };
+    load_q(cur.b);
+    begin_segment();
+    PageRegs<NW> r;
+    load_page(cur.table[start - cur.pb], r);
+    for (int p = start; p < end; ++p)
+    {
+        const int  pg = static_cast<int>(p - cur.pb);
+        const int  n_tok = min(kBlockSize, cur.Lp - pg * kBlockSize);
+        const bool ok = r.ok;
+        const int  phys = r.phys;
+        const bool row_ends = p + 1 == cur.pb + cur.nb;
+        f32x4      s;
+        if (ok) stage_page(n_tok, r, s);
+        if (p + 1 < end)
+        {
+            load_page(row_ends ? nxt_phys0 : cur.table[pg + 1], r);
+            if (row_ends) load_q(nxt.b);  // the scores of page p have consumed Q
+        }
+        if (ok) finish_page(n_tok, phys, s);
+        if (row_ends || p + 1 == end)
+        {
+            finish_segment(cur, seg_start, p + 1);
+            if (p + 1 < end)
             {
-                ++b;
-                nb = row_pages(a, b);
+                cur = nxt;
+                seg_start = p + 1;
+                begin_segment();
             }
         }
     }
-
 }
 
 // Combine the partials of rows split over several work items.
@@ -631,10 +651,9 @@ __global__ __launch_bounds__(256) void paged_decode_mfma_merge(DecodeArgs a)
     __shared__ float s_m[4], s_l[4];
     __shared__ float s_o[4][D];
 
-    if (row_pages(a, b) == 0) return;  // zeroed by the decode kernel
     const int i_lo = a.ws_meta[2 * b];
     const int i_hi = a.ws_meta[2 * b + 1];
-    if (i_lo == i_hi) return;  // written by the decode kernel
+    if (i_lo == i_hi) return;  // one piece (written by the decode kernel) or no token (i_lo = i_hi = -1)
 
     float m = kNegInf, l = 0.0f, o[PER];
 #pragma unroll
