@@ -46,8 +46,7 @@ using u32x2 = uint32_t __attribute__((ext_vector_type(2)));
 
 constexpr float kNegInf = -__builtin_huge_valf();
 
-// MFMA input element type: bf16 for bf16 caches, f16 for f16, int8 and fp8 caches (codes of both quantized
-// formats are exact in f16).
+// MFMA input element type (bf16 or f16), chosen per cache and q type by kBF below.
 template <bool BF>
 struct MType;
 template <>
@@ -87,8 +86,14 @@ struct MType<false>
     }
 };
 
-template <int CT>
-constexpr bool kBF = CT == BF16;
+#ifndef FFKV_I8_BF16
+#define FFKV_I8_BF16 0  // int8 caches with bf16 q: bf16 MFMA (1) or f16 MFMA with q split in two (0)
+#endif
+
+// bf16 MFMA for bf16 caches, f16 for f16 caches.  Quantized codes are exact in both types (int8 has 8
+// significant bits, e4m3 4 bits and exponents -9..8), so they take q's type: then q needs no hi/lo split.
+template <int CT, int QT>
+constexpr bool kBF = CT == BF16 || (CT == FP8 && QT != F16) || (CT == I8 && QT == BF16 && FFKV_I8_BF16);
 template <int CT>
 constexpr int kElemBytes = (CT == I8 || CT == FP8) ? 1 : 2;
 
@@ -118,43 +123,53 @@ __device__ __forceinline__ void i8x4_to_f16(uint32_t w, uint32_t& lo, uint32_t& 
     hi = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, b) + bias);
 }
 
-// 4 OCP e4m3 codes -> 4 f16 values, exact: the code's magnitude bits shifted into the f16 exponent/mantissa
-// fields give 2^-8 times the value (normal and subnormal alike), fixed by one packed multiply by 256; the
-// NaN codes (S.1111.111) become f16 NaN.
-__device__ __forceinline__ void fp8x4_to_f16(uint32_t w, uint32_t& lo, uint32_t& hi)
+using bf16x2 = __bf16 __attribute__((ext_vector_type(2)));
+using f32x2 = float __attribute__((ext_vector_type(2)));
+
+// 4 int8 codes -> 4 bf16 values (two packed words), exact: sign-extending byte converts to f32, then packed
+// converts to bf16 (integers of magnitude <= 128 need 8 significant bits).
+__device__ __forceinline__ void i8x4_to_bf16(uint32_t w, uint32_t& lo, uint32_t& hi)
 {
-    const uint32_t x0 = __builtin_amdgcn_perm(0u, w, 0x010c000cu);  // [0, b0, 0, b1]
-    const uint32_t x1 = __builtin_amdgcn_perm(0u, w, 0x030c020cu);  // [0, b2, 0, b3]
-    const uint32_t f0 = (x0 & 0x80008000u) | ((x0 >> 1) & 0x3f803f80u);
-    const uint32_t f1 = (x1 & 0x80008000u) | ((x1 >> 1) & 0x3f803f80u);
-    const h2       k256 = h2{static_cast<_Float16>(256.0f), static_cast<_Float16>(256.0f)};
-    lo = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, f0) * k256);
-    hi = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, f1) * k256);
-    // a byte whose low 7 bits are all ones is NaN; (b & 0x7f) + 1 carries into bit 7 only for those
-    const uint32_t nan = ((w & 0x7f7f7f7fu) + 0x01010101u) & 0x80808080u;
-    if (__builtin_expect(nan != 0u, 0))
-    {
-        const uint32_t n0 = __builtin_amdgcn_perm(0u, nan, 0x010c000cu);  // NaN flags at bit 15 of each half
-        const uint32_t n1 = __builtin_amdgcn_perm(0u, nan, 0x030c020cu);
-        lo = (lo & ~(((n0 >> 15) & 0x00010001u) * 0x7fffu)) | (((n0 >> 15) & 0x00010001u) * 0x7e00u);
-        hi = (hi & ~(((n1 >> 15) & 0x00010001u) * 0x7fffu)) | (((n1 >> 15) & 0x00010001u) * 0x7e00u);
-    }
+    const float f0 = static_cast<float>(static_cast<int8_t>(w & 0xffu));
+    const float f1 = static_cast<float>(static_cast<int8_t>((w >> 8) & 0xffu));
+    const float f2 = static_cast<float>(static_cast<int8_t>((w >> 16) & 0xffu));
+    const float f3 = static_cast<float>(static_cast<int8_t>(w >> 24));
+    lo = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{f0, f1}, bf16x2));
+    hi = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{f2, f3}, bf16x2));
 }
 
-// 8 cache codes (one k-step of one lane) as 4 packed 16-bit MFMA words.  Quantized codes convert exactly.
-template <int CT>
+// 8 cache codes (one k-step of one lane) as 4 packed 16-bit MFMA words of type bf16 (BF) or f16; exact.  OCP
+// e4m3 codes use the gfx950 conversion instructions (scale 1: exact, NaN codes give NaN).
+template <int CT, bool BF>
 __device__ __forceinline__ u32x4 codes_to_m(uint32_t lo, uint32_t hi)
 {
     uint32_t r0, r1, r2, r3;
     if constexpr (CT == I8)
     {
-        i8x4_to_f16(lo, r0, r1);
-        i8x4_to_f16(hi, r2, r3);
+        if constexpr (BF)
+        {
+            i8x4_to_bf16(lo, r0, r1);
+            i8x4_to_bf16(hi, r2, r3);
+        }
+        else
+        {
+            i8x4_to_f16(lo, r0, r1);
+            i8x4_to_f16(hi, r2, r3);
+        }
+    }
+    else if constexpr (BF)
+    {
+        r0 = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 1.0f, false));
+        r1 = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 1.0f, true));
+        r2 = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 1.0f, false));
+        r3 = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 1.0f, true));
     }
     else
     {
-        fp8x4_to_f16(lo, r0, r1);
-        fp8x4_to_f16(hi, r2, r3);
+        r0 = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(lo, 1.0f, false));
+        r1 = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(lo, 1.0f, true));
+        r2 = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(hi, 1.0f, false));
+        r3 = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(hi, 1.0f, true));
     }
     return u32x4{r0, r1, r2, r3};
 }
@@ -185,23 +200,9 @@ __device__ __forceinline__ void store_out4(void* out, size_t i, f32x4 v)
     }
 }
 
-__device__ __forceinline__ int row_pages(const DecodeArgs& a, int b)
-{
-    int64_t L = static_cast<int64_t>(a.context_lens[b]) + 1;  // +1: the token appended this step (:320)
-    if (L > a.cap_tokens) L = a.cap_tokens;
-    if (L < 0) L = 0;
-    return static_cast<int>((L + kBlockSize - 1) / kBlockSize);
-}
-
-__device__ __forceinline__ int row_tokens(const DecodeArgs& a, int b)
-{
-    int64_t L = static_cast<int64_t>(a.context_lens[b]) + 1;
-    if (L > a.cap_tokens) L = a.cap_tokens;
-    return L < 0 ? 0 : static_cast<int>(L);
-}
-
-// Registers of one loaded page, as loaded: NW 16-byte words of K and of V per lane (one k-step each for 16-bit
-// caches, two for 8-bit codes, which convert when the page is staged so the loads stay in flight until then).
+// One page in flight: NW 16-byte words of K and of V per lane as loaded (one k-step each for 16-bit caches, two
+// for 8-bit codes, which convert when the page is staged so the loads stay in flight until then), the physical
+// block, and the row the page belongs to.
 template <int NW>
 struct PageRegs
 {
@@ -209,6 +210,12 @@ struct PageRegs
     u32x4 v[NW];
     int   phys;
     bool  ok;
+    int   b;   // row
+    int   pb;  // global index of the row's first page
+    int   nb;  // pages of the row
+    int   lp;  // attended tokens of the row
+    float ks;  // int8 caches: K and V scale of token c (lane c of each lane group)
+    float vs;
 };
 
 // Position (16-bit elements) of V[t][d] in a wave's LDS tile of 16 rows x D.  The 16-byte chunk d/8 of row t
@@ -246,62 +253,81 @@ __device__ __forceinline__ float xor_sum(float x)
 
 }  // namespace
 
-// Waves per SIMD the register budget is sized for, with one page's K/V in flight beside the page being finished:
-// 3 (168 registers) at D = 128, 4 (128) at D = 64, 2 at D = 256.
+#ifndef FFKV_MFMA_DEPTH16
+#define FFKV_MFMA_DEPTH16 2  // pages in flight per wave: 16-bit caches
+#endif
+#ifndef FFKV_MFMA_DEPTH_FP8
+#define FFKV_MFMA_DEPTH_FP8 2  // fp8 caches
+#endif
+#ifndef FFKV_MFMA_DEPTH_I8
+#define FFKV_MFMA_DEPTH_I8 1  // int8 caches
+#endif
+#ifndef FFKV_MFMA_WAVES128_16
+#define FFKV_MFMA_WAVES128_16 (FFKV_MFMA_DEPTH16 > 1 ? 2 : 3)
+#endif
+#ifndef FFKV_MFMA_WAVES128_FP8
+#define FFKV_MFMA_WAVES128_FP8 (FFKV_MFMA_DEPTH_FP8 > 1 ? 2 : 3)
+#endif
+#ifndef FFKV_MFMA_WAVES128_I8
+#define FFKV_MFMA_WAVES128_I8 2
+#endif
+
+// Pages whose K/V loads are in flight while a wave finishes the page before them.
+template <int CT>
+constexpr int kMfmaDepth =
+    kElemBytes<CT> == 2 ? FFKV_MFMA_DEPTH16 : (CT == FP8 ? FFKV_MFMA_DEPTH_FP8 : FFKV_MFMA_DEPTH_I8);
+
+// Waves per SIMD the register budget is sized for (168 registers at 3, 128 at 4, 256 at 2).
 template <int CT, int QT, int D>
-constexpr int kMfmaWaves = D == 256 ? 2 : (D == 128 ? 3 : 4);
+constexpr int kMfmaWaves =
+    D == 256 ? 2
+             : (D == 128 ? (kElemBytes<CT> == 2 ? FFKV_MFMA_WAVES128_16
+                                                : (CT == FP8 ? FFKV_MFMA_WAVES128_FP8 : FFKV_MFMA_WAVES128_I8))
+                         : (kMfmaDepth<CT> > 1 ? 3 : 4));
 
 // Work item i (blockIdx.x) of W (gridDim.x); KV heads blockIdx.y*NW .. +NW, one per wave.
 template <int CT, int QT, int D>
 __global__ __launch_bounds__(64 * FFKV_MFMA_MAX_WAVES) __attribute__((amdgpu_waves_per_eu(kMfmaWaves<CT, QT, D>, 8)))
 void paged_decode_mfma(DecodeArgs a)
 {
-    constexpr bool BF = kBF<CT>;
+    constexpr bool BF = kBF<CT, QT>;
     using M = MType<BF>;
     using X8 = typename M::x8;
     constexpr int  KSTEPS = D / 32;
     constexpr int  NT = D / 16;  // output tiles of 16 dims
     constexpr bool NEED_LO = !((QT == BF16 && BF) || (QT == F16 && !BF));
+    constexpr int  DEPTH = kMfmaDepth<CT>;
+    constexpr int  NW = kElemBytes<CT> == 2 ? KSTEPS : KSTEPS / 2;
 
     __shared__ uint16_t s_v[FFKV_MFMA_MAX_WAVES][kBlockSize * D];
 
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int c = lane & 15;  // MFMA column / row-in-tile index
-    const int g = lane >> 4;  // lane group
-    const int B = a.batch;
+    const int  lane = threadIdx.x & 63;
+    const int  wave = threadIdx.x >> 6;
+    const int  c = lane & 15;  // MFMA column / row-in-tile index
+    const int  g = lane >> 4;  // lane group
+    const int  B = a.batch;
     const bool first_wg = blockIdx.x == 0 && blockIdx.y == 0 && wave == 0;
 
-    // ---- total pages P, each wave on its own (64 rows per pass, no barriers) -----------------------------
-    // Rows without any token get a zero output and "no pieces" meta here; nothing else touches them.
-    // Page counts fit in 32 bits: the host bounds batch * pages per row.
-    int P = 0;
-    for (int r0 = 0; r0 < B; r0 += 64)
+    // ---- rows in windows of 64, one row per lane --------------------------------------------------------------
+    // A window holds rows w0 .. w0 + 63: lane l has row w0 + l's attended tokens, pages and first page (relative to
+    // the window's first page `base`); `total` is the window's page count.  Rows are located with ballots over a
+    // window instead of memory reads; a new window costs one vector load of context_lens.
+    struct Win
     {
-        const int r = r0 + lane;
-        const int n = r < B ? row_pages(a, r) : 0;
-        P += uniform(wave_sum(n));
-        if (first_wg && r < B && n == 0)
+        int w0, base, total;
+        int toks, n, excl;  // per lane
+    };
+    auto load_win = [&](int w0, int base)
+    {
+        const int r = w0 + lane;
+        int       t = 0;
+        if (r < B)
         {
-            for (int e = 0; e < a.num_heads * D; e += 4)
-                store_out4<QT>(a.out, static_cast<size_t>(r) * a.num_heads * D + e, f32x4{0.0f, 0.0f, 0.0f, 0.0f});
-            a.ws_meta[2 * r] = -1;
-            a.ws_meta[2 * r + 1] = -1;
+            int64_t L = static_cast<int64_t>(a.context_lens[r]) + 1;  // +1: the token appended this step (:320)
+            if (L > a.cap_tokens) L = a.cap_tokens;
+            t = L < 0 ? 0 : static_cast<int>(L);
         }
-    }
-    const int W = min(static_cast<int>(gridDim.x), P);
-    const int item = blockIdx.x;
-    if (item >= W) return;
-    const int start = static_cast<int>(static_cast<int64_t>(item) * P / W);
-    const int end = static_cast<int>(static_cast<int64_t>(item + 1) * P / W);
-
-    // ---- row holding page `start`: second pass with an inclusive wave scan ------------------------------
-    int b0 = 0;
-    int pb0 = 0;
-    for (int r0 = 0; r0 < B; r0 += 64)
-    {
-        const int r = r0 + lane;
-        const int n = r < B ? row_pages(a, r) : 0;
+        const int n = (t + kBlockSize - 1) / kBlockSize;
         int       incl = n;
 #pragma unroll
         for (int off = 1; off < 64; off <<= 1)
@@ -309,16 +335,32 @@ void paged_decode_mfma(DecodeArgs a)
             const int o = __shfl_up(incl, off, 64);
             if (lane >= off) incl += o;
         }
-        const uint64_t hit = __ballot(pb0 + incl - n <= start && start < pb0 + incl);
-        if (hit != 0)
+        return Win{w0, base, uniform(__shfl(incl, 63, 64)), t, n, incl - n};
+    };
+
+    // ---- total pages P (every wave on its own, no barriers) -------------------------------------------------
+    // Rows without any token get a zero output and "no pieces" meta here; nothing else touches them.
+    const Win win0 = load_win(0, 0);
+    int       P = 0;
+    for (Win w = win0;;)
+    {
+        if (first_wg && w.w0 + lane < B && w.n == 0)
         {
-            const int l = __ffsll(static_cast<long long>(hit)) - 1;
-            b0 = r0 + l;
-            pb0 += uniform(__shfl(incl - n, l, 64));
-            break;
+            const int r = w.w0 + lane;
+            for (int e = 0; e < a.num_heads * D; e += 4)
+                store_out4<QT>(a.out, static_cast<size_t>(r) * a.num_heads * D + e, f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+            a.ws_meta[2 * r] = -1;
+            a.ws_meta[2 * r + 1] = -1;
         }
-        pb0 += uniform(__shfl(incl, 63, 64));
+        P += w.total;
+        if (w.w0 + 64 >= B) break;
+        w = load_win(w.w0 + 64, P);
     }
+    const int W = min(static_cast<int>(gridDim.x), P);
+    const int item = blockIdx.x;
+    if (item >= W) return;
+    const int start = static_cast<int>(static_cast<int64_t>(item) * P / W);
+    const int end = static_cast<int>(static_cast<int64_t>(item + 1) * P / W);
 
     const int kvh = blockIdx.y * (static_cast<int>(blockDim.x) >> 6) + wave;
     if (kvh >= a.num_kv_heads) return;
@@ -333,25 +375,112 @@ void paged_decode_mfma(DecodeArgs a)
         v_head_scale = a.v_scale[kvh];
     }
 
-    // ---- per-row state ------------------------------------------------------------------------------------
-    struct Row
+    // ---- load cursor: the next page to load and its row -----------------------------------------------------
+    // The row's block-table entries come 64 at a time (lane l: entry tb + l); the next row with pages, and its
+    // first 64 entries, are fetched as soon as the cursor enters a row, so crossing into it costs no round trip.
+    struct LRow
     {
-        int            b;
-        int            pb;  // global index of the row's first page
-        int            nb;  // pages in the row
-        int            Lp;  // attended tokens
+        int            b, pb, nb, lp;
         const int32_t* table;
     };
-    auto make_row = [&](int b, int pb)
+    Win  win = win0;  // window of the most advanced row found so far
+    auto row_at = [&](int b)  // row b, which lies in `win`
     {
-        return Row{b, pb, row_pages(a, b), row_tokens(a, b), a.block_table + static_cast<int64_t>(b) * a.max_blocks};
+        const int l = b - win.w0;
+        return LRow{b, win.base + __builtin_amdgcn_readlane(win.excl, l), __builtin_amdgcn_readlane(win.n, l),
+                    __builtin_amdgcn_readlane(win.toks, l), a.block_table + static_cast<int64_t>(b) * a.max_blocks};
     };
-    auto next_row = [&](const Row& r)
+    auto find_page = [&](int x)  // row holding page x (x < P), moving `win` forward from its current window
     {
-        const int pb = r.pb + r.nb;
-        int       b = r.b + 1;
-        while (row_pages(a, b) == 0) ++b;
-        return make_row(b, pb);
+        for (;;)
+        {
+            const uint64_t hit = __ballot(win.w0 + lane < B && win.base + win.excl <= x && x < win.base + win.excl + win.n);
+            if (hit != 0) return row_at(win.w0 + __ffsll(static_cast<long long>(hit)) - 1);
+            win = load_win(win.w0 + 64, win.base + win.total);
+        }
+    };
+    auto next_row = [&](const LRow& r)  // the next row with pages (one exists)
+    {
+        for (;;)
+        {
+            const int      from = r.b + 1 - win.w0;  // lanes at or above `from` are candidates
+            const uint64_t m = __ballot(win.w0 + lane < B && win.n > 0 && lane >= from);
+            if (m != 0) return row_at(win.w0 + __ffsll(static_cast<long long>(m)) - 1);
+            win = load_win(win.w0 + 64, win.base + win.total);
+        }
+    };
+    auto load_tvec = [&](const LRow& r, int tb) { return tb + lane < r.nb ? r.table[tb + lane] : -1; };
+
+    LRow lrow = find_page(start);
+    int  tb = (start - lrow.pb) & ~63;
+    int  tvec = load_tvec(lrow, tb);
+    LRow lnxt = lrow;
+    int  ntvec = -1;
+    auto look_ahead = [&]()  // fetch the row after lrow if the item reaches it
+    {
+        if (lrow.pb + lrow.nb < end)
+        {
+            lnxt = next_row(lrow);
+            ntvec = load_tvec(lnxt, 0);
+        }
+    };
+    look_ahead();
+    int lp = start;  // next page to load
+
+    // Issue the K and V loads of page lp into r and advance the cursor.
+    auto load_next = [&](PageRegs<NW>& r)
+    {
+        if (lp == lrow.pb + lrow.nb)
+        {
+            lrow = lnxt;
+            tb = 0;
+            tvec = ntvec;
+            look_ahead();
+        }
+        const int pg = lp - lrow.pb;
+        if (pg - tb >= 64)
+        {
+            tb += 64;
+            tvec = load_tvec(lrow, tb);
+        }
+        const int phys = __builtin_amdgcn_readlane(tvec, pg - tb);
+        ++lp;
+        r.b = lrow.b;
+        r.pb = lrow.pb;
+        r.nb = lrow.nb;
+        r.lp = lrow.lp;
+        r.phys = phys;
+        r.ok = phys >= 0 && phys < a.num_blocks;  // uniform: a masked page is skipped
+        if (!r.ok) return;
+        const size_t row_c = (static_cast<size_t>(phys) * kBlockSize + c) * a.num_kv_heads + kvh;
+        if constexpr (CT == I8)
+        {
+            // issued before the page's K/V: waiting for them never waits for a later load
+            r.ks = a.k_scale[row_c];
+            r.vs = a.v_scale[row_c];
+        }
+        if constexpr (kElemBytes<CT> == 2)
+        {
+            const char* kp = static_cast<const char*>(a.k_cache) + row_c * D * 2;
+            const char* vp = static_cast<const char*>(a.v_cache) + row_c * D * 2;
+#pragma unroll
+            for (int j = 0; j < KSTEPS; ++j)
+            {
+                r.k[j] = *reinterpret_cast<const u32x4*>(kp + dim_of<CT>(j, g) * 2);
+                r.v[j] = *reinterpret_cast<const u32x4*>(vp + dim_of<CT>(j, g) * 2);
+            }
+        }
+        else
+        {
+            const char* kp = static_cast<const char*>(a.k_cache) + row_c * D;
+            const char* vp = static_cast<const char*>(a.v_cache) + row_c * D;
+#pragma unroll
+            for (int j = 0; j < KSTEPS; j += 2)
+            {
+                r.k[j / 2] = *reinterpret_cast<const u32x4*>(kp + dim_of<CT>(j, g));
+                r.v[j / 2] = *reinterpret_cast<const u32x4*>(vp + dim_of<CT>(j, g));
+            }
+        }
     };
 
     X8   qhi[KSTEPS], qlo[KSTEPS];
@@ -398,48 +527,17 @@ void paged_decode_mfma(DecodeArgs a)
     float l_run = 0.0f;     // this lane's share of the denominator (tokens 4g..4g+3 of each page)
     f32x4 acc[NT];
 
-    // Issue the K and V loads of physical page `phys` (token c of the page, lane group g's dims) into registers.
-    constexpr int NW = kElemBytes<CT> == 2 ? KSTEPS : KSTEPS / 2;
-    auto          load_page = [&](int phys, PageRegs<NW>& r)
-    {
-        r.phys = phys;
-        r.ok = phys >= 0 && phys < a.num_blocks;  // uniform: a masked page is skipped
-        if (!r.ok) return;
-        const size_t row_c = (static_cast<size_t>(phys) * kBlockSize + c) * a.num_kv_heads + kvh;
-        if constexpr (kElemBytes<CT> == 2)
-        {
-            const char* kp = static_cast<const char*>(a.k_cache) + row_c * D * 2;
-            const char* vp = static_cast<const char*>(a.v_cache) + row_c * D * 2;
-#pragma unroll
-            for (int j = 0; j < KSTEPS; ++j)
-            {
-                r.k[j] = *reinterpret_cast<const u32x4*>(kp + dim_of<CT>(j, g) * 2);
-                r.v[j] = *reinterpret_cast<const u32x4*>(vp + dim_of<CT>(j, g) * 2);
-            }
-        }
-        else
-        {
-            const char* kp = static_cast<const char*>(a.k_cache) + row_c * D;
-            const char* vp = static_cast<const char*>(a.v_cache) + row_c * D;
-#pragma unroll
-            for (int j = 0; j < KSTEPS; j += 2)
-            {
-                r.k[j / 2] = *reinterpret_cast<const u32x4*>(kp + dim_of<CT>(j, g));
-                r.v[j / 2] = *reinterpret_cast<const u32x4*>(vp + dim_of<CT>(j, g));
-            }
-        }
-    };
-
-    // Stage a loaded page: V rows into the wave's LDS tile, scores S^T = K Q^T into s.  Consumes r.k and r.v,
-    // so the next page can be loaded into r right after.
     // K or V words of k-step j in the MFMA input type.
     auto mword = [&](const u32x4* w, int j) -> u32x4
     {
         if constexpr (kElemBytes<CT> == 2)
             return w[j];
         else
-            return (j & 1) ? codes_to_m<CT>(w[j / 2][2], w[j / 2][3]) : codes_to_m<CT>(w[j / 2][0], w[j / 2][1]);
+            return (j & 1) ? codes_to_m<CT, BF>(w[j / 2][2], w[j / 2][3]) : codes_to_m<CT, BF>(w[j / 2][0], w[j / 2][1]);
     };
+
+    // Stage a loaded page: V rows into the wave's LDS tile, scores S^T = K Q^T into s.  Consumes r.k and r.v,
+    // so the next page can be loaded into r right after.
     auto stage_page = [&](int n_tok, const PageRegs<NW>& r, f32x4& s)
     {
         const bool tok_ok = c < n_tok;  // V[t = c], zero for slots past the row's last token
@@ -459,8 +557,8 @@ void paged_decode_mfma(DecodeArgs a)
         }
     };
 
-    // Online softmax of a staged page's scores and PV from its LDS tile.
-    auto finish_page = [&](int n_tok, int phys, f32x4 s)
+    // Online softmax of a staged page's scores and PV from its LDS tile.  tks / tvs: int8 scales of token c.
+    auto finish_page = [&](int n_tok, float tks, float tvs, f32x4 s)
     {
         float ks[4], vs[4];
 #pragma unroll
@@ -472,11 +570,10 @@ void paged_decode_mfma(DecodeArgs a)
         if constexpr (CT == I8)
         {
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < 4; ++i)  // token 4g + i's scales sit in lane 4g + i
             {
-                const size_t srow = (static_cast<size_t>(phys) * kBlockSize + 4 * g + i) * a.num_kv_heads + kvh;
-                ks[i] = a.k_scale[srow];
-                vs[i] = a.v_scale[srow];
+                ks[i] = __shfl(tks, 4 * g + i, 64);
+                vs[i] = __shfl(tvs, 4 * g + i, 64);
             }
         }
         float sc[4];
@@ -545,25 +642,26 @@ void paged_decode_mfma(DecodeArgs a)
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     };
 
-    // Write the segment [seg_start, seg_end) of row `row`: the output if it is the whole row, else a partial.
-    auto finish_segment = [&](const Row& row, int seg_start, int seg_end)
+    // Write the segment [seg_start, seg_end) of row b (pages pb .. pb + nb - 1): the output if it is the whole row,
+    // else a partial.
+    auto finish_segment = [&](int b, int pb, int nb, int seg_start, int seg_end)
     {
         const float l_tot = xor_sum(l_run);
         const int   h = kvh * G + c;
-        if (seg_start == row.pb && seg_end == row.pb + row.nb)
+        if (seg_start == pb && seg_end == pb + nb)
         {
             if (c < G)
             {
                 const float inv = l_tot > 0.0f ? v_head_scale / l_tot : 0.0f;
 #pragma unroll
                 for (int n = 0; n < NT; ++n)
-                    store_out4<QT>(a.out, (static_cast<size_t>(row.b) * a.num_heads + h) * D + 16 * n + 4 * g,
+                    store_out4<QT>(a.out, (static_cast<size_t>(b) * a.num_heads + h) * D + 16 * n + 4 * g,
                                    acc[n] * inv);
             }
         }
         else if (c < G)
         {
-            const int64_t slot = static_cast<int64_t>(item) + row.b;
+            const int64_t slot = static_cast<int64_t>(item) + b;
             float*        dst = a.ws_acc + (slot * a.num_heads + h) * D;
 #pragma unroll
             for (int n = 0; n < NT; ++n)
@@ -575,64 +673,62 @@ void paged_decode_mfma(DecodeArgs a)
             }
         }
         // the item holding a row's first page records which items cover the row
-        if (seg_start == row.pb && blockIdx.y == 0 && wave == 0 && lane == 0)
+        if (seg_start == pb && blockIdx.y == 0 && wave == 0 && lane == 0)
         {
-            const int64_t last = row.pb + row.nb - 1;
+            const int64_t last = pb + nb - 1;
             const int64_t i_hi = ((last + 1) * W + P - 1) / P - 1;  // largest i with i*P/W <= last
-            a.ws_meta[2 * row.b] = item;
-            a.ws_meta[2 * row.b + 1] = static_cast<int32_t>(i_hi);
+            a.ws_meta[2 * b] = item;
+            a.ws_meta[2 * b + 1] = static_cast<int32_t>(i_hi);
         }
     };
 
-    // ---- one flat pass over the item's pages ------------------------------------------------------------
-    // The loads of page p + 1 are issued as soon as page p's registers are consumed and stay in flight during
-    // page p's softmax and PV - across row boundaries too: the next row, its first block-table entry and its Q
-    // are fetched ahead, so a row change costs no extra memory round trip.
-    Row     cur = make_row(b0, pb0);
-    Row     nxt = cur;
-    int     nxt_phys0 = -1;
-    int     seg_start = start;
-    auto    begin_segment = [&]()
-    {
-        m_run = kNegInf;
-        l_run = 0.0f;
+    // ---- pages start .. end - 1, DEPTH of them in flight ---------------------------------------------------
+    // Page p sits in r[(p - start) % DEPTH]; right after it is staged, page p + DEPTH is loaded into the same
+    // registers, and stays in flight while p is finished.
+    load_q(lrow.b);
+    int seg_start = start;
 #pragma unroll
-        for (int n = 0; n < NT; ++n) acc[n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-        if (cur.pb + cur.nb < end)
-        {
-            nxt = next_row(cur);
-            nxt_phys0 = nxt.table[0];
-        }
-    };
-    load_q(cur.b);
-    begin_segment();
-    PageRegs<NW> r;
-    load_page(cur.table[start - cur.pb], r);
-    for (int p = start; p < end; ++p)
+    for (int n = 0; n < NT; ++n) acc[n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    PageRegs<NW> r[DEPTH];
+#pragma unroll
+    for (int sl = 0; sl < DEPTH; ++sl)
+        if (start + sl < end) load_next(r[sl]);
+
+    auto step = [&]<int S>(int p)
     {
-        const int  pg = static_cast<int>(p - cur.pb);
-        const int  n_tok = min(kBlockSize, cur.Lp - pg * kBlockSize);
-        const bool ok = r.ok;
-        const int  phys = r.phys;
-        const bool row_ends = p + 1 == cur.pb + cur.nb;
-        f32x4      s;
-        if (ok) stage_page(n_tok, r, s);
-        if (p + 1 < end)
-        {
-            load_page(row_ends ? nxt_phys0 : cur.table[pg + 1], r);
-            if (row_ends) load_q(nxt.b);  // the scores of page p have consumed Q
-        }
-        if (ok) finish_page(n_tok, phys, s);
+        PageRegs<NW>& cur = r[S];
+        const int     b = cur.b, pb = cur.pb, nb = cur.nb;
+        const float   tks = cur.ks, tvs = cur.vs;
+        const bool    ok = cur.ok;
+        const int     n_tok = min(kBlockSize, cur.lp - (p - pb) * kBlockSize);
+        const bool    row_ends = p + 1 == pb + nb;
+        f32x4         s;
+        if (ok) stage_page(n_tok, cur, s);
+        // The scores of page p have consumed Q: a new row's Q is loaded now, ahead of page p + DEPTH's K/V when
+        // page p + 1 is already in flight (loads complete in issue order for the wait counter).
+        if constexpr (DEPTH > 1)
+            if (row_ends && p + 1 < end) load_q(r[(S + 1) % DEPTH].b);
+        if (p + DEPTH < end) load_next(cur);
+        if constexpr (DEPTH == 1)
+            if (row_ends && p + 1 < end) load_q(cur.b);
+        if (ok) finish_page(n_tok, tks, tvs, s);
         if (row_ends || p + 1 == end)
         {
-            finish_segment(cur, seg_start, p + 1);
-            if (p + 1 < end)
-            {
-                cur = nxt;
-                seg_start = p + 1;
-                begin_segment();
-            }
+            finish_segment(b, pb, nb, seg_start, p + 1);
+            seg_start = p + 1;
+            m_run = kNegInf;
+            l_run = 0.0f;
+#pragma unroll
+            for (int n = 0; n < NT; ++n) acc[n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
         }
+    };
+    for (int p = start; p < end; p += DEPTH)
+    {
+        step.template operator()<0>(p);
+        if constexpr (DEPTH > 1)
+            if (p + 1 < end) step.template operator()<1 % DEPTH>(p + 1);
+        if constexpr (DEPTH > 2)
+            if (p + 2 < end) step.template operator()<2 % DEPTH>(p + 2);
     }
 }
 
