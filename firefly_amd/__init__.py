@@ -57,6 +57,11 @@ def _load() -> ctypes.CDLL:
     lib.ffkv_paged_decode.restype = i32
     lib.ffkv_paged_decode.argtypes = [vp, vp, i32, vp, vp, i32, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32,
                                       i32, f32, vp, sz, vp]
+    lib.ffkv_rope.restype = i32
+    lib.ffkv_rope.argtypes = [vp, vp, i32, vp, i32, i32, i32, i32, i32, ctypes.c_float, vp]
+    lib.ffkv_rope_append.restype = i32
+    lib.ffkv_rope_append.argtypes = [vp, vp, vp, i32, vp, vp, i32, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32,
+                                     i32, ctypes.c_float, vp]
     lib.ffkv_last_error.restype = ctypes.c_char_p
     lib.ffkv_last_error.argtypes = []
     lib.ffkv_version.restype = ctypes.c_char_p
@@ -117,6 +122,28 @@ def append_kv_cache(k, v, k_cache, v_cache, block_table, context_lens=None, k_sc
     check(lib.ffkv_append(_ptr(k), _ptr(v), torch_dtype_code(k), _ptr(k_cache), _ptr(v_cache),
                           torch_dtype_code(k_cache), _ptr(k_scale), _ptr(v_scale), _ptr(block_table),
                           _ptr(context_lens), B, S, Hkv, D, BLOCK_SIZE, max_blocks, N, _stream(stream)))
+
+
+def apply_rope(q, k, context_lens=None, theta: float = 1e6, stream=None) -> None:
+    """Rotary embedding of ``q`` ``[B, S, Hq, D]`` (or None) and ``k`` ``[B, S, Hkv, D]`` in place
+    (``ffkv_rope``; the reference's ``kernels::apply_rope``)."""
+    B, S, Hkv, D = k.shape
+    Hq = 0 if q is None else q.shape[2]
+    check(lib.ffkv_rope(_ptr(q), _ptr(k), torch_dtype_code(k), _ptr(context_lens), B, S, Hq, Hkv, D, float(theta),
+                        _stream(stream)))
+
+
+def rope_append_kv_cache(q, k, v, k_cache, v_cache, block_table, context_lens=None, theta: float = 1e6,
+                         k_scale=None, v_scale=None, num_blocks: int | None = None, stream=None) -> None:
+    """``apply_rope(q, k)`` then ``append_kv_cache(k, v, ...)`` in one kernel (``ffkv_rope_append``)."""
+    B, S, Hkv, D = k.shape
+    Hq = 0 if q is None else q.shape[2]
+    max_blocks = block_table.shape[-1]
+    N = k_cache.shape[0] if num_blocks is None else num_blocks
+    check(lib.ffkv_rope_append(_ptr(q), _ptr(k), _ptr(v), torch_dtype_code(k), _ptr(k_cache), _ptr(v_cache),
+                               torch_dtype_code(k_cache), _ptr(k_scale), _ptr(v_scale), _ptr(block_table),
+                               _ptr(context_lens), B, S, Hq, Hkv, D, BLOCK_SIZE, max_blocks, N, float(theta),
+                               _stream(stream)))
 
 
 def decode_workspace_bytes(batch: int, num_heads: int, head_dim: int, max_blocks: int,

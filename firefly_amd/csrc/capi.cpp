@@ -214,6 +214,66 @@ int ffkv_append(const void* k_src, const void* v_src, int src_dtype, void* k_cac
     return ok();
 }
 
+int ffkv_rope(void* q, void* k, int dtype, const int32_t* context_lens, int batch, int seq_len, int num_heads,
+              int num_kv_heads, int head_dim, float rope_theta, void* stream)
+{
+    return ffkv_rope_append(q, k, nullptr, dtype, nullptr, nullptr, dtype, nullptr, nullptr, nullptr, context_lens,
+                            batch, seq_len, num_heads, num_kv_heads, head_dim, FFKV_BLOCK_SIZE, 0, 0, rope_theta,
+                            stream);
+}
+
+int ffkv_rope_append(void* q, void* k, const void* v, int src_dtype, void* k_cache, void* v_cache, int cache_dtype,
+                     float* k_scale, float* v_scale, const int32_t* block_table, const int32_t* context_lens,
+                     int batch, int seq_len, int num_heads, int num_kv_heads, int head_dim, int block_size,
+                     int max_blocks, int num_blocks, float rope_theta, void* stream)
+{
+    const bool append = k_cache != nullptr || v_cache != nullptr;
+    if (block_size != FFKV_BLOCK_SIZE) return fail(FFKV_ERR_UNSUPPORTED, "block_size must be 16, got %d", block_size);
+    if (!is_act(src_dtype)) return fail(FFKV_ERR_UNSUPPORTED, "unsupported q/k/v dtype %d", src_dtype);
+    if (append && !is_cache(cache_dtype)) return fail(FFKV_ERR_UNSUPPORTED, "unsupported cache dtype %d", cache_dtype);
+    if (!head_dim_ok(head_dim)) return fail(FFKV_ERR_UNSUPPORTED, "head_dim must be 64, 128 or 256, got %d", head_dim);
+    if (q == nullptr) num_heads = 0;
+    if (batch < 0 || seq_len < 0 || num_heads < 0 || num_kv_heads <= 0 || max_blocks < 0 || num_blocks < 0)
+        return fail(FFKV_ERR_INVALID_ARGUMENT, "negative size (batch %d seq_len %d heads %d kv_heads %d max_blocks %d "
+                    "num_blocks %d)", batch, seq_len, num_heads, num_kv_heads, max_blocks, num_blocks);
+    if (!(rope_theta > 0.0f) || rope_theta == __builtin_huge_valf())
+        return fail(FFKV_ERR_INVALID_ARGUMENT, "rope_theta must be positive and finite, got %g",
+                    static_cast<double>(rope_theta));
+    if (batch == 0 || seq_len == 0) return ok();
+    if (!k) return fail(FFKV_ERR_INVALID_ARGUMENT, "null k pointer");
+    if (append && (!v || !k_cache || !v_cache || !block_table))
+        return fail(FFKV_ERR_INVALID_ARGUMENT, "null v, cache or block_table pointer");
+    if (append && quantized(cache_dtype) && (!k_scale || !v_scale))
+        return fail(FFKV_ERR_INVALID_ARGUMENT, "quantized cache needs k_scale and v_scale");
+    if ((q && !aligned16(q)) || !aligned16(k) || (append && (!aligned16(v) || !aligned16(k_cache) ||
+                                                             !aligned16(v_cache))))
+        return fail(FFKV_ERR_INVALID_ARGUMENT, "q, k, v and cache pointers must be 16-byte aligned");
+
+    ffkv::RopeArgs a{};
+    a.q = q;
+    a.k = k;
+    a.v = v;
+    a.k_cache = append ? k_cache : nullptr;
+    a.v_cache = append ? v_cache : nullptr;
+    a.k_scale = k_scale;
+    a.v_scale = v_scale;
+    a.block_table = block_table;
+    a.context_lens = context_lens;
+    a.src_dtype = src_dtype;
+    a.cache_dtype = cache_dtype;
+    a.batch = batch;
+    a.seq_len = seq_len;
+    a.num_heads = num_heads;
+    a.num_kv_heads = num_kv_heads;
+    a.head_dim = head_dim;
+    a.max_blocks = max_blocks;
+    a.num_blocks = num_blocks;
+    a.theta = rope_theta;
+    hipError_t e = ffkv::launch_rope_append(a, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, append ? "rope_append launch" : "rope launch");
+    return ok();
+}
+
 size_t ffkv_decode_workspace_bytes(int batch, int num_heads, int head_dim, int max_blocks, int max_context_len)
 {
     if (batch <= 0 || num_heads <= 0 || head_dim <= 0) return 0;

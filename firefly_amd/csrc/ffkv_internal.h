@@ -30,6 +30,29 @@ struct AppendArgs
     int            num_blocks;
 };
 
+struct RopeArgs
+{
+    void*          q;  // [B, S, Hq, D] rotated in place, or null (num_heads = 0)
+    void*          k;  // [B, S, Hkv, D] rotated in place
+    const void*    v;  // [B, S, Hkv, D], appended with k (when k_cache is set)
+    void*          k_cache;  // null: rotate only
+    void*          v_cache;
+    float*         k_scale;
+    float*         v_scale;
+    const int32_t* block_table;
+    const int32_t* context_lens;
+    int            src_dtype;
+    int            cache_dtype;
+    int            batch;
+    int            seq_len;
+    int            num_heads;
+    int            num_kv_heads;
+    int            head_dim;
+    int            max_blocks;
+    int            num_blocks;
+    float          theta;
+};
+
 struct DecodeArgs
 {
     const void*    q;
@@ -61,6 +84,7 @@ struct DecodeArgs
 };
 
 hipError_t launch_append(const AppendArgs& a, hipStream_t stream);
+hipError_t launch_rope_append(const RopeArgs& a, hipStream_t stream);  // rotate q/k, then append when k_cache set
 hipError_t launch_decode(const DecodeArgs& a, hipStream_t stream);       // generic kernel (any cache dtype)
 hipError_t launch_decode_mfma(const DecodeArgs& a, hipStream_t stream);  // matrix-core kernel (16-bit/8-bit caches)
 

@@ -125,6 +125,28 @@ void append(const Tensor& k, const Tensor& v, Tensor& kc, Tensor& vc, float* ks,
     report(rc, "append_kv_cache failed");
 }
 
+void rope_append(Tensor& q, Tensor& k, const Tensor* v, Tensor* kc, Tensor* vc, float* ks, float* vs,
+                 const int* block_table, const int* context_lens, int max_blocks, float theta)
+{
+    const bool has_q = q.data() != nullptr;
+    if (k.shape().size() != 4 || (has_q && (q.shape().size() != 4 || q.shape()[0] != k.shape()[0] ||
+                                            q.shape()[1] != k.shape()[1] || q.shape()[3] != k.shape()[3] ||
+                                            q.dtype() != k.dtype())))
+        return fail("apply_rope: q must be [B, S, Hq, D] and k [B, S, Hkv, D] of one dtype");
+    if (v != nullptr && (v->shape() != k.shape() || v->dtype() != k.dtype() || kc->shape().size() != 4 ||
+                         vc->shape() != kc->shape() || kc->shape()[2] != k.shape()[2] ||
+                         kc->shape()[3] != k.shape()[3]))
+        return fail("rope_append_kv_cache: v must match k and the caches be [num_blocks, 16, Hkv, D]");
+    const int rc = ffkv_rope_append(
+        has_q ? q.data() : nullptr, k.data(), v ? v->data() : nullptr, code(k.dtype()), kc ? kc->data() : nullptr,
+        vc ? vc->data() : nullptr, kc ? code(kc->dtype()) : code(k.dtype()), ks, vs,
+        reinterpret_cast<const int32_t*>(block_table), reinterpret_cast<const int32_t*>(context_lens),
+        static_cast<int>(k.shape()[0]), static_cast<int>(k.shape()[1]), has_q ? static_cast<int>(q.shape()[2]) : 0,
+        static_cast<int>(k.shape()[2]), static_cast<int>(k.shape()[3]), kc ? static_cast<int>(kc->shape()[1]) : 16,
+        max_blocks, kc ? static_cast<int>(kc->shape()[0]) : 0, theta, t_stream);
+    report(rc, v ? "rope_append_kv_cache failed" : "apply_rope failed");
+}
+
 }  // namespace
 
 void        set_default_stream(hipStream_t stream) { t_stream = stream; }
@@ -161,6 +183,27 @@ void append_kv_cache(const Tensor& k, const Tensor& v, Tensor& k_cache, Tensor& 
 {
     append(k, v, k_cache, v_cache, k_scale.data_as<float>(), v_scale.data_as<float>(), block_table, context_lens,
            max_blocks);
+}
+
+void apply_rope(Tensor& q, Tensor& k, int head_dim, int seq_len, float theta, const int* context_lens)
+{
+    if (k.shape().size() != 4 || k.shape()[3] != head_dim || k.shape()[1] != seq_len)
+        return fail("apply_rope: k must be [B, seq_len, Hkv, head_dim]");
+    rope_append(q, k, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, context_lens, 0, theta);
+}
+
+void rope_append_kv_cache(Tensor& q, Tensor& k, const Tensor& v, Tensor& k_cache, Tensor& v_cache,
+                          const int* block_table, const int* context_lens, int max_blocks, float theta)
+{
+    rope_append(q, k, &v, &k_cache, &v_cache, nullptr, nullptr, block_table, context_lens, max_blocks, theta);
+}
+
+void rope_append_kv_cache(Tensor& q, Tensor& k, const Tensor& v, Tensor& k_cache, Tensor& v_cache, Tensor& k_scale,
+                          Tensor& v_scale, const int* block_table, const int* context_lens, int max_blocks,
+                          float theta)
+{
+    rope_append(q, k, &v, &k_cache, &v_cache, k_scale.data_as<float>(), v_scale.data_as<float>(), block_table,
+                context_lens, max_blocks, theta);
 }
 
 }  // namespace firefly::kernels

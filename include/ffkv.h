@@ -2,9 +2,9 @@
  * ffkv.h - C ABI of the MI355X (gfx950) paged KV-cache path.
  *
  * This is the drop-in boundary for Firefly's paged KV-cache hot path: appending new K/V tokens into
- * block-table-addressed pages (optionally quantizing to int8 or OCP fp8 e4m3) and PagedAttention decode
- * (GQA, split-K, online softmax).  Plain pointers and sizes only; no C++ or HIP types appear here, so
- * ctypes / cgo / JNI / N-API callers can bind it directly.  `stream` is a hipStream_t passed as void*
+ * block-table-addressed pages (optionally quantizing to int8 or OCP fp8 e4m3, optionally fused with the rotary
+ * embedding of q and k) and PagedAttention decode (GQA, split-K, online softmax).  Plain pointers and sizes
+ * only; no C++ or HIP types appear here, so ctypes / cgo / JNI / N-API callers can bind it directly.  `stream` is a hipStream_t passed as void*
  * (NULL = the legacy default stream).
  *
  * Layout contract (identical to the reference):
@@ -99,13 +99,42 @@ FFKV_API size_t ffkv_decode_workspace_bytes(int batch, int num_heads, int head_d
  * size of at most 16; head_dim 64, 128 or 256; q, out, cache and workspace pointers 16-byte aligned.  Rows are
  * split over the context and the pieces merged; the partials live in `workspace` (ffkv_decode_workspace_bytes;
  * any initial contents), or, when workspace is NULL, in stream-ordered memory the library allocates and frees on
- * `stream`.  Calls sharing one workspace must not overlap in time (use one workspace per stream).  Rows whose context_lens[b] + 1 exceeds max_context_len are truncated to it.
+ * `stream`.  Calls sharing one workspace must not overlap in time (use one workspace per stream).  Rows whose
+ * context_lens[b] + 1 exceeds max_context_len are truncated to it.
  */
 FFKV_API int ffkv_paged_decode(const void* q, void* out, int qo_dtype, const void* k_cache, const void* v_cache,
                       int cache_dtype, const float* k_scale, const float* v_scale, const int32_t* block_table,
                       const int32_t* context_lens, int batch, int num_heads, int num_kv_heads, int head_dim,
                       int block_size, int max_blocks, int num_blocks, int max_context_len, float scale,
                       void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Rotary position embedding of q and k in place.  Replaces `firefly::kernels::apply_rope(q, k, head_dim, seq_len,
+ * theta, context_lens)` (include/firefly/kernels.h:68, src/kernels/rope.cu:22-137, called at
+ * src/model/qwen_model.cu:136).  q [batch, seq_len, num_heads, head_dim] and k [batch, seq_len, num_kv_heads,
+ * head_dim] share `dtype` (F32, F16 or BF16); q may be NULL (then num_heads is ignored).  Token t of row b is
+ * at position context_lens[b] + t (t when context_lens is NULL).  Rotate-half form: pair i (dims i, i + D/2) is
+ * rotated by pos * inv_freq_i with inv_freq_i = theta^(-2i/head_dim):
+ *     x_i' = x_i cos - x_{i+D/2} sin,   x_{i+D/2}' = x_{i+D/2} cos + x_i sin.
+ * inv_freq, cos and sin are evaluated in double precision and rounded once to fp32, the angle is one fp32
+ * product of float(pos) and inv_freq, the rotation uses separately rounded fp32 products and sums, and the
+ * result is rounded to nearest even in `dtype`.  q and k must be 16-byte aligned.
+ */
+FFKV_API int ffkv_rope(void* q, void* k, int dtype, const int32_t* context_lens, int batch, int seq_len, int num_heads,
+                       int num_kv_heads, int head_dim, float rope_theta, void* stream);
+
+/*
+ * ffkv_rope followed by ffkv_append of the rotated k (as rounded in src_dtype) and v, in one pass: the
+ * reference's `kernels::apply_rope` + append launch pair (src/model/qwen_model.cu:136-143) fused, saving a
+ * launch and a read of k.  Arguments as for ffkv_rope and ffkv_append; q may be NULL.  k is rotated in place
+ * (as apply_rope leaves it) and v is only read.  The page contents are bit-identical to ffkv_rope followed by
+ * ffkv_append.
+ */
+FFKV_API int ffkv_rope_append(void* q, void* k, const void* v, int src_dtype, void* k_cache, void* v_cache,
+                              int cache_dtype, float* k_scale, float* v_scale, const int32_t* block_table,
+                              const int32_t* context_lens, int batch, int seq_len, int num_heads, int num_kv_heads,
+                              int head_dim, int block_size, int max_blocks, int num_blocks, float rope_theta,
+                              void* stream);
 
 /* Message describing the last error returned on the calling thread ("" if none). */
 FFKV_API const char* ffkv_last_error(void);

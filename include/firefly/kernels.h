@@ -3,8 +3,10 @@
 // Drop-in for the KV-cache part of include/firefly/kernels.h (reference, :8-9 and :70-84):
 //   set_default_stream / get_default_stream   thread-local stream every launch below uses
 //   attention(...)                            paged decode when kv_cache_block_table != nullptr
+//   apply_rope(...)                           rotary embedding of q and k (reference :68)
 // plus the append the reference keeps private to its model (src/model/qwen_model.cu:21-47, launched at
-// :138-143), exported here, and quantized-cache overloads of both.  Each forwards to the C ABI in ffkv.h.
+// :138-143), exported here, a fused rope + append, and quantized-cache overloads.  Each forwards to the C ABI
+// in ffkv.h.
 //
 // Like the reference, the functions return void and report failures on std::cerr
 // (src/kernels/attention.cu:487-491); last_error() additionally returns the message of the calling thread's
@@ -56,5 +58,27 @@ FIREFLY_API void append_kv_cache(const Tensor& k, const Tensor& v, Tensor& k_cac
 // head) or fp8 e4m3 cache (k_scale/v_scale read, fp32 [Hkv] per head).
 FIREFLY_API void append_kv_cache(const Tensor& k, const Tensor& v, Tensor& k_cache, Tensor& v_cache, Tensor& k_scale,
                                  Tensor& v_scale, const int* block_table, const int* context_lens, int max_blocks);
+
+/**
+ * @brief Rotary position embedding of q and k in place (reference include/firefly/kernels.h:68,
+ * src/kernels/rope.cu:22-137).
+ *
+ * q [B, S, Hq, D] and k [B, S, Hkv, D] of one dtype (F32/F16/BF16); head_dim must equal D and seq_len S.  Token t
+ * of row b is at position context_lens[b] + t (context_lens == nullptr: t); rotate-half pairs (i, i + D/2) turn by
+ * position * theta^(-2i/D).  An empty q (no data) rotates k only.
+ */
+FIREFLY_API void apply_rope(Tensor& q, Tensor& k, int head_dim, int seq_len, float theta, const int* context_lens);
+
+/**
+ * @brief apply_rope(q, k, ...) then append_kv_cache(k, v, ...) in one kernel: the pair the reference's model runs
+ * back to back (src/model/qwen_model.cu:136-143).  Pages are bit-identical to the two separate calls.
+ */
+FIREFLY_API void rope_append_kv_cache(Tensor& q, Tensor& k, const Tensor& v, Tensor& k_cache, Tensor& v_cache,
+                                      const int* block_table, const int* context_lens, int max_blocks, float theta);
+
+// Quantizing variant (k_scale/v_scale as for the quantizing append_kv_cache).
+FIREFLY_API void rope_append_kv_cache(Tensor& q, Tensor& k, const Tensor& v, Tensor& k_cache, Tensor& v_cache,
+                                      Tensor& k_scale, Tensor& v_scale, const int* block_table,
+                                      const int* context_lens, int max_blocks, float theta);
 
 }  // namespace firefly::kernels

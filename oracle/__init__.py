@@ -34,6 +34,8 @@ def _load() -> ctypes.CDLL:
     lib.ffo_paged_decode_f64.restype = i32
     lib.ffo_paged_decode_f64.argtypes = [vp, i32, vp, vp, i32, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32,
                                          i32, f32, vp]
+    lib.ffo_rope.restype = i32
+    lib.ffo_rope.argtypes = [vp, i32, vp, i32, i32, i32, i32, f32]
     lib.ffo_quant_i8_row.restype = f32
     lib.ffo_quant_i8_row.argtypes = [vp, i32, vp]
     for name, src, dst in [("f32_to_bf16", vp, vp), ("f32_to_f16", vp, vp), ("f32_to_e4m3", vp, vp),
@@ -117,6 +119,17 @@ def append(k_src, v_src, src_dtype, k_cache, v_cache, cache_dtype, block_table, 
                         _p(k_scale), _p(v_scale), _p(bt), _p(ctx), B, S, Hkv, D, 16, bt.shape[-1], N)
     if rc != 0:
         raise ValueError(f"ffo_append returned {rc}")
+
+
+def rope(x, dtype, context_lens, theta):
+    """Rotated copy of x [B, S, H, D] (storage array of `dtype`)."""
+    y = np.array(x, copy=True, order="C")
+    B, S, H, D = y.shape
+    ctx = _c(context_lens, np.int32)
+    rc = lib.ffo_rope(_p(y), dtype, _p(ctx), B, S, H, D, theta)
+    if rc != 0:
+        raise ValueError(f"ffo_rope returned {rc}")
+    return y
 
 
 def paged_decode(q, qo_dtype, k_cache, v_cache, cache_dtype, block_table, context_lens, k_scale=None,

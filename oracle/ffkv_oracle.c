@@ -13,6 +13,7 @@
  *                                            (:323-325, :372-399), 8-lane-chunk dot plus a 16-lane shuffle tree
  *                                            (:345-369), final merge of the eight states (:403-446)
  *   dispatch src/kernels/attention.cu:455-458 scale = 1/sqrtf(head_dim)
+ *   rope     src/kernels/rope.cu:22-137       rotate-half pairs (i, i + D/2), pos = ctx + t, theta^(-2i/D)
  *
  * Extensions the reference does not have (it is fp16-only and leaves bad addressing undefined), restated
  * from the specification in include/ffkv.h: bf16/fp32 storage, int8 and OCP fp8 e4m3 quantization, skipped
@@ -27,6 +28,8 @@
  *                 saturation edge pinned by the OCP spec values (448, 464, inf, NaN).
  *   int8 quant    torch.round (half-even) on the closed form, golden fixtures.
  *   ffo_append    closed-form address formula in numpy, whole-pool sentinel check, append->gather round trip.
+ *   ffo_rope      torch float64 rotate_half formulation (q*cos + rotate_half(q)*sin), position 0 = identity,
+ *                 unit vectors give (cos, sin), pair norms preserved, q.k depends only on the position offset.
  *   ffo_paged_decode  float64 closed form (ffo_paged_decode_f64), torch SDPA on gathered K/V with repeated
  *                 heads, special cases (one token, constant K, dominant logit, GQA symmetry, shared prefix).
  */
@@ -318,6 +321,55 @@ int ffo_append(const void* k_src, const void* v_src, int src_dtype, void* k_cach
     }
     free(tmp);
     free(qtmp);
+    return 0;
+}
+
+/* ----------------------------------------------------------------------------------------------------------
+ * Rotary embedding.  Restates rope_kernel_optimized (src/kernels/rope.cu:22-137): position pos = ctx[b] + t
+ * (t when ctx is null, :36-37), pair i = (dims i, i + D/2) rotated by pos * theta^(-2i/D) (:74-77) in the
+ * rotate-half form lo' = lo*c - hi*s, hi' = hi*c + lo*s (:84-91), written back in the tensor's dtype.  The
+ * arithmetic is the one include/ffkv.h specifies (the reference's fast-math powf/cosf/sinf are not
+ * reproducible): inv_freq, cos and sin in double rounded once to float, the angle one float product, the
+ * rotation float products and sums (built with -ffp-contract=off, so each is rounded separately).
+ * -------------------------------------------------------------------------------------------------------- */
+
+int ffo_rope(void* x, int dtype, const int32_t* context_lens, int batch, int seq_len, int heads, int head_dim,
+             float theta)
+{
+    if (!is_act_dtype(dtype)) return ERR_UNSUPPORTED;
+    if (batch < 0 || seq_len < 0 || heads < 0 || head_dim <= 0 || (head_dim & 1)) return ERR_ARG;
+    if (!(theta > 0.0f)) return ERR_ARG;
+    if (batch == 0 || seq_len == 0 || heads == 0) return 0;
+    if (!x) return ERR_ARG;
+    const int half = head_dim / 2;
+    float*    cs = (float*)malloc(sizeof(float) * 2 * (size_t)half);
+    for (int b = 0; b < batch; ++b)
+    {
+        for (int t = 0; t < seq_len; ++t)
+        {
+            long long pos = (long long)(context_lens ? context_lens[b] : 0) + t; /* rope.cu:36-37 */
+            for (int i = 0; i < half; ++i)
+            {
+                float inv_freq = (float)pow((double)theta, -2.0 * i / head_dim); /* :74-76 */
+                float ang = (float)pos * inv_freq;                              /* :77 */
+                cs[2 * i] = (float)cos((double)ang);
+                cs[2 * i + 1] = (float)sin((double)ang);
+            }
+            for (int h = 0; h < heads; ++h)
+            {
+                size_t base = (((size_t)b * seq_len + t) * heads + h) * (size_t)head_dim;
+                for (int i = 0; i < half; ++i)
+                {
+                    float c = cs[2 * i], s = cs[2 * i + 1];
+                    float lo = load_act(x, dtype, base + i), hi = load_act(x, dtype, base + i + half);
+                    float lc = lo * c, hs = hi * s, hc = hi * c, ls = lo * s;
+                    store_act(x, dtype, base + i, lc - hs);   /* :84-85 */
+                    store_act(x, dtype, base + i + half, hc + ls);
+                }
+            }
+        }
+    }
+    free(cs);
     return 0;
 }
 

@@ -41,6 +41,10 @@ int ffo_append(const void* k_src, const void* v_src, int src_dtype, void* k_cach
                float* k_scale, float* v_scale, const int32_t* block_table, const int32_t* context_lens, int batch,
                int seq_len, int num_kv_heads, int head_dim, int block_size, int max_blocks, int num_blocks);
 
+/* Rotary embedding in place of x [batch, seq_len, heads, head_dim] (src/kernels/rope.cu:22-137); see ffkv_rope. */
+int ffo_rope(void* x, int dtype, const int32_t* context_lens, int batch, int seq_len, int heads, int head_dim,
+             float theta);
+
 /*
  * Restatement of paged_attention_kernel (src/kernels/attention.cu:291-447): per (sequence, query head), eight
  * interleaved token groups each run an online softmax in fp32, then the eight states are merged.  Output is

@@ -6,6 +6,7 @@
 // from kernels::last_error().
 #include <cstring>
 #include <string>
+#include <vector>
 
 #include "firefly/kernels.h"
 
@@ -46,6 +47,44 @@ int kas_append_then_decode(void* q, void* k_new, void* v_new, void* k_cache, voi
         kernels::append_kv_cache(tk, tv, kc, vc, block_table, context_lens, max_blocks);
         if (!kernels::last_error().empty()) return g_err = kernels::last_error(), -1;
         kernels::attention(tq, kc, vc, to, const_cast<int*>(block_table), Hkv, 1, max_blocks, context_lens);
+    }
+    if (!kernels::last_error().empty()) return g_err = kernels::last_error(), -1;
+    return 0;
+}
+
+// The reference's per-layer sequence with the rotary embedding (src/model/qwen_model.cu:136-143): fused == 1
+// calls kernels::rope_append_kv_cache, else kernels::apply_rope then kernels::append_kv_cache.  q [B,S,Hq,D],
+// k/v [B,S,Hkv,D] in dtype qd (q and k rotated in place); caches [N,16,Hkv,D] in dtype cd.
+int kas_rope_append(void* q, void* k_new, void* v_new, void* k_cache, void* v_cache, void* k_scale, void* v_scale,
+                    const int* block_table, const int* context_lens, int B, int S, int Hq, int Hkv, int D, int N,
+                    int max_blocks, int qd, int cd, float theta, int fused, void* stream)
+{
+    kernels::set_default_stream(static_cast<hipStream_t>(stream));
+    const DType qt = static_cast<DType>(qd), ct = static_cast<DType>(cd);
+    Tensor      tq = Tensor::from_external(q, {B, S, Hq, D}, qt, Device::GPU);
+    Tensor      tk = Tensor::from_external(k_new, {B, S, Hkv, D}, qt, Device::GPU);
+    Tensor      tv = Tensor::from_external(v_new, {B, S, Hkv, D}, qt, Device::GPU);
+    Tensor      kc = Tensor::from_external(k_cache, {N, 16, Hkv, D}, ct, Device::GPU);
+    Tensor      vc = Tensor::from_external(v_cache, {N, 16, Hkv, D}, ct, Device::GPU);
+    const bool  quant = ct == DType::I8 || ct == DType::FP8_E4M3;
+    std::vector<int64_t> sshape = ct == DType::I8 ? std::vector<int64_t>{N, 16, Hkv} : std::vector<int64_t>{Hkv};
+    Tensor      ks = Tensor::from_external(k_scale, sshape, DType::F32, Device::GPU);
+    Tensor      vs = Tensor::from_external(v_scale, sshape, DType::F32, Device::GPU);
+    if (fused)
+    {
+        if (quant)
+            kernels::rope_append_kv_cache(tq, tk, tv, kc, vc, ks, vs, block_table, context_lens, max_blocks, theta);
+        else
+            kernels::rope_append_kv_cache(tq, tk, tv, kc, vc, block_table, context_lens, max_blocks, theta);
+    }
+    else
+    {
+        kernels::apply_rope(tq, tk, D, S, theta, context_lens);
+        if (!kernels::last_error().empty()) return g_err = kernels::last_error(), -1;
+        if (quant)
+            kernels::append_kv_cache(tk, tv, kc, vc, ks, vs, block_table, context_lens, max_blocks);
+        else
+            kernels::append_kv_cache(tk, tv, kc, vc, block_table, context_lens, max_blocks);
     }
     if (!kernels::last_error().empty()) return g_err = kernels::last_error(), -1;
     return 0;

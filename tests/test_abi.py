@@ -101,3 +101,40 @@ def test_workspace_bytes_monotone(ff):
     assert ff.decode_workspace_bytes(8, 28, 128, 16, 0) > 0
     assert ff.decode_workspace_bytes(0, 28, 128, 2049, 0) == 0
 
+
+
+def _rope_append(ff, **kw):
+    a = dict(q=16, k=16, v=16, src_dtype=ff.DTYPE_BF16, k_cache=16, v_cache=16, cache_dtype=ff.DTYPE_BF16,
+             k_scale=None, v_scale=None, block_table=16, context_lens=None, batch=1, seq_len=1, num_heads=32,
+             num_kv_heads=8, head_dim=128, block_size=16, max_blocks=4, num_blocks=4, theta=1e6, stream=None)
+    a.update(kw)
+    return ff.lib.ffkv_rope_append(*a.values())
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(block_size=32), -2),
+    (dict(head_dim=96), -2),
+    (dict(src_dtype=3), -2),
+    (dict(cache_dtype=7), -2),
+    (dict(batch=-1), -1),
+    (dict(num_kv_heads=0), -1),
+    (dict(theta=0.0), -1),
+    (dict(theta=float("nan")), -1),
+    (dict(theta=float("inf")), -1),
+    (dict(k=None), -1),
+    (dict(v=None), -1),
+    (dict(block_table=None), -1),
+    (dict(cache_dtype=3), -1),        # int8 cache without scales
+    (dict(q=18), -1),                 # misaligned
+])
+def test_rope_append_rejects(ff, kw, code):
+    assert _rope_append(ff, **kw) == code
+    assert ff.lib.ffkv_last_error().decode() != ""
+
+
+def test_rope_rejects_and_empty(ff):
+    assert ff.lib.ffkv_rope(16, 16, ff.DTYPE_BF16, None, 1, 1, 32, 8, 96, 1e6, None) == -2
+    assert ff.lib.ffkv_rope(16, None, ff.DTYPE_BF16, None, 1, 1, 32, 8, 128, 1e6, None) == -1
+    assert ff.lib.ffkv_rope(16, 16, ff.DTYPE_BF16, None, 0, 1, 32, 8, 128, 1e6, None) == 0
+    assert ff.lib.ffkv_rope(None, 16, ff.DTYPE_BF16, None, 1, 0, 0, 8, 128, 1e6, None) == 0
+    assert _rope_append(ff, batch=0, k=None, v=None, q=None) == 0

@@ -25,6 +25,8 @@ def shim(ff):
     vp, i = ctypes.c_void_p, ctypes.c_int
     lib.kas_append_then_decode.restype = i
     lib.kas_append_then_decode.argtypes = [vp] * 7 + [i, vp, vp, vp] + [i] * 9 + [vp]
+    lib.kas_rope_append.restype = i
+    lib.kas_rope_append.argtypes = [vp] * 7 + [vp, vp] + [i] * 9 + [ctypes.c_float, i, vp]
     lib.kas_last_error.restype = ctypes.c_char_p
     lib.kas_prefill_branch_rejected.restype = i
     return lib
@@ -70,3 +72,44 @@ def test_cxx_api_append_then_decode(shim, gpu, act, kv, tol):
 @pytest.mark.gpu
 def test_cxx_api_prefill_branch_reports_error(shim, gpu):
     assert shim.kas_prefill_branch_rejected() == 1
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("act,kv", [("bf16", "bf16"), ("f16", "i8"), ("bf16", "fp8")])
+@pytest.mark.parametrize("fused", [1, 0])
+def test_cxx_api_rope_then_append(shim, gpu, act, kv, fused):
+    """kernels::rope_append_kv_cache and kernels::apply_rope + kernels::append_kv_cache: rotated q/k and pages
+    bit-identical to the checker (rope, then append of the rotated k)."""
+    import torch
+
+    import gpu_util as gu
+
+    theta = 1e6
+    c = cases.make_case(80, 3, 8, 2, 128, [0, 40, 777], act=act, kv=kv, S=5)
+    rng = np.random.default_rng(81)
+    qn = cases.encode(rng.standard_normal((c.B, c.S, c.Hq, c.D), dtype=np.float32), c.act)
+    q, kn, vn = gu.to_dev(qn, c.act, gpu), gu.to_dev(c.k_new, c.act, gpu), gu.to_dev(c.v_new, c.act, gpu)
+    dk, dv = gu.to_dev(c.k_pool, c.kv, gpu), gu.to_dev(c.v_pool, c.kv, gpu)
+    dks = None if c.k_scale is None else torch.from_numpy(c.k_scale.copy()).to(gpu)
+    dvs = None if c.v_scale is None else torch.from_numpy(c.v_scale.copy()).to(gpu)
+    bt, ctx = torch.from_numpy(c.block_table).to(gpu), torch.from_numpy(c.ctx).to(gpu)
+    p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+    rc = shim.kas_rope_append(p(q), p(kn), p(vn), p(dk), p(dv), p(dks), p(dvs), p(bt), p(ctx), c.B, c.S, c.Hq,
+                              c.Hkv, c.D, c.num_blocks, c.max_blocks, c.act, c.kv, theta, fused,
+                              torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert rc == 0, shim.kas_last_error()
+    q_ref, k_ref = O.rope(qn, c.act, c.ctx, theta), O.rope(c.k_new, c.act, c.ctx, theta)
+    host = (lambda t: gu.to_host(t, np.uint16)) if q.dtype in (torch.float16, torch.bfloat16) else \
+        (lambda t: t.cpu().numpy())
+    assert np.array_equal(host(q), q_ref) and np.array_equal(host(kn), k_ref)
+    rk, rv = c.k_pool.copy(), c.v_pool.copy()
+    rks = None if c.k_scale is None else c.k_scale.copy()
+    rvs = None if c.v_scale is None else c.v_scale.copy()
+    O.append(k_ref, c.v_new, c.act, rk, rv, c.kv, c.block_table, c.ctx, rks, rvs)
+    conv = (lambda t: gu.to_host(t, np.uint16)) if dk.dtype in (torch.float16, torch.bfloat16) else \
+        (lambda t: t.cpu().numpy())
+    assert np.array_equal(conv(dk).view(np.uint8), rk.view(np.uint8))
+    assert np.array_equal(conv(dv).view(np.uint8), rv.view(np.uint8))
+    if c.kv == O.DTYPE_I8:
+        assert np.array_equal(dks.cpu().numpy().view(np.uint32), rks.view(np.uint32))
