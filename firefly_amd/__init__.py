@@ -57,6 +57,9 @@ def _load() -> ctypes.CDLL:
     lib.ffkv_paged_decode.restype = i32
     lib.ffkv_paged_decode.argtypes = [vp, vp, i32, vp, vp, i32, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32,
                                       i32, f32, vp, sz, vp]
+    lib.ffkv_paged_prefill.restype = i32
+    lib.ffkv_paged_prefill.argtypes = [vp, vp, i32, vp, vp, i32, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32,
+                                       i32, i32, ctypes.c_float, vp]
     lib.ffkv_rope.restype = i32
     lib.ffkv_rope.argtypes = [vp, vp, i32, vp, i32, i32, i32, i32, i32, ctypes.c_float, vp]
     lib.ffkv_rope_append.restype = i32
@@ -122,6 +125,26 @@ def append_kv_cache(k, v, k_cache, v_cache, block_table, context_lens=None, k_sc
     check(lib.ffkv_append(_ptr(k), _ptr(v), torch_dtype_code(k), _ptr(k_cache), _ptr(v_cache),
                           torch_dtype_code(k_cache), _ptr(k_scale), _ptr(v_scale), _ptr(block_table),
                           _ptr(context_lens), B, S, Hkv, D, BLOCK_SIZE, max_blocks, N, _stream(stream)))
+
+
+def paged_prefill(q, k_cache, v_cache, block_table, context_lens, out=None, k_scale=None, v_scale=None,
+                  max_context_len: int = 0, scale: float = 0.0, num_blocks: int | None = None, stream=None):
+    """Causal prefill attention (``ffkv_paged_prefill``): ``q`` ``[B, S, Hq, D]`` over the paged cache (queries at
+    ``context_lens[b] + t``), or, with ``block_table=None``, over contiguous ``k_cache``/``v_cache``
+    ``[B, S, Hkv, D]``.  Returns ``out`` ``[B, S, Hq * D]``."""
+    import torch
+
+    B, S, Hq, D = q.shape
+    Hkv = k_cache.shape[2]
+    if out is None:
+        out = torch.empty((B, S, Hq * D), dtype=q.dtype, device=q.device)
+    max_blocks = 0 if block_table is None else block_table.shape[-1]
+    N = (k_cache.shape[0] if num_blocks is None else num_blocks) if block_table is not None else 0
+    check(lib.ffkv_paged_prefill(_ptr(q), _ptr(out), torch_dtype_code(q), _ptr(k_cache), _ptr(v_cache),
+                                 torch_dtype_code(k_cache), _ptr(k_scale), _ptr(v_scale), _ptr(block_table),
+                                 _ptr(context_lens), B, S, Hq, Hkv, D, BLOCK_SIZE, max_blocks, N, max_context_len,
+                                 float(scale), _stream(stream)))
+    return out
 
 
 def apply_rope(q, k, context_lens=None, theta: float = 1e6, stream=None) -> None:

@@ -214,6 +214,67 @@ int ffkv_append(const void* k_src, const void* v_src, int src_dtype, void* k_cac
     return ok();
 }
 
+int ffkv_paged_prefill(const void* q, void* out, int qo_dtype, const void* k_cache, const void* v_cache,
+                       int cache_dtype, const float* k_scale, const float* v_scale, const int32_t* block_table,
+                       const int32_t* context_lens, int batch, int seq_len, int num_heads, int num_kv_heads,
+                       int head_dim, int block_size, int max_blocks, int num_blocks, int max_context_len, float scale,
+                       void* stream)
+{
+    const bool paged = block_table != nullptr;
+    if (block_size != FFKV_BLOCK_SIZE) return fail(FFKV_ERR_UNSUPPORTED, "block_size must be 16, got %d", block_size);
+    if (!is_act(qo_dtype)) return fail(FFKV_ERR_UNSUPPORTED, "unsupported q/out dtype %d", qo_dtype);
+    if (!is_cache(cache_dtype) || cache_dtype == FFKV_DTYPE_F32)
+        return fail(FFKV_ERR_UNSUPPORTED, "prefill supports F16, BF16, I8 and FP8_E4M3 caches, got dtype %d",
+                    cache_dtype);
+    if (!head_dim_ok(head_dim)) return fail(FFKV_ERR_UNSUPPORTED, "head_dim must be 64, 128 or 256, got %d", head_dim);
+    if (batch < 0 || seq_len < 0 || num_heads <= 0 || num_kv_heads <= 0 || (paged && (max_blocks < 0 || num_blocks < 0)))
+        return fail(FFKV_ERR_INVALID_ARGUMENT, "bad size (batch %d seq_len %d heads %d kv_heads %d max_blocks %d "
+                    "num_blocks %d)", batch, seq_len, num_heads, num_kv_heads, max_blocks, num_blocks);
+    if (num_heads % num_kv_heads != 0)
+        return fail(FFKV_ERR_INVALID_ARGUMENT, "num_heads %d is not a multiple of num_kv_heads %d", num_heads,
+                    num_kv_heads);
+    if (batch > 65535 || num_kv_heads > 65535)
+        return fail(FFKV_ERR_UNSUPPORTED, "batch and num_kv_heads must be <= 65535");
+    if (static_cast<int64_t>(seq_len) * (num_heads / num_kv_heads) > INT32_MAX - 64)
+        return fail(FFKV_ERR_UNSUPPORTED, "seq_len * group too large");
+    if (batch == 0 || seq_len == 0) return ok();
+    if (!q || !out || !k_cache || !v_cache || (paged && !context_lens))
+        return fail(FFKV_ERR_INVALID_ARGUMENT, "null q, out, cache or context_lens pointer");
+    if (!paged && cache_dtype == FFKV_DTYPE_I8)
+        return fail(FFKV_ERR_UNSUPPORTED, "int8 K/V need a block table (their scales are per page slot)");
+    if (quantized(cache_dtype) && (!k_scale || !v_scale))
+        return fail(FFKV_ERR_INVALID_ARGUMENT, "quantized cache needs k_scale and v_scale");
+    if (!aligned16(q) || !aligned16(out) || !aligned16(k_cache) || !aligned16(v_cache))
+        return fail(FFKV_ERR_INVALID_ARGUMENT, "q, out and cache pointers must be 16-byte aligned");
+
+    const float       sm_scale = scale > 0.0f ? scale : 1.0f / sqrtf(static_cast<float>(head_dim));
+    ffkv::PrefillArgs a{};
+    a.q = q;
+    a.out = out;
+    a.k_cache = k_cache;
+    a.v_cache = v_cache;
+    a.k_scale = k_scale;
+    a.v_scale = v_scale;
+    a.block_table = block_table;
+    a.context_lens = context_lens;
+    a.qo_dtype = qo_dtype;
+    a.cache_dtype = cache_dtype;
+    a.batch = batch;
+    a.seq_len = seq_len;
+    a.num_heads = num_heads;
+    a.num_kv_heads = num_kv_heads;
+    a.group = num_heads / num_kv_heads;
+    a.head_dim = head_dim;
+    a.max_blocks = paged ? max_blocks : 0;
+    a.num_blocks = paged ? num_blocks : 0;
+    a.cap_tokens = paged ? ffkv::decode_cap_tokens(max_blocks, max_context_len) : seq_len;
+    a.paged = paged;
+    a.scale_log2 = sm_scale * 1.4426950408889634f;
+    hipError_t e = ffkv::launch_prefill(a, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "prefill launch");
+    return ok();
+}
+
 int ffkv_rope(void* q, void* k, int dtype, const int32_t* context_lens, int batch, int seq_len, int num_heads,
               int num_kv_heads, int head_dim, float rope_theta, void* stream)
 {

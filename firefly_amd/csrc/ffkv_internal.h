@@ -53,6 +53,31 @@ struct RopeArgs
     float          theta;
 };
 
+struct PrefillArgs
+{
+    const void*    q;    // [B, S, Hq, D]
+    void*          out;  // [B, S, Hq * D]
+    const void*    k_cache;  // paged: [N, 16, Hkv, D]; contiguous: [B, S, Hkv, D]
+    const void*    v_cache;
+    const float*   k_scale;
+    const float*   v_scale;
+    const int32_t* block_table;   // paged only
+    const int32_t* context_lens;  // paged only: tokens cached before the chunk
+    int            qo_dtype;
+    int            cache_dtype;
+    int            batch;
+    int            seq_len;
+    int            num_heads;
+    int            num_kv_heads;
+    int            group;
+    int            head_dim;
+    int            max_blocks;
+    int            num_blocks;
+    int            cap_tokens;  // paged: keys per row are clamped to this
+    bool           paged;
+    float          scale_log2;
+};
+
 struct DecodeArgs
 {
     const void*    q;
@@ -84,7 +109,8 @@ struct DecodeArgs
 };
 
 hipError_t launch_append(const AppendArgs& a, hipStream_t stream);
-hipError_t launch_rope_append(const RopeArgs& a, hipStream_t stream);  // rotate q/k, then append when k_cache set
+hipError_t launch_rope_append(const RopeArgs& a, hipStream_t stream);
+hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream);  // matrix-core prefill (16-bit/8-bit caches)  // rotate q/k, then append when k_cache set
 hipError_t launch_decode(const DecodeArgs& a, hipStream_t stream);       // generic kernel (any cache dtype)
 hipError_t launch_decode_mfma(const DecodeArgs& a, hipStream_t stream);  // matrix-core kernel (16-bit/8-bit caches)
 

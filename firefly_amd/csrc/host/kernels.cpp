@@ -110,6 +110,32 @@ void decode(Tensor& q, Tensor& k, Tensor& v, const float* k_scale, const float* 
     report(rc, "PagedAttention failed");
 }
 
+// Prefill: block_table == nullptr is the reference's contiguous causal branch (k, v [B, S, Hkv, D],
+// src/kernels/attention.cu:460-474); otherwise chunked prefill over the paged cache with the chunk's queries at
+// context_lens[b] + t.
+void prefill(Tensor& q, Tensor& k, Tensor& v, const float* k_scale, const float* v_scale, Tensor& out,
+             void* block_table, int kv_head_num, int seq_len, int max_context_blocks, const int* context_lens)
+{
+    if (q.shape().size() != 4 || k.shape().size() != 4 || !is_gpu(q) || !is_gpu(k) || !is_gpu(v) || !is_gpu(out))
+        return fail("attention (prefill): q must be [B, S, Hq, D] and all tensors on the GPU");
+    const int B = static_cast<int>(q.shape()[0]);
+    const int S = static_cast<int>(q.shape()[1]);
+    const int Hq = static_cast<int>(q.shape()[2]);
+    const int D = static_cast<int>(q.shape()[3]);
+    if (seq_len != S) return fail("attention (prefill): seq_len must equal q.shape()[1]");
+    if (out.numel() < static_cast<int64_t>(B) * S * Hq * D || out.dtype() != q.dtype())
+        return fail("attention (prefill): output must hold B*S*Hq*D elements of q's dtype");
+    if (k.shape()[2] != kv_head_num || k.shape()[3] != D || v.shape() != k.shape() || v.dtype() != k.dtype())
+        return fail("attention (prefill): k/v must be [.., .., kv_head_num, head_dim] and alike");
+    if (block_table == nullptr && (k.shape()[0] != B || k.shape()[1] != S))
+        return fail("attention (prefill): contiguous k/v must be [B, seq_len, kv_head_num, head_dim]");
+    const int rc = ffkv_paged_prefill(q.data(), out.data(), code(q.dtype()), k.data(), v.data(), code(k.dtype()),
+                                      k_scale, v_scale, reinterpret_cast<const int32_t*>(block_table), context_lens, B,
+                                      S, Hq, kv_head_num, D, FFKV_BLOCK_SIZE, block_table ? max_context_blocks : 0,
+                                      block_table ? static_cast<int>(k.shape()[0]) : 0, 0, 0.0f, t_stream);
+    report(rc, "attention (prefill) failed");
+}
+
 void append(const Tensor& k, const Tensor& v, Tensor& kc, Tensor& vc, float* ks, float* vs, const int* block_table,
             const int* context_lens, int max_blocks)
 {
@@ -156,9 +182,9 @@ std::string last_error() { return t_error; }
 void attention(Tensor& q, Tensor& k, Tensor& v, Tensor& output, void* kv_cache_block_table, int kv_head_num,
                int seq_len, int max_context_blocks, const int* context_lens)
 {
-    (void)seq_len;  // the decode branch attends context_lens[b] + 1 tokens whatever seq_len says
-    if (kv_cache_block_table == nullptr)
-        return fail("attention: contiguous (block-table-free) prefill attention is not part of this library");
+    if (kv_cache_block_table == nullptr || (q.shape().size() == 4 && q.shape()[1] > 1))
+        return prefill(q, k, v, nullptr, nullptr, output, kv_cache_block_table, kv_head_num, seq_len,
+                       max_context_blocks, context_lens);
     decode(q, k, v, nullptr, nullptr, output, kv_cache_block_table, kv_head_num, max_context_blocks, context_lens);
 }
 
@@ -166,8 +192,9 @@ void attention(Tensor& q, Tensor& k_cache, Tensor& v_cache, const Tensor& k_scal
                Tensor& output, void* kv_cache_block_table, int kv_head_num, int seq_len, int max_context_blocks,
                const int* context_lens)
 {
-    (void)seq_len;
-    if (kv_cache_block_table == nullptr) return fail("attention: a quantized cache needs a block table");
+    if (kv_cache_block_table == nullptr || (q.shape().size() == 4 && q.shape()[1] > 1))
+        return prefill(q, k_cache, v_cache, k_scale.data_as<const float>(), v_scale.data_as<const float>(), output,
+                       kv_cache_block_table, kv_head_num, seq_len, max_context_blocks, context_lens);
     decode(q, k_cache, v_cache, k_scale.data_as<const float>(), v_scale.data_as<const float>(), output,
            kv_cache_block_table, kv_head_num, max_context_blocks, context_lens);
 }

@@ -109,6 +109,29 @@ FFKV_API int ffkv_paged_decode(const void* q, void* out, int qo_dtype, const voi
                       void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * Causal prefill attention over the paged cache (chunked prefill with prefix reuse).  Replaces the prefill branch
+ * of `firefly::kernels::attention` (kv_cache_block_table == nullptr: flash_attn_wmma_kernel,
+ * src/kernels/attention.cu:22-286, dispatched at :460-474) and extends it to cached prefixes, which the
+ * reference's model skips (src/model/qwen_model.cu:147-151 routes every multi-token batch-1 step to the
+ * contiguous kernel).
+ *
+ * q [batch, seq_len, num_heads, head_dim], out [batch, seq_len, num_heads*head_dim], both qo_dtype.  With a
+ * block table, query token t of row b sits at position context_lens[b] + t and attends the row's keys
+ * 0 .. context_lens[b] + t read from the pages (context_lens = tokens cached BEFORE this chunk, whose K/V must
+ * already be appended, e.g. by ffkv_append with the same context_lens); keys on invalid pages or at or beyond
+ * min(context_lens[b] + seq_len, max_context_len or max_blocks*16) are skipped, and a query with no key gives
+ * zeros.  With block_table == NULL, k_cache / v_cache are the chunk's contiguous [batch, seq_len, num_kv_heads,
+ * head_dim] tensors and positions start at 0: the reference's causal prefill.  seq_len = 1 is decode attention.
+ * cache_dtype F16, BF16, I8 or FP8_E4M3 (scales as for ffkv_paged_decode); any GQA group; scale <= 0 selects
+ * 1/sqrt(head_dim).  No workspace; pointers 16-byte aligned.
+ */
+FFKV_API int ffkv_paged_prefill(const void* q, void* out, int qo_dtype, const void* k_cache, const void* v_cache,
+                                int cache_dtype, const float* k_scale, const float* v_scale, const int32_t* block_table,
+                                const int32_t* context_lens, int batch, int seq_len, int num_heads, int num_kv_heads,
+                                int head_dim, int block_size, int max_blocks, int num_blocks, int max_context_len,
+                                float scale, void* stream);
+
+/*
  * Rotary position embedding of q and k in place.  Replaces `firefly::kernels::apply_rope(q, k, head_dim, seq_len,
  * theta, context_lens)` (include/firefly/kernels.h:68, src/kernels/rope.cu:22-137, called at
  * src/model/qwen_model.cu:136).  q [batch, seq_len, num_heads, head_dim] and k [batch, seq_len, num_kv_heads,

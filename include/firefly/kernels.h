@@ -29,12 +29,18 @@ FIREFLY_API std::string last_error();
 /**
  * @brief Scaled dot-product attention (reference include/firefly/kernels.h:83-84).
  *
- * Paged decode when kv_cache_block_table != nullptr: q [B, 1, Hq, D]; k / v the page pools
+ * Paged decode when kv_cache_block_table != nullptr and q is [B, 1, Hq, D]: k / v the page pools
  * [num_blocks, 16, kv_head_num, D]; output [B, 1, Hq*D] (or any tensor of B*Hq*D elements) in q's dtype;
  * kv_cache_block_table int32 [B, max_context_blocks] on the device; context_lens int32 [B] on the device, tokens
- * cached before this step (context_lens[b] + 1 tokens are attended).  seq_len is ignored, as in the reference's
- * decode branch.  The reference's other branch (kv_cache_block_table == nullptr: contiguous causal prefill
- * attention, src/kernels/attention.cu:460-474) is not part of this library and is reported as an error.
+ * cached before this step (context_lens[b] + 1 tokens are attended); seq_len is not used, as in the reference's
+ * decode branch.
+ *
+ * Prefill otherwise (seq_len must equal q.shape()[1]; output [B, S, Hq*D]):
+ *   - kv_cache_block_table == nullptr: the reference's contiguous causal prefill (src/kernels/attention.cu:460-474),
+ *     k / v the chunk's [B, S, kv_head_num, D] tensors;
+ *   - kv_cache_block_table != nullptr and S > 1: chunked prefill over the pages, query t of row b at position
+ *     context_lens[b] + t attending keys 0 .. context_lens[b] + t (the chunk must already be appended), which
+ *     reuses a cached prefix instead of recomputing it.
  */
 FIREFLY_API void attention(Tensor& q, Tensor& k, Tensor& v, Tensor& output, void* kv_cache_block_table,
                            int kv_head_num, int seq_len, int max_context_blocks, const int* context_lens);

@@ -34,6 +34,9 @@ def _load() -> ctypes.CDLL:
     lib.ffo_paged_decode_f64.restype = i32
     lib.ffo_paged_decode_f64.argtypes = [vp, i32, vp, vp, i32, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32,
                                          i32, f32, vp]
+    lib.ffo_paged_prefill_f64.restype = i32
+    lib.ffo_paged_prefill_f64.argtypes = [vp, i32, vp, vp, i32, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32,
+                                          i32, f32, vp]
     lib.ffo_rope.restype = i32
     lib.ffo_rope.argtypes = [vp, i32, vp, i32, i32, i32, i32, f32]
     lib.ffo_quant_i8_row.restype = f32
@@ -167,4 +170,24 @@ def paged_decode_f64(q, qo_dtype, k_cache, v_cache, cache_dtype, block_table, co
                                   Hkv, D, 16, bt.shape[-1], N, max_context_len, scale, _p(out))
     if rc != 0:
         raise ValueError(f"ffo_paged_decode_f64 returned {rc}")
+    return out
+
+
+def paged_prefill_f64(q, qo_dtype, k_cache, v_cache, cache_dtype, block_table, context_lens, k_scale=None,
+                      v_scale=None, max_context_len=0, scale=0.0, num_blocks=None):
+    """q [B, S, Hq, D] storage array; block_table None means contiguous K/V [B, S, Hkv, D].
+    Returns float64 [B, S, Hq, D]."""
+    q = _c(q)
+    B, S, Hq, D = q.shape
+    Hkv = k_cache.shape[2]
+    bt = None if block_table is None else _c(block_table, np.int32)
+    ctx = None if context_lens is None else _c(context_lens, np.int32)
+    out = np.zeros((B, S, Hq, D), dtype=np.float64)
+    mb = 0 if bt is None else bt.shape[-1]
+    N = k_cache.shape[0] if num_blocks is None else num_blocks
+    rc = lib.ffo_paged_prefill_f64(_p(q), qo_dtype, _p(_c(k_cache)), _p(_c(v_cache)), cache_dtype,
+                                   _p(_c(k_scale, np.float32)), _p(_c(v_scale, np.float32)), _p(bt), _p(ctx), B, S,
+                                   Hq, Hkv, D, mb, N, max_context_len, scale, _p(out))
+    if rc != 0:
+        raise ValueError(f"ffo_paged_prefill_f64 returned {rc}")
     return out

@@ -14,6 +14,8 @@
  *                                            (:345-369), final merge of the eight states (:403-446)
  *   dispatch src/kernels/attention.cu:455-458 scale = 1/sqrtf(head_dim)
  *   rope     src/kernels/rope.cu:22-137       rotate-half pairs (i, i + D/2), pos = ctx + t, theta^(-2i/D)
+ *   prefill  src/kernels/attention.cu:22-286  causal attention (key n > query m masked, :173-174), generalized
+ *                                            to queries at ctx + t over the paged cache (prefix included)
  *
  * Extensions the reference does not have (it is fp16-only and leaves bad addressing undefined), restated
  * from the specification in include/ffkv.h: bf16/fp32 storage, int8 and OCP fp8 e4m3 quantization, skipped
@@ -28,6 +30,9 @@
  *                 saturation edge pinned by the OCP spec values (448, 464, inf, NaN).
  *   int8 quant    torch.round (half-even) on the closed form, golden fixtures.
  *   ffo_append    closed-form address formula in numpy, whole-pool sentinel check, append->gather round trip.
+ *   ffo_paged_prefill_f64  seq_len = 1 equals ffo_paged_decode_f64; torch SDPA with an explicit causal mask on
+ *                 the gathered K/V (prefix included); contiguous mode = torch SDPA is_causal; shared prefix
+ *                 = private copy.
  *   ffo_rope      torch float64 rotate_half formulation (q*cos + rotate_half(q)*sin), position 0 = identity,
  *                 unit vectors give (cos, sin), pair norms preserved, q.k depends only on the position offset.
  *   ffo_paged_decode  float64 closed form (ffo_paged_decode_f64), torch SDPA on gathered K/V with repeated
@@ -624,6 +629,96 @@ int ffo_paged_decode_f64(const void* q, int qo_dtype, const void* k_cache, const
                                                    (size_t)rows[i], kvh);
             }
             for (int d = 0; d < D; ++d) o[d] /= den;
+        }
+        free(s);
+        free(rows);
+    }
+    return 0;
+}
+
+/* ----------------------------------------------------------------------------------------------------------
+ * Prefill (chunked, paged).  Extends the decode restatement to seq_len query tokens per row: query t of row b
+ * sits at position ctx[b] + t and attends the keys 0 .. ctx[b] + t of the row (causal over the cached prefix and
+ * the chunk), read after this chunk's K/V were appended; keys at or beyond L_b = ctx[b] + seq_len (clamped to
+ * [0, max_blocks*16] and to max_context_len > 0) or on an invalid page are skipped.  With block_table == NULL
+ * the K/V are contiguous [batch, seq_len, Hkv, D] and ctx is 0: the causal attention of the reference's prefill
+ * branch (flash_attn_wmma_kernel, src/kernels/attention.cu:22-286, key n masked when n >= seq_len or n > m at
+ * :173-174, scale 1/sqrtf(D) at :458).  With seq_len = 1 it equals ffo_paged_decode_f64.  Closed form in
+ * float64; out is [batch, seq_len, num_heads, head_dim].
+ * -------------------------------------------------------------------------------------------------------- */
+
+int ffo_paged_prefill_f64(const void* q, int qo_dtype, const void* k_cache, const void* v_cache, int cache_dtype,
+                          const float* k_scale, const float* v_scale, const int32_t* block_table,
+                          const int32_t* context_lens, int batch, int seq_len, int num_heads, int num_kv_heads,
+                          int head_dim, int max_blocks, int num_blocks, int max_context_len, float scale, double* out)
+{
+    if (!is_act_dtype(qo_dtype) || !is_cache_dtype(cache_dtype)) return ERR_UNSUPPORTED;
+    if (batch < 0 || seq_len < 0 || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 ||
+        num_heads % num_kv_heads != 0 || max_blocks < 0 || num_blocks < 0)
+        return ERR_ARG;
+    if (batch == 0 || seq_len == 0) return 0;
+    const int paged = block_table != NULL;
+    if (!q || !k_cache || !v_cache || !out || (paged && !context_lens)) return ERR_ARG;
+    if ((cache_dtype == DT_I8 || cache_dtype == DT_FP8) && (!k_scale || !v_scale)) return ERR_ARG;
+    const int    D = head_dim, S = seq_len, G = num_heads / num_kv_heads;
+    const double sc = scale > 0.0f ? (double)scale : 1.0 / sqrt((double)head_dim);
+    long long    cap = (long long)max_blocks * 16;
+    if (max_context_len > 0 && cap > max_context_len) cap = max_context_len;
+
+    for (int b = 0; b < batch; ++b)
+    {
+        long long ctx = paged ? (long long)context_lens[b] : 0;
+        long long L = ctx + S;
+        if (paged && L > cap) L = cap;
+        if (L < 0) L = 0;
+        double*    s = (double*)malloc(sizeof(double) * (size_t)(L > 0 ? L : 1));
+        long long* rows = (long long*)malloc(sizeof(long long) * (size_t)(L > 0 ? L : 1));
+        for (int t = 0; t < S; ++t)
+        {
+            long long kend = ctx + t + 1;
+            if (kend > L) kend = L;
+            for (int h = 0; h < num_heads; ++h)
+            {
+                const int kvh = h / G;
+                double*   o = out + (((size_t)b * S + t) * num_heads + (size_t)h) * (size_t)D;
+                size_t    qoff = (((size_t)b * S + t) * num_heads + (size_t)h) * (size_t)D;
+                long long n = 0;
+                double    mx = -INFINITY;
+                for (long long j = 0; j < kend; ++j)
+                {
+                    long long row;
+                    if (paged)
+                    {
+                        int phys = block_table[(size_t)b * (size_t)max_blocks + (size_t)(j / 16)];
+                        if (phys < 0 || phys >= num_blocks) continue;
+                        row = ((long long)phys * 16 + j % 16) * num_kv_heads + kvh;
+                    }
+                    else
+                    {
+                        row = ((long long)b * S + j) * num_kv_heads + kvh;
+                    }
+                    double dot = 0.0;
+                    for (int d = 0; d < D; ++d)
+                        dot += (double)load_act(q, qo_dtype, qoff + d) *
+                               (double)load_cache(k_cache, cache_dtype, (size_t)row * D + d, k_scale, (size_t)row, kvh);
+                    s[n] = dot * sc;
+                    rows[n] = row;
+                    if (s[n] > mx) mx = s[n];
+                    ++n;
+                }
+                for (int d = 0; d < D; ++d) o[d] = 0.0;
+                if (n == 0) continue;
+                double den = 0.0;
+                for (long long i = 0; i < n; ++i)
+                {
+                    double p = exp(s[i] - mx);
+                    den += p;
+                    for (int d = 0; d < D; ++d)
+                        o[d] += p * (double)load_cache(v_cache, cache_dtype, (size_t)rows[i] * D + d, v_scale,
+                                                       (size_t)rows[i], kvh);
+                }
+                for (int d = 0; d < D; ++d) o[d] /= den;
+            }
         }
         free(s);
         free(rows);

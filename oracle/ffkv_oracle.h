@@ -41,6 +41,14 @@ int ffo_append(const void* k_src, const void* v_src, int src_dtype, void* k_cach
                float* k_scale, float* v_scale, const int32_t* block_table, const int32_t* context_lens, int batch,
                int seq_len, int num_kv_heads, int head_dim, int block_size, int max_blocks, int num_blocks);
 
+/* Causal prefill over the paged cache (queries at ctx + t, prefix included) or, with block_table == NULL, over
+ * contiguous [batch, seq_len, Hkv, D] K/V (the reference's prefill branch); float64 closed form, out
+ * [batch, seq_len, num_heads, head_dim]. */
+int ffo_paged_prefill_f64(const void* q, int qo_dtype, const void* k_cache, const void* v_cache, int cache_dtype,
+                          const float* k_scale, const float* v_scale, const int32_t* block_table,
+                          const int32_t* context_lens, int batch, int seq_len, int num_heads, int num_kv_heads,
+                          int head_dim, int max_blocks, int num_blocks, int max_context_len, float scale, double* out);
+
 /* Rotary embedding in place of x [batch, seq_len, heads, head_dim] (src/kernels/rope.cu:22-137); see ffkv_rope. */
 int ffo_rope(void* x, int dtype, const int32_t* context_lens, int batch, int seq_len, int heads, int head_dim,
              float theta);

@@ -90,12 +90,40 @@ int kas_rope_append(void* q, void* k_new, void* v_new, void* k_cache, void* v_ca
     return 0;
 }
 
-// The reference's prefill branch (no block table) is reported as an error by this library.
-int kas_prefill_branch_rejected()
+// The reference's prefill branch: kernels::attention(q, k, v, out, nullptr, Hkv, S, max_blocks, nullptr) with the
+// chunk's contiguous q [B,S,Hq,D], k/v [B,S,Hkv,D] (src/model/qwen_model.cu:147-151); all in dtype qd.
+int kas_contiguous_prefill(void* q, void* k, void* v, void* out, int B, int S, int Hq, int Hkv, int D, int qd,
+                           void* stream)
 {
-    Tensor q = Tensor::from_external(nullptr, {1, 4, 2, 128}, DType::BF16, Device::GPU);
-    kernels::attention(q, q, q, q, nullptr, 2, 4, 0, nullptr);
-    return kernels::last_error().empty() ? 0 : 1;
+    kernels::set_default_stream(static_cast<hipStream_t>(stream));
+    const DType qt = static_cast<DType>(qd);
+    Tensor      tq = Tensor::from_external(q, {B, S, Hq, D}, qt, Device::GPU);
+    Tensor      tk = Tensor::from_external(k, {B, S, Hkv, D}, qt, Device::GPU);
+    Tensor      tv = Tensor::from_external(v, {B, S, Hkv, D}, qt, Device::GPU);
+    Tensor      to = Tensor::from_external(out, {B, S, Hq * D}, qt, Device::GPU);
+    kernels::attention(tq, tk, tv, to, nullptr, Hkv, S, 0, nullptr);
+    if (!kernels::last_error().empty()) return g_err = kernels::last_error(), -1;
+    return 0;
+}
+
+// Chunked prefill through the paged branch: q [B,S,Hq,D] with a block table, after kernels::append_kv_cache.
+int kas_paged_prefill(void* q, void* k_new, void* v_new, void* k_cache, void* v_cache, void* out,
+                      const int* block_table, const int* context_lens, int B, int S, int Hq, int Hkv, int D, int N,
+                      int max_blocks, int qd, int cd, void* stream)
+{
+    kernels::set_default_stream(static_cast<hipStream_t>(stream));
+    const DType qt = static_cast<DType>(qd), ct = static_cast<DType>(cd);
+    Tensor      tq = Tensor::from_external(q, {B, S, Hq, D}, qt, Device::GPU);
+    Tensor      tk = Tensor::from_external(k_new, {B, S, Hkv, D}, qt, Device::GPU);
+    Tensor      tv = Tensor::from_external(v_new, {B, S, Hkv, D}, qt, Device::GPU);
+    Tensor      kc = Tensor::from_external(k_cache, {N, 16, Hkv, D}, ct, Device::GPU);
+    Tensor      vc = Tensor::from_external(v_cache, {N, 16, Hkv, D}, ct, Device::GPU);
+    Tensor      to = Tensor::from_external(out, {B, S, Hq * D}, qt, Device::GPU);
+    kernels::append_kv_cache(tk, tv, kc, vc, block_table, context_lens, max_blocks);
+    if (!kernels::last_error().empty()) return g_err = kernels::last_error(), -1;
+    kernels::attention(tq, kc, vc, to, const_cast<int*>(block_table), Hkv, S, max_blocks, context_lens);
+    if (!kernels::last_error().empty()) return g_err = kernels::last_error(), -1;
+    return 0;
 }
 
 }  // extern "C"

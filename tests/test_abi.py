@@ -138,3 +138,36 @@ def test_rope_rejects_and_empty(ff):
     assert ff.lib.ffkv_rope(16, 16, ff.DTYPE_BF16, None, 0, 1, 32, 8, 128, 1e6, None) == 0
     assert ff.lib.ffkv_rope(None, 16, ff.DTYPE_BF16, None, 1, 0, 0, 8, 128, 1e6, None) == 0
     assert _rope_append(ff, batch=0, k=None, v=None, q=None) == 0
+
+
+def _prefill(ff, **kw):
+    a = dict(q=16, out=16, qo_dtype=ff.DTYPE_BF16, k_cache=16, v_cache=16, cache_dtype=ff.DTYPE_BF16,
+             k_scale=None, v_scale=None, block_table=16, context_lens=16, batch=1, seq_len=8, num_heads=32,
+             num_kv_heads=8, head_dim=128, block_size=16, max_blocks=4, num_blocks=4, max_context_len=0, scale=0.0,
+             stream=None)
+    a.update(kw)
+    return ff.lib.ffkv_paged_prefill(*a.values())
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(block_size=8), -2),
+    (dict(head_dim=80), -2),
+    (dict(qo_dtype=3), -2),
+    (dict(cache_dtype=0), -2),                     # fp32 caches: decode only
+    (dict(num_heads=30), -1),
+    (dict(batch=-1), -1),
+    (dict(q=None), -1),
+    (dict(context_lens=None), -1),                 # paged mode needs context_lens
+    (dict(cache_dtype=3), -1),                     # int8 without scales
+    (dict(cache_dtype=3, block_table=None, k_scale=16, v_scale=16), -2),  # int8 needs pages
+    (dict(out=24), -1),                            # misaligned
+])
+def test_prefill_rejects(ff, kw, code):
+    assert _prefill(ff, **kw) == code
+    assert ff.lib.ffkv_last_error().decode() != ""
+
+
+def test_prefill_empty_and_contiguous_args_ok(ff):
+    assert _prefill(ff, batch=0, q=None) == 0
+    assert _prefill(ff, seq_len=0) == 0
+    assert ff.lib.ffkv_last_error().decode() == ""

@@ -17,6 +17,13 @@ import oracle as O
 SHIM = Path(__file__).resolve().parent / "cpp" / "libkernels_api_shim.so"
 
 
+def _excess_bf16(got, ref):
+    """Max-abs error beyond half a bf16 ulp at the value (the output's own rounding)."""
+    m = np.maximum(np.abs(got), np.abs(ref))
+    half = 2.0 ** (np.floor(np.log2(np.maximum(m, 2.0 ** -126))) - 8)
+    return float((np.abs(got.astype(np.float64) - ref) - half).max())
+
+
 @pytest.fixture(scope="module")
 def shim(ff):
     if not SHIM.exists():
@@ -28,7 +35,10 @@ def shim(ff):
     lib.kas_rope_append.restype = i
     lib.kas_rope_append.argtypes = [vp] * 7 + [vp, vp] + [i] * 9 + [ctypes.c_float, i, vp]
     lib.kas_last_error.restype = ctypes.c_char_p
-    lib.kas_prefill_branch_rejected.restype = i
+    lib.kas_contiguous_prefill.restype = i
+    lib.kas_contiguous_prefill.argtypes = [vp] * 4 + [i] * 6 + [vp]
+    lib.kas_paged_prefill.restype = i
+    lib.kas_paged_prefill.argtypes = [vp] * 8 + [i] * 9 + [vp]
     return lib
 
 
@@ -70,8 +80,51 @@ def test_cxx_api_append_then_decode(shim, gpu, act, kv, tol):
 
 
 @pytest.mark.gpu
-def test_cxx_api_prefill_branch_reports_error(shim, gpu):
-    assert shim.kas_prefill_branch_rejected() == 1
+def test_cxx_api_contiguous_prefill_branch(shim, gpu):
+    """kernels::attention with a null block table: the reference's causal prefill over the chunk's K/V."""
+    import torch
+
+    import gpu_util as gu
+
+    rng = np.random.default_rng(90)
+    B, S, Hq, Hkv, D = 2, 45, 16, 4, 128
+    q, k, v = (cases.encode(rng.standard_normal(s, dtype=np.float32), O.DTYPE_BF16)
+               for s in [(B, S, Hq, D), (B, S, Hkv, D), (B, S, Hkv, D)])
+    dq, dk, dv = (gu.to_dev(a, O.DTYPE_BF16, gpu) for a in (q, k, v))
+    out = torch.empty((B, S, Hq * D), dtype=torch.bfloat16, device=gpu)
+    rc = shim.kas_contiguous_prefill(dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), out.data_ptr(), B, S, Hq, Hkv, D,
+                                     O.DTYPE_BF16, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert rc == 0, shim.kas_last_error()
+    ref = O.paged_prefill_f64(q, O.DTYPE_BF16, k, v, O.DTYPE_BF16, None, None)
+    got = out.float().cpu().numpy().reshape(ref.shape)
+    assert _excess_bf16(got, ref) <= 2e-3
+
+
+@pytest.mark.gpu
+def test_cxx_api_chunked_prefill_over_cached_prefix(shim, gpu):
+    """kernels::append_kv_cache then kernels::attention with a block table and a multi-token q."""
+    import torch
+
+    import gpu_util as gu
+
+    c = cases.make_case(91, 3, 16, 4, 128, [0, 40, 130], act="bf16", S=20)
+    rng = np.random.default_rng(92)
+    qn = cases.encode(rng.standard_normal((c.B, c.S, c.Hq, c.D), dtype=np.float32), c.act)
+    dq, kn, vn = gu.to_dev(qn, c.act, gpu), gu.to_dev(c.k_new, c.act, gpu), gu.to_dev(c.v_new, c.act, gpu)
+    dk, dv = gu.to_dev(c.k_pool, c.kv, gpu), gu.to_dev(c.v_pool, c.kv, gpu)
+    bt, ctx = torch.from_numpy(c.block_table).to(gpu), torch.from_numpy(c.ctx).to(gpu)
+    out = torch.empty((c.B, c.S, c.Hq * c.D), dtype=dq.dtype, device=gpu)
+    rc = shim.kas_paged_prefill(dq.data_ptr(), kn.data_ptr(), vn.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+                                out.data_ptr(), bt.data_ptr(), ctx.data_ptr(), c.B, c.S, c.Hq, c.Hkv, c.D,
+                                c.num_blocks, c.max_blocks, c.act, c.kv, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert rc == 0, shim.kas_last_error()
+    rk, rv = c.k_pool.copy(), c.v_pool.copy()
+    O.append(c.k_new, c.v_new, c.act, rk, rv, c.kv, c.block_table, c.ctx)
+    ref = O.paged_prefill_f64(qn, c.act, rk, rv, c.kv, c.block_table, c.ctx)
+    got = out.float().cpu().numpy().reshape(ref.shape)
+    assert _excess_bf16(got, ref) <= 2e-3
 
 
 @pytest.mark.gpu

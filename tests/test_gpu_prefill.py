@@ -1,0 +1,143 @@
+"""Chunked / paged prefill attention on the GPU against the CPU closed form (oracle ffo_paged_prefill_f64).
+
+Bar (as for decode): outputs within max-abs 2e-3 for 16-bit caches and 2e-2 for int8/fp8 caches of the float64
+closed form, beyond the output format's own rounding (half an ulp at the value).  Cases: chunks with and without
+a cached prefix (context_lens > 0 is the prefix-reuse step the reference's model skips), GQA groups 1..16, head
+dims 64/128/256, quantized caches, invalid pages and rows without keys, shared prefix pages, the contiguous
+(block-table-free) mode of the reference's prefill branch, and seq_len = 1 against the decode kernel.
+"""
+
+import math
+
+import numpy as np
+import pytest
+
+import cases
+import gpu_util as gu
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def half_ulp(x, act):
+    if act == O.DTYPE_F32:
+        return np.zeros_like(x)
+    mant, emin = (7, -126) if act == O.DTYPE_BF16 else (10, -14)
+    e = np.floor(np.log2(np.maximum(np.abs(x), 2.0 ** emin)))
+    return 2.0 ** (e - mant - 1)
+
+
+def _run(ff, dev, c, qn, tbl=None, ctx=None, contiguous=False):
+    """Append the case's chunk (k_new/v_new) to its pools, then prefill; returns (out f32 [B,S,Hq,D], ref f64)."""
+    import torch
+
+    tbl = c.block_table if tbl is None else tbl
+    ctx = c.ctx if ctx is None else ctx
+    if contiguous:
+        k = gu.to_dev(c.k_new, c.act, dev)
+        v = gu.to_dev(c.v_new, c.act, dev)
+        q = gu.to_dev(qn, c.act, dev)
+        out = ff.paged_prefill(q, k, v, None, None)
+        torch.cuda.synchronize()
+        ref = O.paged_prefill_f64(qn, c.act, c.k_new, c.v_new, c.act, None, None)
+    else:
+        kp = gu.to_dev(c.k_pool, c.kv, dev)
+        vp = gu.to_dev(c.v_pool, c.kv, dev)
+        ks = None if c.k_scale is None else torch.from_numpy(c.k_scale.copy()).to(dev)
+        vs = None if c.v_scale is None else torch.from_numpy(c.v_scale.copy()).to(dev)
+        bt = torch.from_numpy(np.ascontiguousarray(tbl)).to(dev)
+        cx = torch.from_numpy(np.ascontiguousarray(ctx)).to(dev)
+        ff.append_kv_cache(gu.to_dev(c.k_new, c.act, dev), gu.to_dev(c.v_new, c.act, dev), kp, vp, bt, cx, ks, vs)
+        q = gu.to_dev(qn, c.act, dev)
+        out = ff.paged_prefill(q, kp, vp, bt, cx, k_scale=ks, v_scale=vs)
+        torch.cuda.synchronize()
+        rk, rv = c.k_pool.copy(), c.v_pool.copy()
+        rks = None if c.k_scale is None else c.k_scale.copy()
+        rvs = None if c.v_scale is None else c.v_scale.copy()
+        O.append(c.k_new, c.v_new, c.act, rk, rv, c.kv, tbl, ctx, rks, rvs)
+        ref = O.paged_prefill_f64(qn, c.act, rk, rv, c.kv, tbl, ctx, rks, rvs)
+    got = out.float().cpu().numpy().reshape(ref.shape)
+    return got, ref
+
+
+def _check(got, ref, act, tol):
+    diff = np.abs(got.astype(np.float64) - ref)
+    excess = float((diff - half_ulp(np.maximum(np.abs(got), np.abs(ref)), act)).max())
+    print(f"  max-abs err {diff.max():.3e}, beyond output rounding {excess:.3e} (tol {tol})", flush=True)
+    assert excess <= tol
+
+
+def _case(seed, B, Hq, Hkv, D, ctx, S, act="bf16", kv=None, shared=0):
+    c = cases.make_case(seed, B, Hq, Hkv, D, ctx, act=act, kv=kv, S=S, input_scale=1.0,
+                        shared_prefix_blocks=shared)
+    rng = np.random.default_rng(seed + 1000)
+    qn = cases.encode(rng.standard_normal((B, S, Hq, D), dtype=np.float32), c.act)
+    print(f"case prefill seed={seed} B={B} Hq={Hq} Hkv={Hkv} D={D} S={S} act={act} kv={kv or act} "
+          f"ctx={list(np.asarray(ctx))}", flush=True)
+    return c, qn
+
+
+@pytest.mark.parametrize("S", [1, 16, 37, 130])
+@pytest.mark.parametrize("ctx", [[0, 0, 0], [17, 300, 5]])
+def test_prefill_bf16(ff, gpu, S, ctx):
+    c, qn = _case(100 + S, 3, 32, 8, 128, ctx, S)
+    _check(*_run(ff, gpu, c, qn), c.act, 2e-3)
+
+
+@pytest.mark.parametrize("act,kv,tol", [("f16", "f16", 2e-3), ("bf16", "i8", 2e-2), ("bf16", "fp8", 2e-2),
+                                        ("f16", "i8", 2e-2), ("f32", "bf16", 2e-3), ("f32", "fp8", 2e-2)])
+def test_prefill_dtypes(ff, gpu, act, kv, tol):
+    c, qn = _case(200, 3, 16, 4, 128, [0, 33, 250], 24, act=act, kv=kv)
+    _check(*_run(ff, gpu, c, qn), c.act, tol)
+
+
+@pytest.mark.parametrize("D", [64, 256])
+@pytest.mark.parametrize("G", [1, 7, 16])
+def test_prefill_head_shapes(ff, gpu, D, G):
+    c, qn = _case(300 + D + G, 2, 2 * G, 2, D, [9, 70], 19)
+    _check(*_run(ff, gpu, c, qn), c.act, 2e-3)
+
+
+def test_prefill_long_chunk_over_long_prefix(ff, gpu):
+    """A 512-token chunk after a 1500-token prefix (many workgroups per row, the causal limit varying)."""
+    c, qn = _case(400, 2, 32, 8, 128, [1500, 64], 512)
+    _check(*_run(ff, gpu, c, qn), c.act, 2e-3)
+
+
+def test_prefill_invalid_pages_and_rows_without_keys(ff, gpu):
+    c, qn = _case(500, 4, 8, 2, 128, [40, 0, 64, 20], 9)
+    tbl = c.block_table.copy()
+    tbl[0, 1] = -1                    # a hole in row 0's prefix
+    tbl[2, 0] = c.num_blocks + 5      # out of the pool
+    ctx = c.ctx.copy()
+    ctx[3] = -30                      # positions -30..-22: no key; the append skips them too
+    _check(*_run(ff, gpu, c, qn, tbl=tbl, ctx=ctx), c.act, 2e-3)
+
+
+def test_prefill_shared_prefix_pages(ff, gpu):
+    c, qn = _case(600, 4, 32, 8, 128, [64, 64, 80, 100], 12, shared=4)
+    _check(*_run(ff, gpu, c, qn), c.act, 2e-3)
+
+
+@pytest.mark.parametrize("S", [5, 64, 200])
+def test_prefill_contiguous_mode_is_reference_causal_prefill(ff, gpu, S):
+    c, qn = _case(700 + S, 2, 28, 4, 128, [0, 0], S)
+    _check(*_run(ff, gpu, c, qn, contiguous=True), c.act, 2e-3)
+
+
+def test_prefill_single_token_agrees_with_decode(ff, gpu):
+    import torch
+
+    c, qn = _case(800, 6, 32, 8, 128, [0, 15, 16, 200, 1023, 4000], 1)
+    got, ref = _run(ff, gpu, c, qn)
+    # decode kernel on the same appended cache
+    kp = gu.to_dev(c.k_pool, c.kv, gpu)
+    vp = gu.to_dev(c.v_pool, c.kv, gpu)
+    bt = torch.from_numpy(c.block_table).to(gpu)
+    cx = torch.from_numpy(c.ctx).to(gpu)
+    ff.append_kv_cache(gu.to_dev(c.k_new, c.act, gpu), gu.to_dev(c.v_new, c.act, gpu), kp, vp, bt, cx)
+    dec = ff.paged_attention(gu.to_dev(qn, c.act, gpu), kp, vp, bt, cx)
+    torch.cuda.synchronize()
+    d = dec.float().cpu().numpy().reshape(got.shape)
+    _check(got, ref, c.act, 2e-3)
+    assert np.abs(d - got).max() <= 2 * 2e-3
