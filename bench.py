@@ -81,6 +81,223 @@ def measured_traffic():
     return rec.get("bytes_per_call")
 
 
+BF16_MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense bf16
+
+
+def _events_us(fn, n: int, stream) -> float:
+    """Mean duration in us of fn(i) over n back-to-back calls, HIP events on the launch stream."""
+    import torch
+
+    for i in range(3):
+        fn(i)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(n):
+        fn(i)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / n * 1e3
+
+
+def _tables(rng, need, shared_blocks=0):
+    """Block tables for rows needing `need` blocks each; the first `shared_blocks` logical blocks of every row map
+    to the same physical blocks (a radix-cache prefix).  Returns (table int32 [B, max], pool blocks)."""
+    import numpy as np
+
+    private = [max(0, n - shared_blocks) for n in need]
+    total = shared_blocks + sum(private)
+    N = math.ceil(total * 1.1)
+    perm = rng.permutation(N).astype(np.int32)
+    table = np.full((len(need), max(need)), -1, dtype=np.int32)
+    pos = shared_blocks
+    for b, n in enumerate(need):
+        k = min(shared_blocks, n)
+        table[b, :k] = perm[:k]
+        table[b, k:n] = perm[pos:pos + private[b]]
+        pos += private[b]
+    return table, N
+
+
+def _pools(torch, gen, dev, N, Hkv, D, kv, layers):
+    shape = (N, BLOCK, Hkv, D)
+    out = []
+    for _ in range(layers):
+        if kv == "bf16":
+            kp = torch.randn(shape, generator=gen, device=dev, dtype=torch.bfloat16)
+            vp = torch.randn(shape, generator=gen, device=dev, dtype=torch.bfloat16)
+            ks = vs = None
+        elif kv == "i8":
+            kp = torch.randint(-127, 128, shape, generator=gen, device=dev, dtype=torch.int8)
+            vp = torch.randint(-127, 128, shape, generator=gen, device=dev, dtype=torch.int8)
+            ks = torch.rand((N, BLOCK, Hkv), generator=gen, device=dev) * 0.05
+            vs = torch.rand((N, BLOCK, Hkv), generator=gen, device=dev) * 0.05
+        else:  # fp8 e4m3 codes of magnitude <= 448 (no NaN codes)
+            kp = torch.randint(0, 126, shape, generator=gen, device=dev, dtype=torch.uint8)
+            kp |= torch.randint(0, 2, shape, generator=gen, device=dev, dtype=torch.uint8) << 7
+            vp = torch.randint(0, 126, shape, generator=gen, device=dev, dtype=torch.uint8)
+            vp |= torch.randint(0, 2, shape, generator=gen, device=dev, dtype=torch.uint8) << 7
+            ks = torch.full((Hkv,), 0.01, device=dev)
+            vs = torch.full((Hkv,), 0.01, device=dev)
+        out.append((kp, vp, ks, vs))
+    return out
+
+
+def decode_config(ff, torch, dev, stream, name, B, Hq, Hkv, D, ctx, kv="bf16", layers=2, shared_blocks=0,
+                  calls=50, seed=0):
+    """Decode attention alone on one configuration (layers rotated to defeat the 256 MB Infinity Cache)."""
+    import numpy as np
+
+    rng = np.random.default_rng(seed)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    Lp = [int(c) + 1 for c in ctx]
+    need = [math.ceil(x / BLOCK) for x in Lp]
+    table_np, N = _tables(rng, need, shared_blocks)
+    pools = _pools(torch, gen, dev, N, Hkv, D, kv, layers)
+    q = torch.randn((B, 1, Hq, D), generator=gen, device=dev, dtype=torch.bfloat16)
+    out = torch.empty((B, 1, Hq * D), device=dev, dtype=torch.bfloat16)
+    bt = torch.from_numpy(table_np).to(dev)
+    cx = torch.from_numpy(np.asarray(ctx, np.int32)).to(dev)
+    ws = ff.decode_workspace(B, Hq, D, table_np.shape[1], max(Lp), device=dev)
+
+    def call(i):
+        kp, vp, ks, vs = pools[i % layers]
+        ff.paged_attention(q, kp, vp, bt, cx, out=out, k_scale=ks, v_scale=vs, max_context_len=max(Lp),
+                           workspace=ws, stream=stream)
+
+    us = _events_us(call, calls, stream)
+    es = 2 if kv == "bf16" else 1
+    tok = sum(Lp)
+    kv_bytes = tok * Hkv * D * es * 2 + (tok * Hkv * 4 * 2 if kv == "i8" else 0)
+    other = B * Hq * D * 2 * 2 + sum(need) * 4 + 4 * B
+    logical = kv_bytes + other
+    rec = {"workload": name, "kv": kv, "batch": B, "heads": f"{Hq}/{Hkv}", "head_dim": D,
+           "context_tokens": tok, "us_per_call": us, "algorithmic_bytes": logical,
+           "TB_per_s": logical / (us * 1e-6) / 1e12, "pct_of_peak": logical / (us * 1e-6) / 1e12 / HBM_PEAK_TBS * 100,
+           "tokens_per_s": B / (us * 1e-6)}
+    if shared_blocks:
+        ushared = shared_blocks * BLOCK
+        utok = ushared + sum(x - min(ushared, x) for x in Lp)
+        unique = utok * Hkv * D * es * 2 + other
+        rec.update({"unique_bytes": unique, "unique_TB_per_s": unique / (us * 1e-6) / 1e12,
+                    "unique_pct_of_peak": unique / (us * 1e-6) / 1e12 / HBM_PEAK_TBS * 100,
+                    "effective_TB_per_s_logical": rec["TB_per_s"]})
+    del pools
+    torch.cuda.empty_cache()
+    return rec
+
+
+def c4_config(ff, torch, dev, stream, layers=2, calls=30, seed=4):
+    """128 sequences sharing a 2048-token prefix (128 physical blocks in every table), private
+    suffixes U[64, 1024]; per step 120 rows decode (append 1 token + attention) and 8 rows run a 512-token chunked
+    prefill (append 512 tokens + causal attention over their cached prefix and the chunk)."""
+    import numpy as np
+
+    Bt, Bd, Hq, Hkv, D, PRE, CH = 128, 120, 32, 8, 128, 2048, 512
+    rng = np.random.default_rng(seed)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    suffix = rng.integers(64, 1025, size=Bt)
+    ctx = (PRE + suffix).astype(np.int32)                     # cached before this step
+    new = np.array([1] * Bd + [CH] * (Bt - Bd))
+    need = [math.ceil((int(c) + int(n)) / BLOCK) for c, n in zip(ctx, new)]
+    table_np, N = _tables(rng, need, PRE // BLOCK)
+    pools = _pools(torch, gen, dev, N, Hkv, D, "bf16", layers)
+    bt_d = torch.from_numpy(table_np[:Bd].copy()).to(dev)
+    bt_c = torch.from_numpy(table_np[Bd:].copy()).to(dev)
+    cx_d = torch.from_numpy(ctx[:Bd].copy()).to(dev)
+    cx_c = torch.from_numpy(ctx[Bd:].copy()).to(dev)
+    Bc = Bt - Bd
+    qd = torch.randn((Bd, 1, Hq, D), generator=gen, device=dev, dtype=torch.bfloat16)
+    kd = torch.randn((Bd, 1, Hkv, D), generator=gen, device=dev, dtype=torch.bfloat16)
+    vd = torch.randn((Bd, 1, Hkv, D), generator=gen, device=dev, dtype=torch.bfloat16)
+    qc = torch.randn((Bc, CH, Hq, D), generator=gen, device=dev, dtype=torch.bfloat16)
+    kc = torch.randn((Bc, CH, Hkv, D), generator=gen, device=dev, dtype=torch.bfloat16)
+    vc = torch.randn((Bc, CH, Hkv, D), generator=gen, device=dev, dtype=torch.bfloat16)
+    od = torch.empty((Bd, 1, Hq * D), device=dev, dtype=torch.bfloat16)
+    oc = torch.empty((Bc, CH, Hq * D), device=dev, dtype=torch.bfloat16)
+    ws = ff.decode_workspace(Bd, Hq, D, table_np.shape[1], device=dev)
+
+    def dec(i):
+        kp, vp, _, _ = pools[i % layers]
+        ff.paged_attention(qd, kp, vp, bt_d, cx_d, out=od, workspace=ws, stream=stream)
+
+    def chunk_append(i):
+        kp, vp, _, _ = pools[i % layers]
+        ff.append_kv_cache(kc, vc, kp, vp, bt_c, cx_c, stream=stream)
+
+    def pre(i):
+        kp, vp, _, _ = pools[i % layers]
+        ff.paged_prefill(qc, kp, vp, bt_c, cx_c, out=oc, stream=stream)
+
+    def step(i):
+        kp, vp, _, _ = pools[i % layers]
+        ff.append_kv_cache(kd, vd, kp, vp, bt_d, cx_d, stream=stream)
+        ff.paged_attention(qd, kp, vp, bt_d, cx_d, out=od, workspace=ws, stream=stream)
+        ff.append_kv_cache(kc, vc, kp, vp, bt_c, cx_c, stream=stream)
+        ff.paged_prefill(qc, kp, vp, bt_c, cx_c, out=oc, stream=stream)
+
+    for i in range(layers):
+        chunk_append(i)  # the chunks' K/V are in the pages before any prefill reads them
+    torch.cuda.synchronize()
+    us_dec = _events_us(dec, calls, stream)
+    us_app = _events_us(chunk_append, calls, stream)
+    us_pre = _events_us(pre, calls, stream)
+    us_step = _events_us(step, calls, stream)
+    Lp = [int(c) + 1 for c in ctx[:Bd]]
+    tok = sum(Lp)
+    other = Bd * Hq * D * 2 * 2 + sum(math.ceil(x / BLOCK) for x in Lp) * 4 + 4 * Bd
+    logical = tok * Hkv * D * 2 * 2 + other
+    unique = (PRE + sum(x - PRE for x in Lp)) * Hkv * D * 2 * 2 + other
+    flops = sum((int(c) + t + 1) * Hq * D * 4 for c in ctx[Bd:] for t in range(CH))
+    app_bytes = append_bytes(Bc * CH, Bc)
+    del pools
+    torch.cuda.empty_cache()
+    return {
+        "workload": "C4 prefix-shared: 128 rows, 2048-token shared prefix (128 shared blocks), suffix U[64,1024]; "
+                    "120 decode rows + 8 rows chunk-prefilling 512 tokens",
+        "step_us": us_step,
+        "decode": {"rows": Bd, "us_per_call": us_dec, "logical_bytes": logical, "unique_bytes": unique,
+                   "unique_TB_per_s": unique / (us_dec * 1e-6) / 1e12,
+                   "unique_pct_of_peak": unique / (us_dec * 1e-6) / 1e12 / HBM_PEAK_TBS * 100,
+                   "effective_TB_per_s_logical": logical / (us_dec * 1e-6) / 1e12},
+        "chunk_append": {"tokens": Bc * CH, "us_per_call": us_app, "bytes": app_bytes,
+                         "GB_per_s": app_bytes / (us_app * 1e-6) / 1e9},
+        "prefill": {"rows": Bc, "chunk": CH, "us_per_call": us_pre, "causal_flops": flops,
+                    "TFLOP_per_s": flops / (us_pre * 1e-6) / 1e12,
+                    "pct_of_bf16_mfma_peak": flops / (us_pre * 1e-6) / 1e12 / BF16_MFMA_PEAK_TFLOPS * 100},
+    }
+
+
+def rope_append_config(ff, torch, dev, stream, calls=50, seed=5):
+    """Fused rotary embedding + KV append: the C2 decode-step shape (64 tokens) and a bulk 64 x 2048 prefill."""
+    import numpy as np
+
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    rng = np.random.default_rng(seed)
+    res = {}
+    for label, S in (("decode_step", 1), ("bulk", 2048)):
+        nb = math.ceil(S / BLOCK) + 1
+        bt = torch.from_numpy(rng.permutation(B * nb).astype(np.int32).reshape(B, nb)).to(dev)
+        ctx = torch.from_numpy(rng.integers(0, BLOCK, size=B).astype(np.int32)).to(dev)
+        q = torch.randn((B, S, HQ, D), generator=gen, device=dev, dtype=torch.bfloat16)
+        k = torch.randn((B, S, HKV, D), generator=gen, device=dev, dtype=torch.bfloat16)
+        v = torch.randn((B, S, HKV, D), generator=gen, device=dev, dtype=torch.bfloat16)
+        kc = torch.empty((B * nb, BLOCK, HKV, D), device=dev, dtype=torch.bfloat16)
+        vc = torch.empty_like(kc)
+        us = _events_us(lambda i: ff.rope_append_kv_cache(q, k, v, kc, vc, bt, ctx, 1e6, stream=stream),
+                        calls if S == 1 else 10, stream)
+        T = B * S
+        # read q, k, v; write q, k back; write the K/V pages; the rows' context_lens and block-table entries
+        nbytes = T * (HQ + 2 * HKV) * D * 2 + T * (HQ + HKV) * D * 2 + T * HKV * D * 2 * 2 + 4 * B + 4 * T
+        res[label] = {"tokens": T, "us_per_call": us, "bytes": nbytes, "GB_per_s": nbytes / (us * 1e-6) / 1e9}
+        del q, k, v, kc, vc
+    torch.cuda.empty_cache()
+    return res
+
+
 def cpu_baseline(ctx, table, N, k_pool, v_pool, q, gpu_out, seconds: float = 10.0):
     """Time the CPU restatement (oracle/) of the decode call on the host cores, on the same inputs as layer 0,
     and return (baseline dict, max-abs error of the GPU output against it)."""
@@ -119,6 +336,8 @@ def main(argv=None) -> int:
     ap.add_argument("--layers", type=int, default=4, help="independent KV pools rotated over the steps")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline time budget (0 = skip)")
     ap.add_argument("--no-bulk", action="store_true", help="skip the bulk-append measurement")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the other BASELINE configurations (C3, C4, C5 int8/fp8) and the rope+append figures")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run one 1 GiB device-to-device copy (a kernel of known read/write bytes, used to "
                          "scale rocprofv3 FETCH_SIZE/WRITE_SIZE counters)")
@@ -222,6 +441,23 @@ def main(argv=None) -> int:
                 "GB_per_s": append_bytes(B * S, B) / (bms * 1e-3) / 1e9}
         del ks, vs, kc, vc
 
+    # The other BASELINE configurations (decode attention alone unless stated), measured the same way.
+    configs = None
+    if not args.no_configs:
+        rng = np.random.default_rng(SEED + 3)
+        configs = {
+            "C3": decode_config(ff, torch, dev, stream, "C3 Qwen2.5-7B layer: Hq28/Hkv4/D128 bf16, B=8, ctx 32768",
+                                8, 28, 4, 128, [32768] * 8, seed=3),
+            "C5_int8": decode_config(ff, torch, dev, stream, "C5 int8 KV (per-token scales): Hq32/Hkv8/D128, B=256, "
+                                     "ctx U[1024,8192]", 256, 32, 8, 128, rng.integers(1024, 8193, size=256),
+                                     kv="i8", seed=5),
+            "C5_fp8": decode_config(ff, torch, dev, stream, "C5 fp8 e4m3 KV (per-head scales): Hq32/Hkv8/D128, B=256, "
+                                    "ctx U[1024,8192]", 256, 32, 8, 128, rng.integers(1024, 8193, size=256),
+                                    kv="fp8", seed=6),
+            "C4": c4_config(ff, torch, dev, stream),
+            "rope_append": rope_append_config(ff, torch, dev, stream),
+        }
+
     # Layer-0 output for the parity figure and the CPU baseline on the same inputs.
     kp0, vp0 = pools[0]
     ff.paged_attention(q, kp0, vp0, table, ctx, out=out, max_context_len=max_ctx, workspace=ws, stream=stream)
@@ -257,6 +493,7 @@ def main(argv=None) -> int:
                      "achieved": achieved * 1e3, "peak": HBM_PEAK_TBS * 1e3, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_TBS, "traffic": measured_traffic(),
                      "algorithmic_bytes": dbytes},
+        "other_configs": configs,
         "cpu_baseline": cpu,
         "parity_max_abs_err_vs_cpu": err,
     }
