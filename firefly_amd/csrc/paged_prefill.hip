@@ -8,21 +8,31 @@
 // block table the K/V are the chunk's contiguous [B, S, Hkv, D] tensors and ctx = 0: exactly the reference's
 // causal prefill.  With S = 1 it is the decode attention.
 //
-// Mapping: a workgroup of four waves serves 64 query rows of one (row b, kv head); a query row is a (token,
+// Mapping: a workgroup of eight waves serves 128 query rows of one (row b, kv head); a query row is a (token,
 // head-in-group) pair, so GQA heads sharing a kv head share every K/V page.  Each wave owns 16 rows as the 16
 // columns of its MFMA tiles, exactly as the decode kernel's columns are the heads of one kv head:
 //   S^T[key, row] = K Q^T with K (16 keys x 32 dims) as the A operand from LDS and Q^T in registers,
-//   online softmax per column (causal limit per column), O^T += V^T P^T with V^T read from LDS and P^T (split
-//   into two 16-bit parts) straight from the score registers.
-// K/V pages are loaded once per workgroup by all 256 threads, converted to the MFMA type (8-bit codes too) and
-// double-buffered in LDS: page p + 1 is in flight while page p is computed, one barrier per page.
+//   online softmax per column (causal limit per column) over a step of pages at a time, O^T += V^T P^T as 16x16x32
+//   products over those 32 keys with V^T read from a transposed LDS tile (8-byte reads) and P^T (split into two
+//   16-bit parts) straight from the score registers.
+// K/V pages are loaded once per workgroup by all its threads, four at a time (two at D = 256), converted to the
+// MFMA type (8-bit codes too) and double-buffered in LDS: the next four pages are in flight while the current
+// four are computed, one barrier per four pages.
 #include "mfma_common.h"
 
 namespace ffkv
 {
 
+#ifndef FFKV_PREFILL_WAVES
+#define FFKV_PREFILL_WAVES 8  // waves per workgroup (16 query rows each)
+#endif
+
+constexpr int kPfWaves = FFKV_PREFILL_WAVES;
+constexpr int kPfThreads = 64 * kPfWaves;
+constexpr int kPfRows = 16 * kPfWaves;  // query rows per workgroup
+
 template <int CT, int QT, int D>
-__global__ __launch_bounds__(256) void paged_prefill_mfma(PrefillArgs a)
+__global__ __launch_bounds__(kPfThreads) void paged_prefill_mfma(PrefillArgs a)
 {
     constexpr bool BF = kBF<CT, QT>;
     using M = MType<BF>;
@@ -31,14 +41,16 @@ __global__ __launch_bounds__(256) void paged_prefill_mfma(PrefillArgs a)
     constexpr int  NT = D / 16;  // output tiles of 16 dims
     constexpr bool NEED_LO = !((QT == BF16 && BF) || (QT == F16 && !BF));
     constexpr bool Q8 = kElemBytes<CT> == 1;
+    constexpr int  KP = D <= 128 ? 4 : 2;       // pages per step (one barrier per step), an even number
+    constexpr int  RS = KP * kBlockSize + 4;    // row stride of the V^T tile (keys, padded against bank conflicts)
     constexpr int  CPT = D / 8;                 // 8-element chunks per key row
     constexpr int  CHUNKS = kBlockSize * CPT;   // chunks per page
-    constexpr int  PER = (CHUNKS + 255) / 256;  // chunks per thread
+    constexpr int  PER = (CHUNKS + kPfThreads - 1) / kPfThreads;  // chunks per thread and page
 
-    __shared__ uint16_t s_k[2][kBlockSize * D];
-    __shared__ uint16_t s_v[2][kBlockSize * D];
-    __shared__ float    s_ks[2][kBlockSize];
-    __shared__ float    s_vs[2][kBlockSize];
+    __shared__ uint16_t s_k[2][KP][kBlockSize * D];  // K rows (swizzled 16-byte chunks)
+    __shared__ uint16_t s_vt[2][D * RS];             // V^T: dim-major, keys of the step's pages contiguous
+    __shared__ float    s_ks[2][KP][kBlockSize];
+    __shared__ float    s_vs[2][KP][kBlockSize];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -52,7 +64,7 @@ __global__ __launch_bounds__(256) void paged_prefill_mfma(PrefillArgs a)
     const int Hq = a.num_heads;
     const int Hkv = a.num_kv_heads;
     const int R = S * G;  // query rows of (b, kvh)
-    const int row0 = blockIdx.x * 64;
+    const int row0 = blockIdx.x * kPfRows;
     if (row0 >= R) return;  // uniform over the workgroup
 
     // keys of the row: L = ctx + S after the chunk's append (clamped); contiguous mode: the chunk only
@@ -71,10 +83,11 @@ __global__ __launch_bounds__(256) void paged_prefill_mfma(PrefillArgs a)
     ke = ke > L ? L : (ke < 0 ? 0 : ke);
     const int kend = col_ok ? static_cast<int>(ke) : 0;
     // pages the workgroup needs: up to its last query row's limit
-    const int r_last = min(row0 + 64, R) - 1;
+    const int r_last = min(row0 + kPfRows, R) - 1;
     int64_t   kw = ctx + r_last / G + 1;
     kw = kw > L ? L : (kw < 0 ? 0 : kw);
     const int  pages = static_cast<int>((kw + kBlockSize - 1) / kBlockSize);
+    const int  steps = (pages + KP - 1) / KP;
     const bool wave_active = row0 + 16 * wave < R;
 
     float kv_scale_log2 = a.scale_log2;
@@ -121,7 +134,7 @@ __global__ __launch_bounds__(256) void paged_prefill_mfma(PrefillArgs a)
         }
     }
 
-    // ---- cooperative page loads ----------------------------------------------------------------------------
+    // ---- cooperative loads of KP pages per step --------------------------------------------------------------
     // Block-table entries come 64 at a time (lane l of every wave: entry tb + l).
     int  tb = 0;
     auto load_tvec = [&](int base) -> int
@@ -132,94 +145,116 @@ __global__ __launch_bounds__(256) void paged_prefill_mfma(PrefillArgs a)
 
     struct Stage
     {
-        u32x4 k[PER];  // 16-bit: 8 elements; 8-bit: codes in .x, .y
-        u32x4 v[PER];
-        float ks, vs;  // int8 scales of key `tid` (threads 0..15)
-        bool  ok;      // page present
+        u32x4 k[KP][PER];  // 16-bit: 8 elements; 8-bit: codes in [0], [1]
+        u32x4 v[KP][PER];
+        float ks[KP], vs[KP];  // int8 scales of key `tid` of each page (threads 0..15)
+        bool  ok[KP];          // page present (and inside the row)
     };
-    auto load_page = [&](int pg, Stage& st)
-    {
-        int  phys = 0;
-        bool ok = true;
-        if (a.paged)
-        {
-            if (pg - tb >= 64)  // uniform
-            {
-                tb += 64;
-                tvec = load_tvec(tb);
-            }
-            phys = __builtin_amdgcn_readlane(tvec, pg - tb);
-            ok = phys >= 0 && phys < a.num_blocks;
-        }
-        st.ok = ok;
-        if (!ok) return;
-#pragma unroll
-        for (int i = 0; i < PER; ++i)
-        {
-            const int e = tid + 256 * i;
-            st.k[i] = u32x4{0u, 0u, 0u, 0u};
-            st.v[i] = u32x4{0u, 0u, 0u, 0u};
-            if (e >= CHUNKS) continue;
-            const int tok = e / CPT, ch = e % CPT;
-            if (pg * kBlockSize + tok >= L) continue;  // past the row's last key (contiguous: no such row)
-            const size_t row = a.paged ? (static_cast<size_t>(phys) * kBlockSize + tok) * Hkv + kvh
-                                       : (static_cast<size_t>(b) * S + pg * kBlockSize + tok) * Hkv + kvh;
-            if constexpr (!Q8)
-            {
-                st.k[i] = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.k_cache) + row * D + 8 * ch);
-                st.v[i] = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.v_cache) + row * D + 8 * ch);
-            }
-            else
-            {
-                const u32x2 kw8 = *reinterpret_cast<const u32x2*>(static_cast<const uint8_t*>(a.k_cache) + row * D + 8 * ch);
-                const u32x2 vw8 = *reinterpret_cast<const u32x2*>(static_cast<const uint8_t*>(a.v_cache) + row * D + 8 * ch);
-                st.k[i] = u32x4{kw8[0], kw8[1], 0u, 0u};
-                st.v[i] = u32x4{vw8[0], vw8[1], 0u, 0u};
-            }
-        }
-        if constexpr (CT == I8)
-        {
-            st.ks = 0.0f;
-            st.vs = 0.0f;
-            if (tid < kBlockSize && pg * kBlockSize + tid < L)
-            {
-                const size_t row = (static_cast<size_t>(phys) * kBlockSize + tid) * Hkv + kvh;
-                st.ks = a.k_scale[row];
-                st.vs = a.v_scale[row];
-            }
-        }
-    };
-    auto store_page = [&](int buf, const Stage& st)
+    auto load_step = [&](int st_i, Stage& st)
     {
 #pragma unroll
-        for (int i = 0; i < PER; ++i)
+        for (int u = 0; u < KP; ++u)
         {
-            const int e = tid + 256 * i;
-            if (e >= CHUNKS) continue;
-            const int tok = e / CPT, ch = e % CPT;
-            u32x4     kw = u32x4{0u, 0u, 0u, 0u}, vw = u32x4{0u, 0u, 0u, 0u};
-            if (st.ok)
+            const int pg = st_i * KP + u;
+            int       phys = 0;
+            bool      ok = pg < pages;
+            if (ok && a.paged)
             {
+                if (pg - tb >= 64)  // uniform
+                {
+                    tb += 64;
+                    tvec = load_tvec(tb);
+                }
+                phys = __builtin_amdgcn_readlane(tvec, pg - tb);
+                ok = phys >= 0 && phys < a.num_blocks;
+            }
+            st.ok[u] = ok;
+#pragma unroll
+            for (int i = 0; i < PER; ++i)
+            {
+                const int e = tid + kPfThreads * i;
+                st.k[u][i] = u32x4{0u, 0u, 0u, 0u};
+                st.v[u][i] = u32x4{0u, 0u, 0u, 0u};
+                if (!ok || e >= CHUNKS) continue;
+                // K: chunk-major (consecutive threads read a token's row contiguously); V: token-major, so the
+                // transposed LDS writes of consecutive threads land on consecutive keys of a V^T row
+                const int ktok = e / CPT, kch = e % CPT;
+                const int vtok = e % kBlockSize, vch = e / kBlockSize;
+                auto      row_of = [&](int tok) -> size_t
+                {
+                    return a.paged ? (static_cast<size_t>(phys) * kBlockSize + tok) * Hkv + kvh
+                                   : (static_cast<size_t>(b) * S + pg * kBlockSize + tok) * Hkv + kvh;
+                };
+                // keys past the row's last one stay zero (contiguous mode: no such row exists)
+                const bool kin = pg * kBlockSize + ktok < L, vin = pg * kBlockSize + vtok < L;
                 if constexpr (!Q8)
                 {
-                    kw = st.k[i];
-                    vw = st.v[i];
+                    if (kin)
+                        st.k[u][i] = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.k_cache) +
+                                                                      row_of(ktok) * D + 8 * kch);
+                    if (vin)
+                        st.v[u][i] = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.v_cache) +
+                                                                      row_of(vtok) * D + 8 * vch);
                 }
                 else
                 {
-                    kw = codes_to_m<CT, BF>(st.k[i][0], st.k[i][1]);
-                    vw = codes_to_m<CT, BF>(st.v[i][0], st.v[i][1]);
+                    if (kin)
+                    {
+                        const u32x2 kw8 = *reinterpret_cast<const u32x2*>(static_cast<const uint8_t*>(a.k_cache) +
+                                                                          row_of(ktok) * D + 8 * kch);
+                        st.k[u][i] = u32x4{kw8[0], kw8[1], 0u, 0u};
+                    }
+                    if (vin)
+                    {
+                        const u32x2 vw8 = *reinterpret_cast<const u32x2*>(static_cast<const uint8_t*>(a.v_cache) +
+                                                                          row_of(vtok) * D + 8 * vch);
+                        st.v[u][i] = u32x4{vw8[0], vw8[1], 0u, 0u};
+                    }
                 }
             }
-            *reinterpret_cast<u32x4*>(&s_k[buf][lds_pos<D>(tok, 8 * ch)]) = kw;
-            *reinterpret_cast<u32x4*>(&s_v[buf][lds_pos<D>(tok, 8 * ch)]) = vw;
-        }
-        if constexpr (CT == I8)
-        {
-            if (tid < kBlockSize)
+            if constexpr (CT == I8)
             {
-                s_ks[buf][tid] = st.ok ? st.ks : 0.0f;
-                s_vs[buf][tid] = st.ok ? st.vs : 0.0f;
+                st.ks[u] = 0.0f;
+                st.vs[u] = 0.0f;
+                if (ok && tid < kBlockSize && pg * kBlockSize + tid < L)
+                {
+                    const size_t row = (static_cast<size_t>(phys) * kBlockSize + tid) * Hkv + kvh;
+                    st.ks[u] = a.k_scale[row];
+                    st.vs[u] = a.v_scale[row];
+                }
+            }
+        }
+    };
+    auto store_step = [&](int buf, const Stage& st)
+    {
+#pragma unroll
+        for (int u = 0; u < KP; ++u)
+        {
+#pragma unroll
+            for (int i = 0; i < PER; ++i)
+            {
+                const int e = tid + kPfThreads * i;
+                if (e >= CHUNKS) continue;
+                const int ktok = e / CPT, kch = e % CPT;
+                const int vtok = e % kBlockSize, vch = e / kBlockSize;
+                u32x4     kw = st.k[u][i], vw = st.v[u][i];
+                if constexpr (Q8)
+                {
+                    kw = codes_to_m<CT, BF>(st.k[u][i][0], st.k[u][i][1]);
+                    vw = codes_to_m<CT, BF>(st.v[u][i][0], st.v[u][i][1]);
+                }
+                *reinterpret_cast<u32x4*>(&s_k[buf][u][lds_pos<D>(ktok, 8 * kch)]) = kw;
+                uint16_t* vt = &s_vt[buf][(8 * vch) * RS + u * kBlockSize + vtok];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) vt[e * RS] = static_cast<uint16_t>(vw[e / 2] >> (16 * (e & 1)));
+            }
+            if constexpr (CT == I8)
+            {
+                if (tid < kBlockSize)
+                {
+                    s_ks[buf][u][tid] = st.ks[u];
+                    s_vs[buf][u][tid] = st.vs[u];
+                }
             }
         }
     };
@@ -231,51 +266,64 @@ __global__ __launch_bounds__(256) void paged_prefill_mfma(PrefillArgs a)
 #pragma unroll
     for (int n = 0; n < NT; ++n) acc[n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    auto compute = [&](int buf, int pg)
+    // Pages u0 and u0 + 1 of a staged step.  The 32 keys form the k-slots of one 16x16x32 PV product: slot
+    // 8g + e holds key 4g + e of page u0 for e < 4 and key 4g + e - 4 of page u0 + 1 otherwise, which is where the
+    // two pages' score tiles leave them in lane (c, g); the V^T operand reads the same keys from the V^T tile.
+    int kaddr[KSTEPS];  // K operand addresses (elements) within a page tile
+#pragma unroll
+    for (int j = 0; j < KSTEPS; ++j) kaddr[j] = lds_pos<D>(c, 32 * j + 8 * g);
+
+    // One staged step of KP pages: the KP score tiles first (independent MFMA chains), one online-softmax update
+    // over the step's 16 * KP keys, then the PV products page pair by page pair.
+    auto compute_step = [&](int buf, int pg0, const bool* okp)
     {
-        const uint16_t* sk = s_k[buf];
-        const uint16_t* sv = s_v[buf];
-        f32x4           s = f32x4{0.0f, 0.0f, 0.0f, 0.0f};  // lane (c, g): keys 4g + i of query row c
+        f32x4 s[KP];
+#pragma unroll
+        for (int u = 0; u < KP; ++u) s[u] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};  // lane (c, g): keys 4g + i, row c
 #pragma unroll
         for (int j = 0; j < KSTEPS; ++j)
         {
-            const X8 kj = __builtin_bit_cast(X8, *reinterpret_cast<const u32x4*>(sk + lds_pos<D>(c, 32 * j + 8 * g)));
-            s = M::mma32(kj, qhi[j], s);
-            if constexpr (NEED_LO) s = M::mma32(kj, qlo[j], s);
-        }
-        float ks[4], vs[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-        {
-            ks[i] = 1.0f;
-            vs[i] = 1.0f;
-            if constexpr (CT == I8)
+            for (int u = 0; u < KP; ++u)
             {
-                ks[i] = s_ks[buf][4 * g + i];
-                vs[i] = s_vs[buf][4 * g + i];
+                const X8 kj = __builtin_bit_cast(X8, *reinterpret_cast<const u32x4*>(s_k[buf][u] + kaddr[j]));
+                s[u] = M::mma32(kj, qhi[j], s[u]);
+                if constexpr (NEED_LO) s[u] = M::mma32(kj, qlo[j], s[u]);
             }
         }
-        float sc[4];
+        float sc[KP * 4];
+        float vs[KP * 4];
         float mt = kNegInf;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int u = 0; u < KP; ++u)
         {
-            const bool vis = pg * kBlockSize + 4 * g + i < kend;  // causal limit of this query row
-            sc[i] = vis ? s[i] * ks[i] * kv_scale_log2 : kNegInf;
-            mt = fmaxf(mt, sc[i]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+            {
+                float ks = 1.0f;
+                vs[4 * u + i] = 1.0f;
+                if constexpr (CT == I8)
+                {
+                    ks = s_ks[buf][u][4 * g + i];
+                    vs[4 * u + i] = s_vs[buf][u][4 * g + i];
+                }
+                const bool vis = okp[u] && (pg0 + u) * kBlockSize + 4 * g + i < kend;  // causal limit
+                sc[4 * u + i] = vis ? s[u][i] * ks * kv_scale_log2 : kNegInf;
+                mt = fmaxf(mt, sc[4 * u + i]);
+            }
         }
         mt = xor_max(mt);
         const float m_new = fmaxf(m_run, mt);
         const float m_use = m_new == kNegInf ? 0.0f : m_new;  // a row with no visible key yet stays empty
         const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
-        float       pv[4];
+        float       pv[KP * 4];
         float       psum = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int e = 0; e < KP * 4; ++e)
         {
-            const float pr = __builtin_amdgcn_exp2f(sc[i] - m_use);
+            const float pr = __builtin_amdgcn_exp2f(sc[e] - m_use);
             psum += pr;
-            pv[i] = pr * vs[i];
+            pv[e] = pr * vs[e];
         }
         l_run = l_run * alpha + psum;
         if (__any(m_new > m_run))
@@ -285,53 +333,69 @@ __global__ __launch_bounds__(256) void paged_prefill_mfma(PrefillArgs a)
         }
         m_run = m_new;
 
-        uint32_t ph[4], pl[4];
+        // Pages u0, u0 + 1 form the 32 k-slots of one 16x16x32 PV product: slot 8g + e holds key 4g + e of page
+        // u0 for e < 4 and key 4g + e - 4 of page u0 + 1 otherwise, where the score tiles leave them in lane
+        // (c, g); the V^T operand reads the same keys from the transposed tile.
+        const uint16_t* vt = s_vt[buf] + c * RS + 4 * g;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int u0 = 0; u0 < KP; u0 += 2)
         {
-            ph[i] = M::bits(pv[i]);
-            pl[i] = M::bits(pv[i] - M::value(ph[i]));
-        }
-        const typename M::x4 phi =
-            __builtin_bit_cast(typename M::x4, u32x2{ph[0] | (ph[1] << 16), ph[2] | (ph[3] << 16)});
-        const typename M::x4 plo =
-            __builtin_bit_cast(typename M::x4, u32x2{pl[0] | (pl[1] << 16), pl[2] | (pl[3] << 16)});
+            uint32_t ph[8], pl[8];
 #pragma unroll
-        for (int n = 0; n < NT; ++n)
-        {
-            const uint32_t v0 = sv[lds_pos<D>(4 * g + 0, 16 * n + c)];
-            const uint32_t v1 = sv[lds_pos<D>(4 * g + 1, 16 * n + c)];
-            const uint32_t v2 = sv[lds_pos<D>(4 * g + 2, 16 * n + c)];
-            const uint32_t v3 = sv[lds_pos<D>(4 * g + 3, 16 * n + c)];
-            const typename M::x4 vt = __builtin_bit_cast(typename M::x4, u32x2{v0 | (v1 << 16), v2 | (v3 << 16)});
-            acc[n] = M::mma16(vt, phi, acc[n]);
-            acc[n] = M::mma16(vt, plo, acc[n]);
+            for (int e = 0; e < 8; ++e)
+            {
+                ph[e] = M::bits(pv[4 * u0 + e]);
+                pl[e] = M::bits(pv[4 * u0 + e] - M::value(ph[e]));
+            }
+            const X8 phi = __builtin_bit_cast(X8, u32x4{ph[0] | (ph[1] << 16), ph[2] | (ph[3] << 16),
+                                                        ph[4] | (ph[5] << 16), ph[6] | (ph[7] << 16)});
+            const X8 plo = __builtin_bit_cast(X8, u32x4{pl[0] | (pl[1] << 16), pl[2] | (pl[3] << 16),
+                                                        pl[4] | (pl[5] << 16), pl[6] | (pl[7] << 16)});
+#pragma unroll
+            for (int n = 0; n < NT; ++n)
+            {
+                const u32x2 a0 = *reinterpret_cast<const u32x2*>(vt + (16 * n) * RS + u0 * kBlockSize);
+                const u32x2 a1 = *reinterpret_cast<const u32x2*>(vt + (16 * n) * RS + (u0 + 1) * kBlockSize);
+                const X8    va = __builtin_bit_cast(X8, u32x4{a0[0], a0[1], a1[0], a1[1]});
+                acc[n] = M::mma32(va, phi, acc[n]);
+                acc[n] = M::mma32(va, plo, acc[n]);
+            }
         }
     };
 
-    // ---- pages 0 .. pages-1, double-buffered -----------------------------------------------------------------
+    // ---- steps of KP pages, double-buffered: step i + 1 in flight while step i is computed -------------------
     Stage st;
-    bool  ok_cur = false;
-    if (pages > 0)
+    bool  ok_cur[KP];
+#pragma unroll
+    for (int u = 0; u < KP; ++u) ok_cur[u] = false;
+    if (steps > 0)
     {
-        load_page(0, st);
-        store_page(0, st);
-        ok_cur = st.ok;
+        load_step(0, st);
+        store_step(0, st);
+#pragma unroll
+        for (int u = 0; u < KP; ++u) ok_cur[u] = st.ok[u];
     }
     __syncthreads();
-    for (int pg = 0; pg < pages; ++pg)
+    for (int si = 0; si < steps; ++si)
     {
-        const int buf = pg & 1;
-        bool      ok_next = false;
-        if (pg + 1 < pages)
+        const int buf = si & 1;
+        bool      ok_next[KP];
+#pragma unroll
+        for (int u = 0; u < KP; ++u) ok_next[u] = false;
+        if (si + 1 < steps)
         {
-            load_page(pg + 1, st);  // in flight while page pg is computed
-            ok_next = st.ok;
+            load_step(si + 1, st);
+#pragma unroll
+            for (int u = 0; u < KP; ++u) ok_next[u] = st.ok[u];
         }
-        if (wave_active && ok_cur) compute(buf, pg);
-        if (pg + 1 < pages) store_page(buf ^ 1, st);  // that buffer was last read before the previous barrier
+        bool any_ok = false;
+#pragma unroll
+        for (int u = 0; u < KP; ++u) any_ok = any_ok || ok_cur[u];
+        if (wave_active && any_ok) compute_step(buf, si * KP, ok_cur);
+        if (si + 1 < steps) store_step(buf ^ 1, st);  // that buffer was last read before the previous barrier
         __syncthreads();
-        ok_cur = ok_next;
+#pragma unroll
+        for (int u = 0; u < KP; ++u) ok_cur[u] = ok_next[u];
     }
 
     if (col_ok)
@@ -351,18 +415,18 @@ template <int CT, int QT>
 hipError_t launch_pf_d(const PrefillArgs& a, hipStream_t stream)
 {
     const int  rows = a.seq_len * a.group;
-    const dim3 grid(static_cast<unsigned>((rows + 63) / 64), static_cast<unsigned>(a.num_kv_heads),
+    const dim3 grid(static_cast<unsigned>((rows + kPfRows - 1) / kPfRows), static_cast<unsigned>(a.num_kv_heads),
                     static_cast<unsigned>(a.batch));
     switch (a.head_dim)
     {
         case 64:
-            hipLaunchKernelGGL((paged_prefill_mfma<CT, QT, 64>), grid, dim3(256), 0, stream, a);
+            hipLaunchKernelGGL((paged_prefill_mfma<CT, QT, 64>), grid, dim3(kPfThreads), 0, stream, a);
             break;
         case 128:
-            hipLaunchKernelGGL((paged_prefill_mfma<CT, QT, 128>), grid, dim3(256), 0, stream, a);
+            hipLaunchKernelGGL((paged_prefill_mfma<CT, QT, 128>), grid, dim3(kPfThreads), 0, stream, a);
             break;
         default:
-            hipLaunchKernelGGL((paged_prefill_mfma<CT, QT, 256>), grid, dim3(256), 0, stream, a);
+            hipLaunchKernelGGL((paged_prefill_mfma<CT, QT, 256>), grid, dim3(kPfThreads), 0, stream, a);
             break;
     }
     return hipGetLastError();
