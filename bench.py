@@ -298,6 +298,54 @@ def rope_append_config(ff, torch, dev, stream, calls=50, seed=5):
     return res
 
 
+def decode_step_config(ff, torch, dev, stream, ctx_np, table_np, N, pools, q, k_new, v_new, out, ws, max_ctx,
+                       calls=50):
+    """The engine's per-step host -> device upload of context lengths and block tables (src/engine.cc:296-322):
+    the reference's layout (row stride = pool blocks, the whole table every step) against the live width only
+    (what firefly::DecodeBatch uploads), from pinned memory; and the C2 append + decode step replayed from one
+    captured hipGraph against eager launches."""
+    import numpy as np
+
+    Bn = len(ctx_np)
+    res = {}
+    for label, stride in (("reference_layout", N), ("live_width", table_np.shape[1])):
+        h = torch.full((Bn, stride), -1, dtype=torch.int32).pin_memory()
+        h[:, :table_np.shape[1]] = torch.from_numpy(table_np)
+        hc = torch.from_numpy(ctx_np.astype(np.int32)).pin_memory()
+        d = torch.empty((Bn, stride), dtype=torch.int32, device=dev)
+        dc = torch.empty(Bn, dtype=torch.int32, device=dev)
+
+        def up(i):
+            dc.copy_(hc, non_blocking=True)
+            d.copy_(h, non_blocking=True)
+
+        us = _events_us(up, calls, stream)
+        res[label] = {"row_stride_blocks": stride, "bytes": Bn * stride * 4 + Bn * 4, "us_per_step": us}
+        del h, d
+    table = torch.from_numpy(table_np).to(dev)
+    cx = torch.from_numpy(ctx_np.astype(np.int32)).to(dev)
+    L = len(pools)
+
+    def step(i, s=stream):
+        kp, vp = pools[i % L]
+        ff.append_kv_cache(k_new, v_new, kp, vp, table, cx, stream=s)
+        ff.paged_attention(q, kp, vp, table, cx, out=out, max_context_len=max_ctx, workspace=ws, stream=s)
+
+    eager = _events_us(step, calls, stream)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(g, stream=side):
+            for i in range(L):
+                step(i, torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    graph = _events_us(lambda i: g.replay(), max(1, calls // L), stream) / L
+    res["step_us_eager"] = eager
+    res["step_us_graph"] = graph
+    return res
+
+
 def cpu_baseline(ctx, table, N, k_pool, v_pool, q, gpu_out, seconds: float = 10.0):
     """Time the CPU restatement (oracle/) of the decode call on the host cores, on the same inputs as layer 0,
     and return (baseline dict, max-abs error of the GPU output against it)."""
@@ -456,6 +504,8 @@ def main(argv=None) -> int:
                                     kv="fp8", seed=6),
             "C4": c4_config(ff, torch, dev, stream),
             "rope_append": rope_append_config(ff, torch, dev, stream),
+            "C2_decode_step_host": decode_step_config(ff, torch, dev, stream, ctx_np, table_np, N, pools, q, k_new,
+                                                      v_new, out, ws, max_ctx),
         }
 
     # Layer-0 output for the parity figure and the CPU baseline on the same inputs.

@@ -73,16 +73,18 @@ def build_library(jobs: int = 8) -> Path:
 
 
 def build_test_shims() -> None:
-    """Test-only helpers linked against libffkv.so: the C++-API shim used by tests/test_gpu_cxx_api.py."""
-    src = ROOT / "tests" / "cpp" / "kernels_api_shim.cpp"
-    if not src.exists():
-        return
-    out = ROOT / "tests" / "cpp" / "libkernels_api_shim.so"
-    cmd = [HIPCC, "-O2", "-std=c++20", "-fPIC", "-shared", f"-I{ROOT / 'include'}", str(src), "-o", str(out),
-           f"-L{PKG}", "-lffkv", "-Wl,-rpath,$ORIGIN/../../firefly_amd"]
-    res = subprocess.run(cmd, capture_output=True, text=True)
-    if res.returncode != 0:
-        raise RuntimeError(f"test shim build failed: {' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
+    """Test-only helpers linked against libffkv.so: the C++-API shims under tests/cpp/ (kernels_api_shim.cpp for
+    tests/test_gpu_cxx_api.py, decode_step_shim.cpp for tests/test_gpu_decode_step.py)."""
+    for name in ("kernels_api_shim", "decode_step_shim"):
+        src = ROOT / "tests" / "cpp" / f"{name}.cpp"
+        if not src.exists():
+            continue
+        out = ROOT / "tests" / "cpp" / f"lib{name}.so"
+        cmd = [HIPCC, "-O2", "-std=c++20", "-fPIC", "-shared", f"-I{ROOT / 'include'}", str(src), "-o", str(out),
+               f"-L{PKG}", "-lffkv", "-Wl,-rpath,$ORIGIN/../../firefly_amd"]
+        res = subprocess.run(cmd, capture_output=True, text=True)
+        if res.returncode != 0:
+            raise RuntimeError(f"test shim build failed: {' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
 
 
 def build_oracle() -> None:

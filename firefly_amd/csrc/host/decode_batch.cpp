@@ -1,0 +1,192 @@
+// decode_batch.cpp - decode-step packing (DecodeBatch) and HIP graph capture (hal::Graph).
+//
+// Packing follows src/engine.cc:296-312 (slot i <- request i's context_len and block_table, other slots padded
+// with context_len 0 and block -1); the upload copies only the rows' live width instead of the whole
+// pool-stride table (src/engine.cc:317-322).  Graph follows include/firefly/hal/graph.h:54-120.
+#include "firefly/decode_batch.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstring>
+
+#include "firefly/hal/graph.h"
+
+namespace firefly
+{
+
+DecodeBatch::DecodeBatch(int batch_capacity, int max_context_blocks)
+    : capacity_(batch_capacity > 0 ? batch_capacity : 0), stride_(max_context_blocks > 0 ? max_context_blocks : 0)
+{
+    if (capacity_ == 0 || stride_ == 0) return;
+    const size_t table = static_cast<size_t>(capacity_) * stride_ * sizeof(int32_t);
+    const size_t lens = static_cast<size_t>(capacity_) * sizeof(int32_t);
+    if (hipHostMalloc(reinterpret_cast<void**>(&h_context_lens_), lens, hipHostMallocDefault) != hipSuccess ||
+        hipHostMalloc(reinterpret_cast<void**>(&h_block_table_), table, hipHostMallocDefault) != hipSuccess ||
+        hipMalloc(reinterpret_cast<void**>(&d_context_lens_), lens) != hipSuccess ||
+        hipMalloc(reinterpret_cast<void**>(&d_block_table_), table) != hipSuccess)
+    {
+        release();
+        return;
+    }
+    // A padded table everywhere before the first upload, and device buffers that hold it from the start.
+    std::fill(h_context_lens_, h_context_lens_ + capacity_, 0);
+    std::fill(h_block_table_, h_block_table_ + static_cast<size_t>(capacity_) * stride_, -1);
+    (void)hipMemcpy(d_context_lens_, h_context_lens_, lens, hipMemcpyHostToDevice);
+    (void)hipMemcpy(d_block_table_, h_block_table_, table, hipMemcpyHostToDevice);
+}
+
+DecodeBatch::~DecodeBatch() { release(); }
+
+void DecodeBatch::release()
+{
+    if (d_block_table_) (void)hipFree(d_block_table_);
+    if (d_context_lens_) (void)hipFree(d_context_lens_);
+    if (h_block_table_) (void)hipHostFree(h_block_table_);
+    if (h_context_lens_) (void)hipHostFree(h_context_lens_);
+    d_block_table_ = d_context_lens_ = h_block_table_ = h_context_lens_ = nullptr;
+}
+
+int DecodeBatch::pack(const std::vector<const GenerationRequest*>& requests)
+{
+    if (!ok() || static_cast<int>(requests.size()) > capacity_) return -1;
+    int width = 1;
+    for (const GenerationRequest* r : requests)
+    {
+        if (r == nullptr || static_cast<int>(r->block_table.size()) > stride_) return -1;
+        width = std::max(width, static_cast<int>(r->block_table.size()));
+    }
+    for (int i = 0; i < capacity_; ++i)
+    {
+        int32_t* row = h_block_table_ + static_cast<size_t>(i) * stride_;
+        if (i < static_cast<int>(requests.size()))
+        {
+            const GenerationRequest* r = requests[i];
+            h_context_lens_[i] = r->context_len;
+            const int n = static_cast<int>(r->block_table.size());
+            std::copy(r->block_table.begin(), r->block_table.end(), row);
+            std::fill(row + n, row + width, -1);
+        }
+        else
+        {
+            h_context_lens_[i] = 0;
+            std::fill(row, row + width, -1);
+        }
+    }
+    rows_ = static_cast<int>(requests.size());
+    width_ = width;
+    return width;
+}
+
+bool DecodeBatch::upload(hipStream_t stream)
+{
+    if (!ok()) return false;
+    const size_t pitch = static_cast<size_t>(stride_) * sizeof(int32_t);
+    if (hipMemcpyAsync(d_context_lens_, h_context_lens_, static_cast<size_t>(capacity_) * sizeof(int32_t),
+                       hipMemcpyHostToDevice, stream) != hipSuccess)
+        return false;
+    if (hipMemcpy2DAsync(d_block_table_, pitch, h_block_table_, pitch, static_cast<size_t>(width_) * sizeof(int32_t),
+                         static_cast<size_t>(capacity_), hipMemcpyHostToDevice, stream) != hipSuccess)
+        return false;
+    last_bytes_ = static_cast<size_t>(capacity_) * sizeof(int32_t) +
+                  static_cast<size_t>(capacity_) * width_ * sizeof(int32_t);
+    return true;
+}
+
+namespace hal
+{
+
+Graph::~Graph() { destroy(); }
+
+Graph::Graph(Graph&& other) noexcept : graph_(other.graph_), exec_(other.exec_), error_(std::move(other.error_))
+{
+    other.graph_ = nullptr;
+    other.exec_ = nullptr;
+}
+
+Graph& Graph::operator=(Graph&& other) noexcept
+{
+    if (this != &other)
+    {
+        destroy();
+        graph_ = other.graph_;
+        exec_ = other.exec_;
+        error_ = std::move(other.error_);
+        other.graph_ = nullptr;
+        other.exec_ = nullptr;
+    }
+    return *this;
+}
+
+void Graph::destroy()
+{
+    if (exec_) (void)hipGraphExecDestroy(exec_);
+    if (graph_) (void)hipGraphDestroy(graph_);
+    exec_ = nullptr;
+    graph_ = nullptr;
+}
+
+bool Graph::capture(hipStream_t stream, const std::function<void()>& fn)
+{
+    destroy();
+    error_.clear();
+    hipError_t e = hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal);
+    if (e != hipSuccess)
+    {
+        error_ = std::string("hipStreamBeginCapture: ") + hipGetErrorString(e);
+        return false;
+    }
+    try
+    {
+        fn();
+    }
+    catch (const std::exception& ex)
+    {
+        (void)hipStreamEndCapture(stream, &graph_);
+        destroy();
+        error_ = std::string("exception during graph capture: ") + ex.what();
+        return false;
+    }
+    catch (...)
+    {
+        (void)hipStreamEndCapture(stream, &graph_);
+        destroy();
+        error_ = "unknown exception during graph capture";
+        return false;
+    }
+    e = hipStreamEndCapture(stream, &graph_);
+    if (e != hipSuccess)
+    {
+        destroy();
+        error_ = std::string("hipStreamEndCapture: ") + hipGetErrorString(e);
+        return false;
+    }
+    e = hipGraphInstantiate(&exec_, graph_, nullptr, nullptr, 0);
+    if (e != hipSuccess)
+    {
+        destroy();
+        error_ = std::string("hipGraphInstantiate: ") + hipGetErrorString(e);
+        return false;
+    }
+    return true;
+}
+
+bool Graph::launch(hipStream_t stream) const
+{
+    if (!exec_)
+    {
+        error_ = "Graph: nothing captured";
+        return false;
+    }
+    const hipError_t e = hipGraphLaunch(exec_, stream);
+    if (e != hipSuccess)
+    {
+        error_ = std::string("hipGraphLaunch: ") + hipGetErrorString(e);
+        return false;
+    }
+    return true;
+}
+
+}  // namespace hal
+
+}  // namespace firefly
