@@ -17,12 +17,18 @@
 //     XOR-swizzled per token, so both the 16-byte row writes and the transposing column reads are free of bank
 //     conflicts while every row stays 16-byte aligned.
 //     P is split into hi + lo parts of the MFMA input type, so the products carry ~16 significant bits.
-//   * quantized caches: int8 and fp8 e4m3 codes convert exactly to f16 for the MFMA; int8 per-token K scales
-//     multiply the scores and V scales multiply P, fp8 per-head scales fold into the score scale and the output.
+//   * quantized caches: int8 and fp8 e4m3 codes convert exactly to the MFMA input type when a page is staged
+//     (fp8 with the gfx950 conversion instructions, int8 with byte permutes and packed f16 ops); int8 per-token
+//     K scales multiply the scores and V scales multiply P, fp8 per-head scales fold into the score scale and
+//     the output.
 //   * work split: the pages of all rows form one sequence; work item i of W takes pages
 //     [i*P/W, (i+1)*P/W), so every wave gets the same number of pages whatever the row lengths (no tail of
 //     long rows).  A row covered by one item writes its output directly; otherwise each piece writes an
 //     unnormalised partial (m, l, acc) to slot item + row and paged_decode_mfma_merge combines them.
+//   * streaming: a load cursor runs DEPTH pages ahead of the page being finished, across row boundaries.  Rows
+//     are found with ballots over windows of 64 rows held one per lane (one vector load of context_lens per
+//     window), block-table entries come 64 per vector load, and the next row's Q is loaded as soon as the last
+//     page of a row has been scored, so a wave never waits on a dependent scalar load between pages.
 #include "mfma_common.h"
 
 #ifndef FFKV_MFMA_MAX_WAVES
