@@ -27,12 +27,20 @@ namespace ffkv
 #define FFKV_PREFILL_WAVES 8  // waves per workgroup (16 query rows each)
 #endif
 
+#ifndef FFKV_PREFILL_KP
+#define FFKV_PREFILL_KP 2  // pages per step at head_dim <= 128
+#endif
+
+#ifndef FFKV_PREFILL_DMA
+#define FFKV_PREFILL_DMA 1  // 16-bit caches take paged_prefill_dma (global->LDS loads, transposed LDS reads)
+#endif
 constexpr int kPfWaves = FFKV_PREFILL_WAVES;
 constexpr int kPfThreads = 64 * kPfWaves;
 constexpr int kPfRows = 16 * kPfWaves;  // query rows per workgroup
 
 template <int CT, int QT, int D>
-__global__ __launch_bounds__(kPfThreads) void paged_prefill_mfma(PrefillArgs a)
+__global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 4 : 1)))
+void paged_prefill_mfma(PrefillArgs a)
 {
     constexpr bool BF = kBF<CT, QT>;
     using M = MType<BF>;
@@ -41,11 +49,10 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_mfma(PrefillArgs a)
     constexpr int  NT = D / 16;  // output tiles of 16 dims
     constexpr bool NEED_LO = !((QT == BF16 && BF) || (QT == F16 && !BF));
     constexpr bool Q8 = kElemBytes<CT> == 1;
-    constexpr int  KP = D <= 128 ? 4 : 2;       // pages per step (one barrier per step), an even number
+    constexpr int  KP = D <= 128 ? FFKV_PREFILL_KP : 2;  // pages per step (one barrier per step), an even number
     constexpr int  RS = KP * kBlockSize + 4;    // row stride of the V^T tile (keys, padded against bank conflicts)
     constexpr int  CPT = D / 8;                 // 8-element chunks per key row
     constexpr int  CHUNKS = kBlockSize * CPT;   // chunks per page
-    constexpr int  PER = (CHUNKS + kPfThreads - 1) / kPfThreads;  // chunks per thread and page
 
     __shared__ uint16_t s_k[2][KP][kBlockSize * D];  // K rows (swizzled 16-byte chunks)
     __shared__ uint16_t s_vt[2][D * RS];             // V^T: dim-major, keys of the step's pages contiguous
@@ -143,10 +150,13 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_mfma(PrefillArgs a)
     };
     int tvec = a.paged ? load_tvec(0) : -1;
 
+    // Each page is 2 * CHUNKS 16-byte units (K chunks, then V chunks); thread tid stages units tid, tid + threads,
+    // ... of every page of a step, so with 8 waves at D = 128 waves 0-3 carry K and waves 4-7 carry V.
+    constexpr int UNITS = 2 * CHUNKS;
+    constexpr int PU = (UNITS + kPfThreads - 1) / kPfThreads;  // units per thread and page
     struct Stage
     {
-        u32x4 k[KP][PER];  // 16-bit: 8 elements; 8-bit: codes in [0], [1]
-        u32x4 v[KP][PER];
+        u32x4 w[KP][PU];       // 16-bit: 8 elements; 8-bit: codes in [0], [1]
         float ks[KP], vs[KP];  // int8 scales of key `tid` of each page (threads 0..15)
         bool  ok[KP];          // page present (and inside the row)
     };
@@ -170,46 +180,29 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_mfma(PrefillArgs a)
             }
             st.ok[u] = ok;
 #pragma unroll
-            for (int i = 0; i < PER; ++i)
+            for (int i = 0; i < PU; ++i)
             {
                 const int e = tid + kPfThreads * i;
-                st.k[u][i] = u32x4{0u, 0u, 0u, 0u};
-                st.v[u][i] = u32x4{0u, 0u, 0u, 0u};
-                if (!ok || e >= CHUNKS) continue;
+                st.w[u][i] = u32x4{0u, 0u, 0u, 0u};
+                if (!ok || e >= UNITS) continue;
                 // K: chunk-major (consecutive threads read a token's row contiguously); V: token-major, so the
                 // transposed LDS writes of consecutive threads land on consecutive keys of a V^T row
-                const int ktok = e / CPT, kch = e % CPT;
-                const int vtok = e % kBlockSize, vch = e / kBlockSize;
-                auto      row_of = [&](int tok) -> size_t
-                {
-                    return a.paged ? (static_cast<size_t>(phys) * kBlockSize + tok) * Hkv + kvh
-                                   : (static_cast<size_t>(b) * S + pg * kBlockSize + tok) * Hkv + kvh;
-                };
-                // keys past the row's last one stay zero (contiguous mode: no such row exists)
-                const bool kin = pg * kBlockSize + ktok < L, vin = pg * kBlockSize + vtok < L;
+                const bool  is_k = e < CHUNKS;
+                const int   f = is_k ? e : e - CHUNKS;
+                const int   tok = is_k ? f / CPT : f % kBlockSize;
+                const int   ch = is_k ? f % CPT : f / kBlockSize;
+                const void* base = is_k ? a.k_cache : a.v_cache;
+                if (pg * kBlockSize + tok >= L) continue;  // past the row's last key (contiguous: no such row)
+                const size_t row = a.paged ? (static_cast<size_t>(phys) * kBlockSize + tok) * Hkv + kvh
+                                           : (static_cast<size_t>(b) * S + pg * kBlockSize + tok) * Hkv + kvh;
                 if constexpr (!Q8)
                 {
-                    if (kin)
-                        st.k[u][i] = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.k_cache) +
-                                                                      row_of(ktok) * D + 8 * kch);
-                    if (vin)
-                        st.v[u][i] = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.v_cache) +
-                                                                      row_of(vtok) * D + 8 * vch);
+                    st.w[u][i] = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(base) + row * D + 8 * ch);
                 }
                 else
                 {
-                    if (kin)
-                    {
-                        const u32x2 kw8 = *reinterpret_cast<const u32x2*>(static_cast<const uint8_t*>(a.k_cache) +
-                                                                          row_of(ktok) * D + 8 * kch);
-                        st.k[u][i] = u32x4{kw8[0], kw8[1], 0u, 0u};
-                    }
-                    if (vin)
-                    {
-                        const u32x2 vw8 = *reinterpret_cast<const u32x2*>(static_cast<const uint8_t*>(a.v_cache) +
-                                                                          row_of(vtok) * D + 8 * vch);
-                        st.v[u][i] = u32x4{vw8[0], vw8[1], 0u, 0u};
-                    }
+                    const u32x2 w8 = *reinterpret_cast<const u32x2*>(static_cast<const uint8_t*>(base) + row * D + 8 * ch);
+                    st.w[u][i] = u32x4{w8[0], w8[1], 0u, 0u};
                 }
             }
             if constexpr (CT == I8)
@@ -231,22 +224,24 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_mfma(PrefillArgs a)
         for (int u = 0; u < KP; ++u)
         {
 #pragma unroll
-            for (int i = 0; i < PER; ++i)
+            for (int i = 0; i < PU; ++i)
             {
                 const int e = tid + kPfThreads * i;
-                if (e >= CHUNKS) continue;
-                const int ktok = e / CPT, kch = e % CPT;
-                const int vtok = e % kBlockSize, vch = e / kBlockSize;
-                u32x4     kw = st.k[u][i], vw = st.v[u][i];
-                if constexpr (Q8)
+                if (e >= UNITS) continue;
+                const bool is_k = e < CHUNKS;
+                const int  f = is_k ? e : e - CHUNKS;
+                u32x4      w = st.w[u][i];
+                if constexpr (Q8) w = codes_to_m<CT, BF>(st.w[u][i][0], st.w[u][i][1]);
+                if (is_k)
                 {
-                    kw = codes_to_m<CT, BF>(st.k[u][i][0], st.k[u][i][1]);
-                    vw = codes_to_m<CT, BF>(st.v[u][i][0], st.v[u][i][1]);
+                    *reinterpret_cast<u32x4*>(&s_k[buf][u][lds_pos<D>(f / CPT, 8 * (f % CPT))]) = w;
                 }
-                *reinterpret_cast<u32x4*>(&s_k[buf][u][lds_pos<D>(ktok, 8 * kch)]) = kw;
-                uint16_t* vt = &s_vt[buf][(8 * vch) * RS + u * kBlockSize + vtok];
+                else
+                {
+                    uint16_t* vt = &s_vt[buf][(8 * (f / kBlockSize)) * RS + u * kBlockSize + f % kBlockSize];
 #pragma unroll
-                for (int e = 0; e < 8; ++e) vt[e * RS] = static_cast<uint16_t>(vw[e / 2] >> (16 * (e & 1)));
+                    for (int e2 = 0; e2 < 8; ++e2) vt[e2 * RS] = static_cast<uint16_t>(w[e2 / 2] >> (16 * (e2 & 1)));
+                }
             }
             if constexpr (CT == I8)
             {
@@ -450,6 +445,9 @@ hipError_t launch_pf_q(const PrefillArgs& a, hipStream_t stream)
 
 hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream)
 {
+#if FFKV_PREFILL_DMA
+    if (a.cache_dtype == F16 || a.cache_dtype == BF16) return launch_prefill_dma(a, stream);
+#endif
     switch (a.cache_dtype)
     {
         case F16:

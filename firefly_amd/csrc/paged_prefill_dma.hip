@@ -1,0 +1,416 @@
+// paged_prefill_dma.hip - chunked / paged prefill attention over 16-bit (f16 / bf16) caches on gfx950, with the
+// K/V pages streamed into LDS by asynchronous global->LDS loads.
+//
+// Same contract and arithmetic as paged_prefill_mfma (paged_prefill.hip), which replaces the reference's prefill
+// branch of kernels::attention (flash_attn_wmma_kernel, src/kernels/attention.cu:22-286, dispatched at :460-474)
+// and extends it to queries over a cached prefix: query token t of row b at position ctx[b] + t attends keys
+// 0 .. ctx[b] + t; without a block table the keys are the chunk's contiguous [B, S, Hkv, D] tensors (ctx = 0).
+//
+// What differs is how pages reach LDS.  16-bit pages need no conversion, so every 16-byte chunk of a step's K and
+// V pages goes from HBM straight into LDS with global_load_lds_dwordx4 (each lane's 16 bytes land at the
+// instruction's LDS base + 16 * lane), with no staging registers and no LDS stores by the waves.  Three stages
+// rotate: step i + 2 is requested as soon as every wave has finished step i - 1, so two steps of loads are in
+// flight behind the step being computed, with one barrier per step.  Each stage is its own LDS object and the
+// main loop is unrolled by three, so the compiler can tell which stage a load writes and does not hold the
+// compute of one stage behind the loads into another.
+//
+// Both tiles stay row-major (key-major).  The K operand of S^T = K Q^T reads 8 consecutive dims of one key as
+// before; the V^T operand of O^T += V^T P^T needs 8 consecutive keys of one dim, which ds_read_b64_tr_b16 gives
+// directly: within each 16-lane group, lane 4r + q supplies the address of dims 4q .. 4q + 3 of key row r, and
+// lane j receives dim j of rows 0..3.  16-byte chunks of a key row are XOR-swizzled by row so that neither the
+// K reads (16 rows, one chunk) nor the transposed V reads (4 rows, two chunks per 16-lane group) collide in LDS
+// banks; the loads apply the same swizzle by choosing which chunk each lane fetches.
+//
+// Keys past the row's end and keys on invalid pages are fetched from a zero block instead, so masked keys meet
+// zero V rows (their probabilities are exactly zero) and no lane reads outside the cache.
+#include "mfma_common.h"
+
+namespace ffkv
+{
+
+namespace
+{
+
+constexpr int kDmaWaves = 8;
+constexpr int kDmaThreads = 64 * kDmaWaves;
+constexpr int kDmaRows = 16 * kDmaWaves;  // query rows per workgroup
+constexpr int kDmaStages = 3;
+
+#ifndef FFKV_PREFILL_DMA_KP128
+#define FFKV_PREFILL_DMA_KP128 2  // pages per step at head_dim 128
+#endif
+
+#define FFKV_LDS __attribute__((address_space(3)))
+#define FFKV_CONST __attribute__((address_space(4)))  // read-only for the kernel's lifetime: scalar loads
+
+// Source of the chunks of keys that are not loaded: 64 lanes x 16 bytes of zeros (never written).
+__device__ __align__(16) uint32_t g_zero_chunks[256];
+
+template <int D>
+struct DmaCfg
+{
+    static constexpr int KP = D == 64 ? 4 : (D == 128 ? FFKV_PREFILL_DMA_KP128 : 2);  // pages per step
+    static constexpr int CPT = D / 8;                                                  // chunks per key row
+    static constexpr int CHUNKS = kBlockSize * CPT;                                    // chunks per page
+    static constexpr int TILE = KP * kBlockSize * D;          // elements of a step's K (or V) tile
+    static constexpr int IPR = KP * CHUNKS / 64;              // load instructions per tile
+    static constexpr int IPW = IPR / kDmaWaves;               // K (and V) load instructions per wave and step
+    static_assert(IPW >= 1 && IPR % kDmaWaves == 0, "every wave loads whole 64-chunk runs of K and of V");
+    static_assert(CHUNKS % 64 == 0, "a 64-chunk run stays inside one page");
+};
+
+// Chunk swizzle of a V row: rows 4g .. 4g + 3 (one transposed read) and the neighbouring four rows put the two
+// chunks a 16-dim tile needs on distinct banks.  Even values only, so the two chunks of a tile stay adjacent.
+template <int D>
+__device__ __forceinline__ int v_swizzle(int t)
+{
+    return D == 64 ? 2 * ((t >> 1) & 3) : 2 * (t & 7);
+}
+
+// K swizzle: the same row permutation as lds_pos<D>.
+__device__ __forceinline__ int k_swizzle(int t)
+{
+    return (t & 7) ^ ((t >> 3) << 1);
+}
+
+// One 16-byte global -> LDS load per lane: lane l's 16 bytes from `src` land at LDS address `dst` + 16 * l (dst
+// uniform).  Issued as inline assembly so the compiler does not track it: its own waits would otherwise hold
+// every LDS read behind every load in flight, whichever stage it writes.  The kernel waits for these loads
+// itself (wait_vm) before the barrier that publishes a stage, and M0 is used by nothing else in the kernel.
+__device__ __forceinline__ void load_lds16(const void* src, const FFKV_LDS void* dst)
+{
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
+                 :
+                 : "v"(src), "s"(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(dst)))
+                 : "memory", "m0");
+#pragma clang diagnostic pop
+}
+
+template <int VM>
+__device__ __forceinline__ void wait_vm()
+{
+    static_assert(VM >= 0 && VM < 16, "vmcnt field");
+    __builtin_amdgcn_s_waitcnt(VM | (0x7 << 4) | (0xF << 8));  // vmcnt(VM), expcnt and lgkmcnt not waited on
+}
+
+}  // namespace
+
+template <int QT, int D, bool BF>
+__global__ __launch_bounds__(kDmaThreads) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 4 : 1)))
+void paged_prefill_dma(PrefillArgs a)
+{
+    using C = DmaCfg<D>;
+    using M = MType<BF>;
+    using X8 = typename M::x8;
+    constexpr int  KP = C::KP;
+    constexpr int  KSTEPS = D / 32;
+    constexpr int  NT = D / 16;
+    constexpr bool NEED_LO = !((QT == BF16 && BF) || (QT == F16 && !BF));
+
+    // three stages, each [K tile | V tile] of KP pages, key-major with swizzled chunks
+    __shared__ __align__(16) uint16_t s_st0[2 * C::TILE];
+    __shared__ __align__(16) uint16_t s_st1[2 * C::TILE];
+    __shared__ __align__(16) uint16_t s_st2[2 * C::TILE];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int c = lane & 15;
+    const int g = lane >> 4;
+    const int b = blockIdx.z;
+    const int kvh = blockIdx.y;
+    const int G = a.group;
+    const int S = a.seq_len;
+    const int Hq = a.num_heads;
+    const int Hkv = a.num_kv_heads;
+    const int R = S * G;
+    const int row0 = blockIdx.x * kDmaRows;
+    if (row0 >= R) return;  // uniform over the workgroup
+
+    const int64_t ctx = a.paged ? static_cast<int64_t>(a.context_lens[b]) : 0;
+    int64_t       Lr = ctx + S;
+    if (a.paged && Lr > a.cap_tokens) Lr = a.cap_tokens;
+    if (Lr < 0) Lr = 0;
+    const int L = static_cast<int>(Lr);
+
+    const int  r = row0 + 16 * wave + c;
+    const bool col_ok = r < R;
+    const int  t = col_ok ? r / G : 0;
+    const int  h = kvh * G + (col_ok ? r % G : 0);
+    int64_t    ke = ctx + t + 1;
+    ke = ke > L ? L : (ke < 0 ? 0 : ke);
+    const int     kend = col_ok ? static_cast<int>(ke) : 0;
+    const int     r_last = min(row0 + kDmaRows, R) - 1;
+    int64_t       kw = ctx + r_last / G + 1;
+    kw = kw > L ? L : (kw < 0 ? 0 : kw);
+    const int  pages = static_cast<int>((kw + kBlockSize - 1) / kBlockSize);
+    const int  steps = (pages + KP - 1) / KP;
+    const bool wave_active = row0 + 16 * wave < R;
+
+    // ---- Q^T operands of the wave's 16 query rows ----------------------------------------------------------
+    X8           qhi[KSTEPS], qlo[KSTEPS];
+    const size_t qrow = (static_cast<size_t>(b) * S + t) * Hq + h;
+#pragma unroll
+    for (int j = 0; j < KSTEPS; ++j)
+    {
+        const int d0 = 32 * j + 8 * g;
+        if constexpr (!NEED_LO)
+        {
+            u32x4 w = u32x4{0u, 0u, 0u, 0u};
+            if (col_ok) w = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.q) + qrow * D + d0);
+            qhi[j] = __builtin_bit_cast(X8, w);
+            qlo[j] = qhi[j];
+        }
+        else
+        {
+            float x[8];
+            if (col_ok)
+                load_q8<QT>(a.q, qrow * D + d0, x);
+            else
+#pragma unroll
+                for (int e = 0; e < 8; ++e) x[e] = 0.0f;
+            uint32_t hi[8], lo[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+            {
+                hi[e] = M::bits(x[e]);
+                lo[e] = M::bits(x[e] - M::value(hi[e]));
+            }
+            qhi[j] = __builtin_bit_cast(X8, u32x4{hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16), hi[4] | (hi[5] << 16),
+                                                  hi[6] | (hi[7] << 16)});
+            qlo[j] = __builtin_bit_cast(X8, u32x4{lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16), lo[4] | (lo[5] << 16),
+                                                  lo[6] | (lo[7] << 16)});
+        }
+    }
+
+    // Nothing else is in flight from here on but the page loads: the pipeline's waits count only those.
+    wait_vm<0>();
+
+    // ---- loads: wave w fetches runs w*IPW .. w*IPW + IPW - 1 (64 chunks each) of the K tile and of the V tile --
+    const FFKV_CONST int32_t* table_row =
+        a.paged ? (const FFKV_CONST int32_t*)(a.block_table + static_cast<int64_t>(b) * a.max_blocks) : nullptr;
+    const uint16_t* zero_src = reinterpret_cast<const uint16_t*>(g_zero_chunks) + 8 * lane;
+    // Returns the step's page mask (bit u: page si * KP + u is present); keys on absent pages are masked.  The
+    // block-table entries are uniform over the workgroup and come through the scalar cache.
+    auto issue = [&](int si, uint16_t* stage) -> int
+    {
+        int okm = 0;
+        int phys[KP];
+#pragma unroll
+        for (int u = 0; u < KP; ++u)
+        {
+            const int pg = si * KP + u;
+            phys[u] = 0;
+            if (pg < pages)  // pages <= max_blocks
+            {
+                if (a.paged)
+                {
+                    phys[u] = table_row[pg];
+                    if (phys[u] >= 0 && phys[u] < a.num_blocks) okm |= 1 << u;
+                }
+                else
+                {
+                    okm |= 1 << u;
+                }
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < 2 * C::IPW; ++k)
+        {
+            const bool      is_v = k >= C::IPW;
+            const int       run = wave * C::IPW + (is_v ? k - C::IPW : k);  // 64-chunk run within the tile
+            const int       u = run * 64 / C::CHUNKS;                         // page of the step (uniform)
+            const int       p = run * 64 % C::CHUNKS + lane;                  // chunk position within the page
+            const int       tok = p / C::CPT;
+            const int       ch = (p % C::CPT) ^ (is_v ? v_swizzle<D>(tok) : k_swizzle(tok));
+            const int       pg = si * KP + u;
+            const void*     base = is_v ? a.v_cache : a.k_cache;
+            const size_t    row = a.paged ? (static_cast<size_t>(phys[u]) * kBlockSize + tok) * Hkv + kvh
+                                          : (static_cast<size_t>(b) * S + pg * kBlockSize + tok) * Hkv + kvh;
+            const bool      take = ((okm >> u) & 1) && pg * kBlockSize + tok < L;
+            const uint16_t* src = take ? static_cast<const uint16_t*>(base) + row * D + 8 * ch : zero_src;
+            load_lds16(src, (const FFKV_LDS void*)(stage + (is_v ? C::TILE : 0) + run * 64 * 8));
+        }
+        return okm;
+    };
+
+    // ---- compute ---------------------------------------------------------------------------------------------
+    float m_run = kNegInf;
+    float l_run = 0.0f;
+    f32x4 acc[NT];
+#pragma unroll
+    for (int n = 0; n < NT; ++n) acc[n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    int kaddr[KSTEPS];  // K operand: key c, dims 32j + 8g .. +8
+#pragma unroll
+    for (int j = 0; j < KSTEPS; ++j) kaddr[j] = lds_pos<D>(c, 32 * j + 8 * g);
+    // V^T operand via transposed reads: this lane supplies dims 16n + 4q .. +3 of key row 4g + rr of a page
+    const int vrow = 4 * g + (c >> 2);
+    const int vq = c & 3;
+    const int vsw = v_swizzle<D>(vrow) >> 1;
+    const int vbase = C::TILE + vrow * D + 4 * vq;
+
+    auto compute = [&](int si, const uint16_t* stage, int okm)
+    {
+        const int pg0 = si * KP;
+        f32x4     s[KP];
+#pragma unroll
+        for (int u = 0; u < KP; ++u) s[u] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int j = 0; j < KSTEPS; ++j)
+        {
+#pragma unroll
+            for (int u = 0; u < KP; ++u)
+            {
+                const X8 kj = __builtin_bit_cast(X8, *reinterpret_cast<const u32x4*>(stage + u * kBlockSize * D + kaddr[j]));
+                s[u] = M::mma32(kj, qhi[j], s[u]);
+                if constexpr (NEED_LO) s[u] = M::mma32(kj, qlo[j], s[u]);
+            }
+        }
+        float sc[KP * 4];
+        float mt = kNegInf;
+#pragma unroll
+        for (int u = 0; u < KP; ++u)
+        {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+            {
+                const bool vis = ((okm >> u) & 1) && (pg0 + u) * kBlockSize + 4 * g + i < kend;  // causal limit
+                sc[4 * u + i] = vis ? s[u][i] * a.scale_log2 : kNegInf;
+                mt = fmaxf(mt, sc[4 * u + i]);
+            }
+        }
+        mt = xor_max(mt);
+        const float m_new = fmaxf(m_run, mt);
+        const float m_use = m_new == kNegInf ? 0.0f : m_new;
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+        float       pv[KP * 4];
+        float       psum = 0.0f;
+#pragma unroll
+        for (int e = 0; e < KP * 4; ++e)
+        {
+            pv[e] = __builtin_amdgcn_exp2f(sc[e] - m_use);
+            psum += pv[e];
+        }
+        l_run = l_run * alpha + psum;
+        if (__any(m_new > m_run))
+        {
+#pragma unroll
+            for (int n = 0; n < NT; ++n) acc[n] *= alpha;
+        }
+        m_run = m_new;
+
+#pragma unroll
+        for (int u0 = 0; u0 < KP; u0 += 2)
+        {
+            uint32_t ph[8], pl[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+            {
+                ph[e] = M::bits(pv[4 * u0 + e]);
+                pl[e] = M::bits(pv[4 * u0 + e] - M::value(ph[e]));
+            }
+            const X8 phi = __builtin_bit_cast(X8, u32x4{ph[0] | (ph[1] << 16), ph[2] | (ph[3] << 16),
+                                                        ph[4] | (ph[5] << 16), ph[6] | (ph[7] << 16)});
+            const X8 plo = __builtin_bit_cast(X8, u32x4{pl[0] | (pl[1] << 16), pl[2] | (pl[3] << 16),
+                                                        pl[4] | (pl[5] << 16), pl[6] | (pl[7] << 16)});
+#pragma unroll
+            for (int n = 0; n < NT; ++n)
+            {
+                const int  off = vbase + 16 * (n ^ vsw);
+                const auto a0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+                    (FFKV_LDS bf16x4*)(stage + u0 * kBlockSize * D + off));
+                const auto a1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+                    (FFKV_LDS bf16x4*)(stage + (u0 + 1) * kBlockSize * D + off));
+                const u32x2 w0 = __builtin_bit_cast(u32x2, a0);
+                const u32x2 w1 = __builtin_bit_cast(u32x2, a1);
+                const X8    va = __builtin_bit_cast(X8, u32x4{w0[0], w0[1], w1[0], w1[1]});
+                acc[n] = M::mma32(va, phi, acc[n]);
+                acc[n] = M::mma32(va, plo, acc[n]);
+            }
+        }
+    };
+
+    // ---- pipeline: stage si % 3 ----------------------------------------------------------------------------
+    // Every step issues the same number of loads (steps past the end fetch the zero block into a stage nobody
+    // reads), so "step si has landed" is always vmcnt <= the 2 * IPW loads of step si + 1.
+    auto body = [&](int si, uint16_t* cur, int okm_cur, uint16_t* nxt, int& okm_nxt)
+    {
+        wait_vm<2 * C::IPW>();
+        __builtin_amdgcn_s_barrier();  // step si visible to all; every wave is past step si - 1 (stage of si + 2)
+        okm_nxt = issue(si + 2, nxt);
+        if (wave_active) compute(si, cur, okm_cur);
+    };
+
+    int okm0 = issue(0, s_st0);
+    int okm1 = issue(1, s_st1);
+    int okm2 = 0;
+    for (int si = 0; si < steps; si += kDmaStages)
+    {
+        body(si, s_st0, okm0, s_st2, okm2);
+        if (si + 1 >= steps) break;
+        body(si + 1, s_st1, okm1, s_st0, okm0);
+        if (si + 2 >= steps) break;
+        body(si + 2, s_st2, okm2, s_st1, okm1);
+    }
+    wait_vm<0>();  // no load may still be writing this workgroup's LDS when it ends
+
+    if (col_ok)
+    {
+        const float  l_tot = xor_sum(l_run);
+        const float  inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+        const size_t ob = qrow * D;
+#pragma unroll
+        for (int n = 0; n < NT; ++n) store_out4<QT>(a.out, ob + 16 * n + 4 * g, acc[n] * inv);
+    }
+}
+
+namespace
+{
+
+template <int CT, int QT>
+hipError_t launch_pfd_d(const PrefillArgs& a, hipStream_t stream)
+{
+    constexpr bool BF = CT == BF16;
+    const int      rows = a.seq_len * a.group;
+    const dim3     grid(static_cast<unsigned>((rows + kDmaRows - 1) / kDmaRows), static_cast<unsigned>(a.num_kv_heads),
+                        static_cast<unsigned>(a.batch));
+    switch (a.head_dim)
+    {
+        case 64:
+            hipLaunchKernelGGL((paged_prefill_dma<QT, 64, BF>), grid, dim3(kDmaThreads), 0, stream, a);
+            break;
+        case 128:
+            hipLaunchKernelGGL((paged_prefill_dma<QT, 128, BF>), grid, dim3(kDmaThreads), 0, stream, a);
+            break;
+        default:
+            hipLaunchKernelGGL((paged_prefill_dma<QT, 256, BF>), grid, dim3(kDmaThreads), 0, stream, a);
+            break;
+    }
+    return hipGetLastError();
+}
+
+template <int CT>
+hipError_t launch_pfd_q(const PrefillArgs& a, hipStream_t stream)
+{
+    switch (a.qo_dtype)
+    {
+        case F32:
+            return launch_pfd_d<CT, F32>(a, stream);
+        case F16:
+            return launch_pfd_d<CT, F16>(a, stream);
+        default:
+            return launch_pfd_d<CT, BF16>(a, stream);
+    }
+}
+
+}  // namespace
+
+hipError_t launch_prefill_dma(const PrefillArgs& a, hipStream_t stream)
+{
+    return a.cache_dtype == F16 ? launch_pfd_q<F16>(a, stream) : launch_pfd_q<BF16>(a, stream);
+}
+
+}  // namespace ffkv
