@@ -88,6 +88,23 @@ __device__ __forceinline__ void load_lds16(const void* src, const FFKV_LDS void*
 #pragma clang diagnostic pop
 }
 
+// The same load with a uniform 64-bit base and a 32-bit per-lane byte offset (no per-lane address arithmetic).
+__device__ __forceinline__ void load_lds16(const void* base, uint32_t offset, const FFKV_LDS void* dst)
+{
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+    const uint64_t b64 = reinterpret_cast<uint64_t>(base);
+    // readfirstlane returns int: go through uint32_t so the low word is not sign-extended into the high word
+    const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(b64)));
+    const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(b64 >> 32)));
+    const uint64_t sb = static_cast<uint64_t>(lo) | (static_cast<uint64_t>(hi) << 32);
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1"
+                 :
+                 : "v"(offset), "s"(sb), "s"(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(dst)))
+                 : "memory", "m0");
+#pragma clang diagnostic pop
+}
+
 template <int VM>
 __device__ __forceinline__ void wait_vm()
 {
@@ -133,7 +150,7 @@ void paged_prefill_dma(PrefillArgs a)
     int64_t       Lr = ctx + S;
     if (a.paged && Lr > a.cap_tokens) Lr = a.cap_tokens;
     if (Lr < 0) Lr = 0;
-    const int L = static_cast<int>(Lr);
+    const int L = __builtin_amdgcn_readfirstlane(static_cast<int>(Lr));
 
     const int  r = row0 + 16 * wave + c;
     const bool col_ok = r < R;
@@ -145,7 +162,8 @@ void paged_prefill_dma(PrefillArgs a)
     const int     r_last = min(row0 + kDmaRows, R) - 1;
     int64_t       kw = ctx + r_last / G + 1;
     kw = kw > L ? L : (kw < 0 ? 0 : kw);
-    const int  pages = static_cast<int>((kw + kBlockSize - 1) / kBlockSize);
+    // uniform values computed through divisions: keep them scalar so the loop's branches stay scalar
+    const int  pages = __builtin_amdgcn_readfirstlane(static_cast<int>((kw + kBlockSize - 1) / kBlockSize));
     const int  steps = (pages + KP - 1) / KP;
     const bool wave_active = row0 + 16 * wave < R;
 
@@ -192,56 +210,100 @@ void paged_prefill_dma(PrefillArgs a)
     const FFKV_CONST int32_t* table_row =
         a.paged ? (const FFKV_CONST int32_t*)(a.block_table + static_cast<int64_t>(b) * a.max_blocks) : nullptr;
     const uint16_t* zero_src = reinterpret_cast<const uint16_t*>(g_zero_chunks) + 8 * lane;
-    // Returns the step's page mask (bit u: page si * KP + u is present); keys on absent pages are masked.  The
-    // block-table entries are uniform over the workgroup and come through the scalar cache.
+    // Per-lane part of each load's source, the same for every page: key row `tok` of the page, chunk `ch`
+    // (swizzled to where this lane's 16 bytes land), as a byte offset from the page's (row, kv head) base.
+    uint32_t voff[2 * C::IPW];
+    int      vtok[2 * C::IPW];
+#pragma unroll
+    for (int k = 0; k < 2 * C::IPW; ++k)
+    {
+        const bool is_v = k >= C::IPW;
+        const int  run = wave * C::IPW + (is_v ? k - C::IPW : k);  // 64-chunk run within the tile
+        const int  p = run * 64 % C::CHUNKS + lane;                  // chunk position within the page
+        const int  tok = p / C::CPT;
+        const int  ch = (p % C::CPT) ^ (is_v ? v_swizzle<D>(tok) : k_swizzle(tok));
+        vtok[k] = tok;
+        voff[k] = static_cast<uint32_t>((tok * Hkv * D + 8 * ch) * 2);
+    }
+    const size_t row_bytes = static_cast<size_t>(Hkv) * D * 2;  // one key row of all kv heads
+
+    // Requests step si into `stage`; returns its page mask (bit u: page si * KP + u is present; keys on absent
+    // pages are masked).  Block-table entries are uniform and come through the scalar cache.  Pages whose 16
+    // rows are all keys of the row load with a uniform base; the row's last, partial page (and absent pages)
+    // fetch the zero block for the missing rows.
     auto issue = [&](int si, uint16_t* stage) -> int
     {
-        int okm = 0;
-        int phys[KP];
+        int    okm = 0, full = 0;
+        size_t page_off[KP];  // byte offset of (page row 0, kv head kvh) in the caches
 #pragma unroll
         for (int u = 0; u < KP; ++u)
         {
             const int pg = si * KP + u;
-            phys[u] = 0;
+            page_off[u] = 0;
             if (pg < pages)  // pages <= max_blocks
             {
+                bool present = true;
+                size_t r0;
                 if (a.paged)
                 {
-                    phys[u] = table_row[pg];
-                    if (phys[u] >= 0 && phys[u] < a.num_blocks) okm |= 1 << u;
+                    const int phys = table_row[pg];
+                    present = phys >= 0 && phys < a.num_blocks;
+                    r0 = static_cast<size_t>(present ? phys : 0) * kBlockSize;
                 }
                 else
                 {
+                    r0 = static_cast<size_t>(b) * S + static_cast<size_t>(pg) * kBlockSize;
+                }
+                page_off[u] = r0 * row_bytes + static_cast<size_t>(kvh) * D * 2;
+                if (present)
+                {
                     okm |= 1 << u;
+                    if ((pg + 1) * kBlockSize <= L) full |= 1 << u;
                 }
             }
         }
 #pragma unroll
         for (int k = 0; k < 2 * C::IPW; ++k)
         {
-            const bool      is_v = k >= C::IPW;
-            const int       run = wave * C::IPW + (is_v ? k - C::IPW : k);  // 64-chunk run within the tile
-            const int       u = run * 64 / C::CHUNKS;                         // page of the step (uniform)
-            const int       p = run * 64 % C::CHUNKS + lane;                  // chunk position within the page
-            const int       tok = p / C::CPT;
-            const int       ch = (p % C::CPT) ^ (is_v ? v_swizzle<D>(tok) : k_swizzle(tok));
-            const int       pg = si * KP + u;
-            const void*     base = is_v ? a.v_cache : a.k_cache;
-            const size_t    row = a.paged ? (static_cast<size_t>(phys[u]) * kBlockSize + tok) * Hkv + kvh
-                                          : (static_cast<size_t>(b) * S + pg * kBlockSize + tok) * Hkv + kvh;
-            const bool      take = ((okm >> u) & 1) && pg * kBlockSize + tok < L;
-            const uint16_t* src = take ? static_cast<const uint16_t*>(base) + row * D + 8 * ch : zero_src;
-            load_lds16(src, (const FFKV_LDS void*)(stage + (is_v ? C::TILE : 0) + run * 64 * 8));
+            const bool  is_v = k >= C::IPW;
+            const int   run = wave * C::IPW + (is_v ? k - C::IPW : k);
+            const int   u = run * 64 / C::CHUNKS;  // page of the step (uniform)
+            size_t      poff = page_off[0];  // page_off[u] without a dynamic index (u is uniform but not constant)
+#pragma unroll
+            for (int uu = 1; uu < KP; ++uu) poff = u == uu ? page_off[uu] : poff;
+            const char* base = static_cast<const char*>(is_v ? a.v_cache : a.k_cache) + poff;
+            const FFKV_LDS void* dst = (const FFKV_LDS void*)(stage + (is_v ? C::TILE : 0) + run * 64 * 8);
+            if ((full >> u) & 1)
+            {
+                load_lds16(base, voff[k], dst);
+            }
+            else
+            {
+                const bool take = ((okm >> u) & 1) && (si * KP + u) * kBlockSize + vtok[k] < L;
+                load_lds16(take ? static_cast<const void*>(base + voff[k]) : static_cast<const void*>(zero_src), dst);
+            }
         }
         return okm;
     };
 
     // ---- compute ---------------------------------------------------------------------------------------------
-    float m_run = kNegInf;
-    float l_run = 0.0f;
-    f32x4 acc[NT];
+    // Online softmax on raw scores: m_run is the column's reference maximum (raw units), p = 2^(s*c - m_run*c)
+    // with c = scale * log2(e).  The reference moves (and acc / l_run are rescaled) only when a new maximum
+    // exceeds it by more than 8 / c, so p stays below 2^8 and most steps rescale nothing; numerator and
+    // denominator share the reference, so the result is the same softmax.
+    const float c_log2 = a.scale_log2;
+    const float thr_raw = 8.0f / c_log2;
+    float       m_run = kNegInf;
+    float       l_run = 0.0f;
+    f32x4       acc[NT];
 #pragma unroll
     for (int n = 0; n < NT; ++n) acc[n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    // Smallest causal limit over the wave's active columns: steps wholly below it need no mask.
+    int kmin = col_ok ? kend : INT32_MAX;
+#pragma unroll
+    for (int off = 1; off < 16; off <<= 1) kmin = min(kmin, __shfl_xor(kmin, off, 64));
+    kmin = __builtin_amdgcn_readfirstlane(kmin);
 
     int kaddr[KSTEPS];  // K operand: key c, dims 32j + 8g .. +8
 #pragma unroll
@@ -271,36 +333,48 @@ void paged_prefill_dma(PrefillArgs a)
         }
         float sc[KP * 4];
         float mt = kNegInf;
-#pragma unroll
-        for (int u = 0; u < KP; ++u)
+        if (okm == (1 << KP) - 1 && (pg0 + KP) * kBlockSize <= kmin)  // uniform: every key visible to every column
         {
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-            {
-                const bool vis = ((okm >> u) & 1) && (pg0 + u) * kBlockSize + 4 * g + i < kend;  // causal limit
-                sc[4 * u + i] = vis ? s[u][i] * a.scale_log2 : kNegInf;
-                mt = fmaxf(mt, sc[4 * u + i]);
-            }
+            for (int u = 0; u < KP; ++u)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                {
+                    sc[4 * u + i] = s[u][i];
+                    mt = fmaxf(mt, sc[4 * u + i]);
+                }
+        }
+        else
+        {
+            const int kr = kend - pg0 * kBlockSize - 4 * g;  // key 4g + i of page u is visible iff 16u + i < kr
+#pragma unroll
+            for (int u = 0; u < KP; ++u)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                {
+                    const bool vis = ((okm >> u) & 1) && u * kBlockSize + i < kr;
+                    sc[4 * u + i] = vis ? s[u][i] : kNegInf;
+                    mt = fmaxf(mt, sc[4 * u + i]);
+                }
         }
         mt = xor_max(mt);
-        const float m_new = fmaxf(m_run, mt);
-        const float m_use = m_new == kNegInf ? 0.0f : m_new;
-        const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+        const bool upd = mt > m_run + thr_raw;  // false while the column has seen no key (mt = -inf)
+        if (__any(upd))
+        {
+            const float alpha = upd ? __builtin_amdgcn_exp2f((m_run - mt) * c_log2) : 1.0f;  // 0 on the first key
+            l_run *= alpha;
+#pragma unroll
+            for (int n = 0; n < NT; ++n) acc[n] *= alpha;
+            m_run = upd ? mt : m_run;
+        }
+        const float mneg = m_run == kNegInf ? 0.0f : -m_run * c_log2;  // a column with no key: every p is 0
         float       pv[KP * 4];
-        float       psum = 0.0f;
 #pragma unroll
         for (int e = 0; e < KP * 4; ++e)
         {
-            pv[e] = __builtin_amdgcn_exp2f(sc[e] - m_use);
-            psum += pv[e];
+            pv[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[e], c_log2, mneg));
+            l_run += pv[e];
         }
-        l_run = l_run * alpha + psum;
-        if (__any(m_new > m_run))
-        {
-#pragma unroll
-            for (int n = 0; n < NT; ++n) acc[n] *= alpha;
-        }
-        m_run = m_new;
 
 #pragma unroll
         for (int u0 = 0; u0 < KP; u0 += 2)
@@ -310,12 +384,14 @@ void paged_prefill_dma(PrefillArgs a)
             for (int e = 0; e < 8; ++e)
             {
                 ph[e] = M::bits(pv[4 * u0 + e]);
-                pl[e] = M::bits(pv[4 * u0 + e] - M::value(ph[e]));
+                if constexpr (BF) pl[e] = M::bits(pv[4 * u0 + e] - M::value(ph[e]));
             }
             const X8 phi = __builtin_bit_cast(X8, u32x4{ph[0] | (ph[1] << 16), ph[2] | (ph[3] << 16),
                                                         ph[4] | (ph[5] << 16), ph[6] | (ph[7] << 16)});
-            const X8 plo = __builtin_bit_cast(X8, u32x4{pl[0] | (pl[1] << 16), pl[2] | (pl[3] << 16),
-                                                        pl[4] | (pl[5] << 16), pl[6] | (pl[7] << 16)});
+            X8 plo{};
+            if constexpr (BF)
+                plo = __builtin_bit_cast(X8, u32x4{pl[0] | (pl[1] << 16), pl[2] | (pl[3] << 16),
+                                                   pl[4] | (pl[5] << 16), pl[6] | (pl[7] << 16)});
 #pragma unroll
             for (int n = 0; n < NT; ++n)
             {
@@ -328,7 +404,8 @@ void paged_prefill_dma(PrefillArgs a)
                 const u32x2 w1 = __builtin_bit_cast(u32x2, a1);
                 const X8    va = __builtin_bit_cast(X8, u32x4{w0[0], w0[1], w1[0], w1[1]});
                 acc[n] = M::mma32(va, phi, acc[n]);
-                acc[n] = M::mma32(va, plo, acc[n]);
+                // bf16 keeps 8 bits of p: the residual goes through a second product (f16's 11 bits suffice)
+                if constexpr (BF) acc[n] = M::mma32(va, plo, acc[n]);
             }
         }
     };
