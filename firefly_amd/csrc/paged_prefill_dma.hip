@@ -376,36 +376,50 @@ void paged_prefill_dma(PrefillArgs a)
             l_run += pv[e];
         }
 
+        auto vread = [&](int n, int u0) -> X8  // V^T operand of output tile n over pages u0, u0 + 1
+        {
+            const int  off = vbase + 16 * (n ^ vsw);
+            const auto a0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((FFKV_LDS bf16x4*)(stage + u0 * kBlockSize * D + off));
+            const auto a1 =
+                __builtin_amdgcn_ds_read_tr16_b64_v4bf16((FFKV_LDS bf16x4*)(stage + (u0 + 1) * kBlockSize * D + off));
+            const u32x2 w0 = __builtin_bit_cast(u32x2, a0);
+            const u32x2 w1 = __builtin_bit_cast(u32x2, a1);
+            return __builtin_bit_cast(X8, u32x4{w0[0], w0[1], w1[0], w1[1]});
+        };
 #pragma unroll
         for (int u0 = 0; u0 < KP; u0 += 2)
         {
-            uint32_t ph[8], pl[8];
+            // P^T operand: pairs of p rounded to the MFMA type (packed conversions); for bf16 also the residual
+            // p - hi, which keeps 16 significant bits in two products (f16's 11 bits suffice in one).
+            uint32_t ph[4], pl[4];
 #pragma unroll
-            for (int e = 0; e < 8; ++e)
+            for (int e = 0; e < 4; ++e)
             {
-                ph[e] = M::bits(pv[4 * u0 + e]);
-                if constexpr (BF) pl[e] = M::bits(pv[4 * u0 + e] - M::value(ph[e]));
+                const f32x2 v = f32x2{pv[4 * u0 + 2 * e], pv[4 * u0 + 2 * e + 1]};
+                if constexpr (BF)
+                {
+                    ph[e] = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+                    const f32x2 r = f32x2{v[0] - __builtin_bit_cast(float, ph[e] << 16),
+                                          v[1] - __builtin_bit_cast(float, ph[e] & 0xffff0000u)};
+                    pl[e] = __builtin_bit_cast(uint32_t, __builtin_convertvector(r, bf16x2));
+                }
+                else
+                {
+                    ph[e] = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, h2));
+                }
             }
-            const X8 phi = __builtin_bit_cast(X8, u32x4{ph[0] | (ph[1] << 16), ph[2] | (ph[3] << 16),
-                                                        ph[4] | (ph[5] << 16), ph[6] | (ph[7] << 16)});
-            X8 plo{};
-            if constexpr (BF)
-                plo = __builtin_bit_cast(X8, u32x4{pl[0] | (pl[1] << 16), pl[2] | (pl[3] << 16),
-                                                   pl[4] | (pl[5] << 16), pl[6] | (pl[7] << 16)});
+            const X8 phi = __builtin_bit_cast(X8, u32x4{ph[0], ph[1], ph[2], ph[3]});
+            X8       plo{};
+            if constexpr (BF) plo = __builtin_bit_cast(X8, u32x4{pl[0], pl[1], pl[2], pl[3]});
+            X8 vcur = vread(0, u0);
 #pragma unroll
             for (int n = 0; n < NT; ++n)
             {
-                const int  off = vbase + 16 * (n ^ vsw);
-                const auto a0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
-                    (FFKV_LDS bf16x4*)(stage + u0 * kBlockSize * D + off));
-                const auto a1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
-                    (FFKV_LDS bf16x4*)(stage + (u0 + 1) * kBlockSize * D + off));
-                const u32x2 w0 = __builtin_bit_cast(u32x2, a0);
-                const u32x2 w1 = __builtin_bit_cast(u32x2, a1);
-                const X8    va = __builtin_bit_cast(X8, u32x4{w0[0], w0[1], w1[0], w1[1]});
-                acc[n] = M::mma32(va, phi, acc[n]);
-                // bf16 keeps 8 bits of p: the residual goes through a second product (f16's 11 bits suffice)
-                if constexpr (BF) acc[n] = M::mma32(va, plo, acc[n]);
+                X8 vnxt{};
+                if (n + 1 < NT) vnxt = vread(n + 1, u0);  // next tile's reads in flight behind this tile's products
+                acc[n] = M::mma32(vcur, phi, acc[n]);
+                if constexpr (BF) acc[n] = M::mma32(vcur, plo, acc[n]);
+                vcur = vnxt;
             }
         }
     };
