@@ -237,6 +237,9 @@ int ffkv_paged_prefill(const void* q, void* out, int qo_dtype, const void* k_cac
         return fail(FFKV_ERR_UNSUPPORTED, "batch and num_kv_heads must be <= 65535");
     if (static_cast<int64_t>(seq_len) * (num_heads / num_kv_heads) > INT32_MAX - 64)
         return fail(FFKV_ERR_UNSUPPORTED, "seq_len * group too large");
+    if (static_cast<int64_t>(batch) * num_kv_heads *
+            ((static_cast<int64_t>(seq_len) * (num_heads / num_kv_heads) + 127) / 128) > INT32_MAX - 64 * 1024)
+        return fail(FFKV_ERR_UNSUPPORTED, "batch * num_kv_heads * ceil(seq_len * group / 128) too large");
     if (batch == 0 || seq_len == 0) return ok();
     if (!q || !out || !k_cache || !v_cache || (paged && !context_lens))
         return fail(FFKV_ERR_INVALID_ARGUMENT, "null q, out, cache or context_lens pointer");

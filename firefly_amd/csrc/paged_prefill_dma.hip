@@ -35,6 +35,11 @@ constexpr int kDmaWaves = 8;
 constexpr int kDmaThreads = 64 * kDmaWaves;
 constexpr int kDmaRows = 16 * kDmaWaves;  // query rows per workgroup
 constexpr int kDmaStages = 3;
+constexpr int kXcds = 8;  // MI355X: workgroups are dealt to 8 XCDs (separate L2s) in turn
+
+#ifndef FFKV_PREFILL_XCD
+#define FFKV_PREFILL_XCD 1
+#endif
 
 #ifndef FFKV_PREFILL_DMA_KP128
 #define FFKV_PREFILL_DMA_KP128 2  // pages per step at head_dim 128
@@ -136,14 +141,28 @@ void paged_prefill_dma(PrefillArgs a)
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int c = lane & 15;
     const int g = lane >> 4;
-    const int b = blockIdx.z;
-    const int kvh = blockIdx.y;
+    // Workgroup -> (row b, kv head, row block).  Consecutive workgroups go to the eight XCDs in turn; every row
+    // block of one (b, kv head) is given to the same XCD so its pages are fetched into one L2, not eight.
+    const int nrb = (a.seq_len * a.group + kDmaRows - 1) / kDmaRows;  // row blocks per (b, kv head)
+#if FFKV_PREFILL_XCD
+    const int wg = blockIdx.x;
+    const int xcd = wg % kXcds;
+    const int k_in_xcd = wg / kXcds;
+    const int grp = (k_in_xcd / nrb) * kXcds + xcd;
+    const int rb = k_in_xcd % nrb;
+    if (grp >= a.batch * a.num_kv_heads) return;  // padding of the grid to whole rounds of XCDs
+#else
+    const int grp = blockIdx.x / nrb;
+    const int rb = blockIdx.x % nrb;
+#endif
+    const int b = grp / a.num_kv_heads;
+    const int kvh = grp % a.num_kv_heads;
     const int G = a.group;
     const int S = a.seq_len;
     const int Hq = a.num_heads;
     const int Hkv = a.num_kv_heads;
     const int R = S * G;
-    const int row0 = blockIdx.x * kDmaRows;
+    const int row0 = rb * kDmaRows;
     if (row0 >= R) return;  // uniform over the workgroup
 
     const int64_t ctx = a.paged ? static_cast<int64_t>(a.context_lens[b]) : 0;
@@ -305,9 +324,11 @@ void paged_prefill_dma(PrefillArgs a)
     for (int off = 1; off < 16; off <<= 1) kmin = min(kmin, __shfl_xor(kmin, off, 64));
     kmin = __builtin_amdgcn_readfirstlane(kmin);
 
-    int kaddr[KSTEPS];  // K operand: key c, dims 32j + 8g .. +8
-#pragma unroll
-    for (int j = 0; j < KSTEPS; ++j) kaddr[j] = lds_pos<D>(c, 32 * j + 8 * g);
+    // K operand of k-step j: key c, dims 32j + 8g .. +8 at lds_pos<D>(c, 32j + 8g) = c*D + 8*(g ^ s01) + 32*(j ^ s2)
+    // with the row swizzle sw = 4*s2 + s01: an even and an odd base plus the constant 32j.
+    const int ksw = k_swizzle(c);
+    const int kb_even = c * D + 8 * (g ^ (ksw & 3)) + 32 * (ksw >> 2);
+    const int kb_odd = c * D + 8 * (g ^ (ksw & 3)) - 32 * (ksw >> 2);
     // V^T operand via transposed reads: this lane supplies dims 16n + 4q .. +3 of key row 4g + rr of a page
     const int vrow = 4 * g + (c >> 2);
     const int vq = c & 3;
@@ -320,16 +341,28 @@ void paged_prefill_dma(PrefillArgs a)
         f32x4     s[KP];
 #pragma unroll
         for (int u = 0; u < KP; ++u) s[u] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        auto kread = [&](int j, int u) -> X8
+        {
+            const int ka = ((j & 1) ? kb_odd : kb_even) + 32 * j;
+            return __builtin_bit_cast(X8, *reinterpret_cast<const u32x4*>(stage + u * kBlockSize * D + ka));
+        };
+        X8 kc[KP];
+#pragma unroll
+        for (int u = 0; u < KP; ++u) kc[u] = kread(0, u);
 #pragma unroll
         for (int j = 0; j < KSTEPS; ++j)
         {
+            X8 kn[KP];
+#pragma unroll
+            for (int u = 0; u < KP; ++u) kn[u] = j + 1 < KSTEPS ? kread(j + 1, u) : kc[u];  // next k-step in flight
 #pragma unroll
             for (int u = 0; u < KP; ++u)
             {
-                const X8 kj = __builtin_bit_cast(X8, *reinterpret_cast<const u32x4*>(stage + u * kBlockSize * D + kaddr[j]));
-                s[u] = M::mma32(kj, qhi[j], s[u]);
-                if constexpr (NEED_LO) s[u] = M::mma32(kj, qlo[j], s[u]);
+                s[u] = M::mma32(kc[u], qhi[j], s[u]);
+                if constexpr (NEED_LO) s[u] = M::mma32(kc[u], qlo[j], s[u]);
             }
+#pragma unroll
+            for (int u = 0; u < KP; ++u) kc[u] = kn[u];
         }
         float sc[KP * 4];
         float mt = kNegInf;
@@ -466,8 +499,14 @@ hipError_t launch_pfd_d(const PrefillArgs& a, hipStream_t stream)
 {
     constexpr bool BF = CT == BF16;
     const int      rows = a.seq_len * a.group;
-    const dim3     grid(static_cast<unsigned>((rows + kDmaRows - 1) / kDmaRows), static_cast<unsigned>(a.num_kv_heads),
-                        static_cast<unsigned>(a.batch));
+    const int64_t  groups = static_cast<int64_t>(a.batch) * a.num_kv_heads;
+    const int64_t  nrb = (rows + kDmaRows - 1) / kDmaRows;
+#if FFKV_PREFILL_XCD
+    const int64_t  wgs = (groups + kXcds - 1) / kXcds * kXcds * nrb;
+#else
+    const int64_t  wgs = groups * nrb;
+#endif
+    const dim3     grid(static_cast<unsigned>(wgs));
     switch (a.head_dim)
     {
         case 64:
