@@ -57,6 +57,11 @@ def _load() -> ctypes.CDLL:
     lib.ffkv_paged_decode.restype = i32
     lib.ffkv_paged_decode.argtypes = [vp, vp, i32, vp, vp, i32, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32,
                                       i32, f32, vp, sz, vp]
+    lib.ffkv_decode_shared_prefix_workspace_bytes.restype = sz
+    lib.ffkv_decode_shared_prefix_workspace_bytes.argtypes = [i32, i32, i32, i32, i32, i32, i32]
+    lib.ffkv_paged_decode_shared_prefix.restype = i32
+    lib.ffkv_paged_decode_shared_prefix.argtypes = [vp, vp, i32, vp, vp, i32, vp, vp, vp, vp, i32, i32, i32, i32,
+                                                    i32, i32, i32, i32, f32, i32, vp, sz, vp]
     lib.ffkv_paged_prefill.restype = i32
     lib.ffkv_paged_prefill.argtypes = [vp, vp, i32, vp, vp, i32, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32,
                                        i32, i32, ctypes.c_float, vp]
@@ -181,6 +186,39 @@ def decode_workspace(batch: int, num_heads: int, head_dim: int, max_blocks: int,
 
     n = max(decode_workspace_bytes(batch, num_heads, head_dim, max_blocks, max_context_len), 256)
     return torch.empty(n, dtype=torch.uint8, device=device if device is not None else "cuda")
+
+
+def shared_prefix_workspace(batch: int, num_heads: int, num_kv_heads: int, head_dim: int, max_blocks: int,
+                            shared_blocks: int, max_context_len: int = 0, device=None):
+    """A workspace for ``paged_attention_shared_prefix`` (``ffkv_decode_shared_prefix_workspace_bytes``)."""
+    import torch
+
+    n = max(int(lib.ffkv_decode_shared_prefix_workspace_bytes(batch, num_heads, num_kv_heads, head_dim, max_blocks,
+                                                              max_context_len, shared_blocks)), 256)
+    return torch.empty(n, dtype=torch.uint8, device=device if device is not None else "cuda")
+
+
+def paged_attention_shared_prefix(q, k_cache, v_cache, block_table, context_lens, shared_blocks: int, out=None,
+                                  k_scale=None, v_scale=None, max_context_len: int = 0, scale: float = 0.0,
+                                  workspace=None, num_blocks: int | None = None, stream=None):
+    """Decode over rows whose first ``shared_blocks`` block-table entries are the same pages
+    (``ffkv_paged_decode_shared_prefix``): the shared pages are attended once for all rows."""
+    import torch
+
+    B = q.shape[0]
+    Hq, D = q.shape[-2], q.shape[-1]
+    Hkv = k_cache.shape[2]
+    if out is None:
+        out = torch.empty((B, 1, Hq * D), dtype=q.dtype, device=q.device)
+    max_blocks = block_table.shape[-1]
+    N = k_cache.shape[0] if num_blocks is None else num_blocks
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    check(lib.ffkv_paged_decode_shared_prefix(_ptr(q), _ptr(out), torch_dtype_code(q), _ptr(k_cache), _ptr(v_cache),
+                                              torch_dtype_code(k_cache), _ptr(k_scale), _ptr(v_scale),
+                                              _ptr(block_table), _ptr(context_lens), B, Hq, Hkv, D, BLOCK_SIZE,
+                                              max_blocks, N, max_context_len, float(scale), int(shared_blocks),
+                                              _ptr(workspace), ws_bytes, _stream(stream)))
+    return out
 
 
 def paged_attention(q, k_cache, v_cache, block_table, context_lens, out=None, k_scale=None, v_scale=None,

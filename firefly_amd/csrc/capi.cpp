@@ -6,6 +6,7 @@
 // keeps a per-thread message for ffkv_last_error().
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <climits>
 #include <cstdarg>
 #include <cstdio>
@@ -94,9 +95,10 @@ struct MfmaLayout
     int64_t meta, ml, acc, total;
 };
 
-MfmaLayout mfma_layout(int batch, int num_heads, int head_dim)
+MfmaLayout mfma_layout(int batch, int num_heads, int head_dim, int prefix_chunks = 0)
 {
-    const int64_t slots = static_cast<int64_t>(kMfmaMaxItems) + batch;
+    // shared-prefix mode adds prefix_chunks slots per row after the decode kernel's
+    const int64_t slots = static_cast<int64_t>(kMfmaMaxItems) + batch + static_cast<int64_t>(prefix_chunks) * batch;
     MfmaLayout    l{};
     l.meta = 0;
     l.ml = align256(static_cast<int64_t>(batch) * 2 * 4);
@@ -108,6 +110,26 @@ MfmaLayout mfma_layout(int batch, int num_heads, int head_dim)
 size_t decode_mfma_workspace_bytes(int batch, int num_heads, int head_dim)
 {
     return static_cast<size_t>(mfma_layout(batch, num_heads, head_dim).total);
+}
+
+// Shared-prefix split: the prefix kernel runs (kv head, chunk) groups of ceil(batch * group / 128) workgroups;
+// about one workgroup per CU (256) without chunks under 8 pages (each chunk's partials cost 4 * (head_dim + 2)
+// bytes per (row, head) written and read back).  FFKV_PREFIX_CHUNKS overrides the count.
+void prefix_chunking(int batch, int group, int num_kv_heads, int shared_blocks, int& chunks, int& chunk_pages)
+{
+    static const int env = []
+    {
+        const char* s = std::getenv("FFKV_PREFIX_CHUNKS");
+        return s ? std::atoi(s) : 0;
+    }();
+    const int64_t nrb = (static_cast<int64_t>(batch) * group + 127) / 128;
+    int64_t       c = env > 0 ? env : (256 + nrb * num_kv_heads / 2) / (nrb * num_kv_heads);
+    const int64_t most = env > 0 ? shared_blocks : (shared_blocks + 7) / 8;
+    if (c > most) c = most;
+    if (c > 256) c = 256;
+    if (c < 1) c = 1;
+    chunk_pages = static_cast<int>((shared_blocks + c - 1) / c);
+    chunks = shared_blocks > 0 ? static_cast<int>((shared_blocks + chunk_pages - 1) / chunk_pages) : 0;
 }
 
 int decode_mfma_items(const void* kernel, int threads, int grid_y)
@@ -347,11 +369,14 @@ size_t ffkv_decode_workspace_bytes(int batch, int num_heads, int head_dim, int m
     return generic > mfma ? generic : mfma;
 }
 
-int ffkv_paged_decode(const void* q, void* out, int qo_dtype, const void* k_cache, const void* v_cache,
-                      int cache_dtype, const float* k_scale, const float* v_scale, const int32_t* block_table,
-                      const int32_t* context_lens, int batch, int num_heads, int num_kv_heads, int head_dim,
-                      int block_size, int max_blocks, int num_blocks, int max_context_len, float scale,
-                      void* workspace, size_t workspace_bytes, void* stream)
+namespace
+{
+
+int decode_impl(const void* q, void* out, int qo_dtype, const void* k_cache, const void* v_cache, int cache_dtype,
+                const float* k_scale, const float* v_scale, const int32_t* block_table, const int32_t* context_lens,
+                int batch, int num_heads, int num_kv_heads, int head_dim, int block_size, int max_blocks,
+                int num_blocks, int max_context_len, float scale, int shared_blocks, void* workspace,
+                size_t workspace_bytes, void* stream)
 {
     if (block_size != FFKV_BLOCK_SIZE) return fail(FFKV_ERR_UNSUPPORTED, "block_size must be 16, got %d", block_size);
     if (!is_act(qo_dtype)) return fail(FFKV_ERR_UNSUPPORTED, "unsupported q/out dtype %d", qo_dtype);
@@ -379,7 +404,16 @@ int ffkv_paged_decode(const void* q, void* out, int qo_dtype, const void* k_cach
     if (static_cast<int64_t>(batch) * ceil_div(cap, FFKV_BLOCK_SIZE) > INT32_MAX)
         return fail(FFKV_ERR_UNSUPPORTED, "batch * pages per row exceeds 2^31 - 1 (batch %d, %d tokens per row)",
                     batch, cap);
+    if (shared_blocks < 0 || shared_blocks > max_blocks)
+        return fail(FFKV_ERR_INVALID_ARGUMENT, "shared_blocks %d outside 0 .. max_blocks %d", shared_blocks,
+                    max_blocks);
     const bool mfma = ffkv::decode_use_mfma(cache_dtype, group);
+    // shared-prefix split: matrix-core decode over 16-bit caches (otherwise the plain decode, same results)
+    const int skip = mfma && (cache_dtype == FFKV_DTYPE_BF16 || cache_dtype == FFKV_DTYPE_F16)
+                         ? std::min(shared_blocks, static_cast<int>(ceil_div(cap, FFKV_BLOCK_SIZE)))
+                         : 0;
+    int pfx_chunks = 0, pfx_chunk_pages = 0;
+    if (skip > 0) ffkv::prefix_chunking(batch, group, num_kv_heads, skip, pfx_chunks, pfx_chunk_pages);
     const int  chunk = ffkv::decode_chunk(batch, num_kv_heads, cap);
     const int  max_chunks = static_cast<int>(ceil_div(cap > 0 ? cap : 1, chunk));
 
@@ -388,7 +422,7 @@ int ffkv_paged_decode(const void* q, void* out, int qo_dtype, const void* k_cach
     int64_t          need = 0;
     if (mfma)
     {
-        lay = ffkv::mfma_layout(batch, num_heads, head_dim);
+        lay = ffkv::mfma_layout(batch, num_heads, head_dim, pfx_chunks);
         need = lay.total;
     }
     else if (max_chunks > 1)
@@ -448,7 +482,40 @@ int ffkv_paged_decode(const void* q, void* out, int qo_dtype, const void* k_cach
     a.chunk = chunk;
     a.max_chunks = max_chunks;
     a.scale_log2 = sm_scale * 1.4426950408889634f;
-    hipError_t e = mfma ? ffkv::launch_decode_mfma(a, s) : ffkv::launch_decode(a, s);
+    hipError_t e = hipSuccess;
+    if (skip > 0)
+    {
+        a.skip_blocks = skip;
+        a.pfx_chunks = pfx_chunks;
+        a.pfx_slot0 = ffkv::kMfmaMaxItems + batch;
+        ffkv::PrefillArgs p{};
+        p.q = q;
+        p.k_cache = k_cache;
+        p.v_cache = v_cache;
+        p.block_table = block_table;
+        p.context_lens = context_lens;
+        p.qo_dtype = qo_dtype;
+        p.cache_dtype = cache_dtype;
+        p.batch = batch;
+        p.seq_len = 1;
+        p.num_heads = num_heads;
+        p.num_kv_heads = num_kv_heads;
+        p.group = group;
+        p.head_dim = head_dim;
+        p.max_blocks = max_blocks;
+        p.num_blocks = num_blocks;
+        p.cap_tokens = cap;
+        p.paged = true;
+        p.scale_log2 = a.scale_log2;
+        p.pfx_blocks = skip;
+        p.pfx_chunks = pfx_chunks;
+        p.pfx_chunk_pages = pfx_chunk_pages;
+        p.pfx_slot0 = a.pfx_slot0;
+        p.ws_ml = a.ws_ml;
+        p.ws_acc = a.ws_acc;
+        e = ffkv::launch_prefix_partials(p, s);
+    }
+    if (e == hipSuccess) e = mfma ? ffkv::launch_decode_mfma(a, s) : ffkv::launch_decode(a, s);
     if (owned)
     {
         hipError_t fe = hipFreeAsync(ws, s);
@@ -456,6 +523,44 @@ int ffkv_paged_decode(const void* q, void* out, int qo_dtype, const void* k_cach
     }
     if (e != hipSuccess) return hip_fail(e, "decode launch");
     return ok();
+}
+
+}  // namespace
+
+int ffkv_paged_decode(const void* q, void* out, int qo_dtype, const void* k_cache, const void* v_cache,
+                      int cache_dtype, const float* k_scale, const float* v_scale, const int32_t* block_table,
+                      const int32_t* context_lens, int batch, int num_heads, int num_kv_heads, int head_dim,
+                      int block_size, int max_blocks, int num_blocks, int max_context_len, float scale,
+                      void* workspace, size_t workspace_bytes, void* stream)
+{
+    return decode_impl(q, out, qo_dtype, k_cache, v_cache, cache_dtype, k_scale, v_scale, block_table, context_lens,
+                       batch, num_heads, num_kv_heads, head_dim, block_size, max_blocks, num_blocks, max_context_len,
+                       scale, 0, workspace, workspace_bytes, stream);
+}
+
+size_t ffkv_decode_shared_prefix_workspace_bytes(int batch, int num_heads, int num_kv_heads, int head_dim,
+                                                 int max_blocks, int max_context_len, int shared_blocks)
+{
+    if (batch <= 0 || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0) return 0;
+    const size_t plain = ffkv_decode_workspace_bytes(batch, num_heads, head_dim, max_blocks, max_context_len);
+    const int    cap = ffkv::decode_cap_tokens(max_blocks, max_context_len);
+    const int    skip = std::min(std::max(shared_blocks, 0), static_cast<int>(ceil_div(cap, FFKV_BLOCK_SIZE)));
+    int          chunks = 0, chunk_pages = 0;
+    if (skip > 0) ffkv::prefix_chunking(batch, num_heads / num_kv_heads, num_kv_heads, skip, chunks, chunk_pages);
+    const size_t shared = static_cast<size_t>(ffkv::mfma_layout(batch, num_heads, head_dim, chunks).total);
+    return plain > shared ? plain : shared;
+}
+
+int ffkv_paged_decode_shared_prefix(const void* q, void* out, int qo_dtype, const void* k_cache, const void* v_cache,
+                                    int cache_dtype, const float* k_scale, const float* v_scale,
+                                    const int32_t* block_table, const int32_t* context_lens, int batch, int num_heads,
+                                    int num_kv_heads, int head_dim, int block_size, int max_blocks, int num_blocks,
+                                    int max_context_len, float scale, int shared_blocks, void* workspace,
+                                    size_t workspace_bytes, void* stream)
+{
+    return decode_impl(q, out, qo_dtype, k_cache, v_cache, cache_dtype, k_scale, v_scale, block_table, context_lens,
+                       batch, num_heads, num_kv_heads, head_dim, block_size, max_blocks, num_blocks, max_context_len,
+                       scale, shared_blocks, workspace, workspace_bytes, stream);
 }
 
 }  // extern "C"

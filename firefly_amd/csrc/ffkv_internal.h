@@ -76,6 +76,15 @@ struct PrefillArgs
     int            cap_tokens;  // paged: keys per row are clamped to this
     bool           paged;
     float          scale_log2;
+    // Shared-prefix partials (launch_prefix_partials) only: decode queries q [batch, 1, num_heads, head_dim] over
+    // pages 0 .. pfx_blocks - 1 of block-table row 0, in pfx_chunks chunks of pfx_chunk_pages pages; the partial
+    // of (row b, head h, chunk k) goes to decode-workspace slot pfx_slot0 + k * batch + b.
+    int            pfx_blocks;
+    int            pfx_chunks;
+    int            pfx_chunk_pages;
+    int            pfx_slot0;
+    float*         ws_ml;
+    float*         ws_acc;
 };
 
 struct DecodeArgs
@@ -106,12 +115,19 @@ struct DecodeArgs
     int            chunk;       // tokens per split-K chunk (multiple of 16)
     int            max_chunks;  // ceil(cap_tokens / chunk)
     float          scale_log2;  // softmax scale * log2(e)
+    // Shared-prefix mode (pfx_chunks > 0, MFMA kernel only): the first skip_blocks pages of every row are left to
+    // launch_prefix_partials, whose pfx_chunks partials per row sit at slots pfx_slot0 + k * batch + b; the decode
+    // kernel attends the remaining pages and writes partials only, and the merge folds both for every row.
+    int            skip_blocks;
+    int            pfx_chunks;
+    int            pfx_slot0;
 };
 
 hipError_t launch_append(const AppendArgs& a, hipStream_t stream);
 hipError_t launch_rope_append(const RopeArgs& a, hipStream_t stream);      // rotate q/k, then append when k_cache set
 hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream);          // matrix-core prefill (any cache dtype)
 hipError_t launch_prefill_dma(const PrefillArgs& a, hipStream_t stream);      // 16-bit caches, global->LDS loads
+hipError_t launch_prefix_partials(const PrefillArgs& a, hipStream_t stream);  // shared-prefix decode partials
 hipError_t launch_decode(const DecodeArgs& a, hipStream_t stream);       // generic kernel (any cache dtype)
 hipError_t launch_decode_mfma(const DecodeArgs& a, hipStream_t stream);  // matrix-core kernel (16-bit/8-bit caches)
 

@@ -135,8 +135,12 @@ void paged_decode_mfma(DecodeArgs a)
             if (L > a.cap_tokens) L = a.cap_tokens;
             t = L < 0 ? 0 : static_cast<int>(L);
         }
-        const int n = (t + kBlockSize - 1) / kBlockSize;
-        int       incl = n;
+        // shared-prefix mode: the row's first skip_blocks pages are attended elsewhere
+        int n = (t + kBlockSize - 1) / kBlockSize - a.skip_blocks;
+        n = n < 0 ? 0 : n;
+        t = t - a.skip_blocks * kBlockSize;
+        t = t < 0 ? 0 : t;
+        int incl = n;
 #pragma unroll
         for (int off = 1; off < 64; off <<= 1)
         {
@@ -155,8 +159,10 @@ void paged_decode_mfma(DecodeArgs a)
         if (first_wg && w.w0 + lane < B && w.n == 0)
         {
             const int r = w.w0 + lane;
-            for (int e = 0; e < a.num_heads * D; e += 4)
-                store_out4<QT>(a.out, static_cast<size_t>(r) * a.num_heads * D + e, f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+            if (a.pfx_chunks == 0)  // shared-prefix mode: the merge writes every row
+                for (int e = 0; e < a.num_heads * D; e += 4)
+                    store_out4<QT>(a.out, static_cast<size_t>(r) * a.num_heads * D + e,
+                                   f32x4{0.0f, 0.0f, 0.0f, 0.0f});
             a.ws_meta[2 * r] = -1;
             a.ws_meta[2 * r + 1] = -1;
         }
@@ -196,7 +202,8 @@ void paged_decode_mfma(DecodeArgs a)
     {
         const int l = b - win.w0;
         return LRow{b, win.base + __builtin_amdgcn_readlane(win.excl, l), __builtin_amdgcn_readlane(win.n, l),
-                    __builtin_amdgcn_readlane(win.toks, l), a.block_table + static_cast<int64_t>(b) * a.max_blocks};
+                    __builtin_amdgcn_readlane(win.toks, l),
+                    a.block_table + static_cast<int64_t>(b) * a.max_blocks + a.skip_blocks};
     };
     auto find_page = [&](int x)  // row holding page x (x < P), moving `win` forward from its current window
     {
@@ -456,7 +463,7 @@ void paged_decode_mfma(DecodeArgs a)
     {
         const float l_tot = xor_sum(l_run);
         const int   h = kvh * G + c;
-        if (seg_start == pb && seg_end == pb + nb)
+        if (seg_start == pb && seg_end == pb + nb && a.pfx_chunks == 0)
         {
             if (c < G)
             {
@@ -557,14 +564,19 @@ __global__ __launch_bounds__(256) void paged_decode_mfma_merge(DecodeArgs a)
 
     const int i_lo = a.ws_meta[2 * b];
     const int i_hi = a.ws_meta[2 * b + 1];
-    if (i_lo == i_hi) return;  // one piece (written by the decode kernel) or no token (i_lo = i_hi = -1)
+    // one piece (written by the decode kernel) or no token (i_lo = i_hi = -1); shared-prefix mode always merges
+    if (i_lo == i_hi && a.pfx_chunks == 0) return;
 
-    float m = kNegInf, l = 0.0f, o[PER];
+    // pieces: the shared-prefix partials (slots pfx_slot0 + k * batch + b), then work items i_lo .. i_hi (slots
+    // i + b) when the row has pages of its own
+    const int pieces = a.pfx_chunks + (i_lo >= 0 ? i_hi - i_lo + 1 : 0);
+    float     m = kNegInf, l = 0.0f, o[PER];
 #pragma unroll
     for (int k = 0; k < PER; ++k) o[k] = 0.0f;
-    for (int i = i_lo + wave; i <= i_hi; i += 4)
+    for (int i = wave; i < pieces; i += 4)
     {
-        const int64_t slot = static_cast<int64_t>(i) + b;
+        const int64_t slot = i < a.pfx_chunks ? static_cast<int64_t>(a.pfx_slot0) + static_cast<int64_t>(i) * a.batch + b
+                                              : static_cast<int64_t>(i_lo + i - a.pfx_chunks) + b;
         const float   ms = a.ws_ml[(slot * a.num_heads + h) * 2];
         const float   ls = a.ws_ml[(slot * a.num_heads + h) * 2 + 1];
         const float*  src = a.ws_acc + (slot * a.num_heads + h) * D + lane * PER;

@@ -119,7 +119,11 @@ __device__ __forceinline__ void wait_vm()
 
 }  // namespace
 
-template <int QT, int D, bool BF>
+// PFX = false: prefill (the contract above).  PFX = true: split-K partials of decode queries over a prefix of
+// pages shared by every row (pages 0 .. pfx_blocks - 1 of row 0's block table, which all rows hold): one query
+// per (row, head), attending keys 0 .. min(ctx + 1, prefix) - 1, written as (max, denominator, unnormalised
+// output) to the decode workspace for the decode merge to fold in.
+template <int QT, int D, bool BF, bool PFX>
 __global__ __launch_bounds__(kDmaThreads) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 4 : 1)))
 void paged_prefill_dma(PrefillArgs a)
 {
@@ -141,54 +145,81 @@ void paged_prefill_dma(PrefillArgs a)
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int c = lane & 15;
     const int g = lane >> 4;
-    // Workgroup -> (row b, kv head, row block).  Consecutive workgroups go to the eight XCDs in turn; every row
-    // block of one (b, kv head) is given to the same XCD so its pages are fetched into one L2, not eight.
-    const int nrb = (a.seq_len * a.group + kDmaRows - 1) / kDmaRows;  // row blocks per (b, kv head)
+    // Workgroup -> (group, row block).  A group is (row b, kv head) for prefill and (kv head, chunk of prefix
+    // pages) for prefix partials.  Consecutive workgroups go to the eight XCDs in turn; every row block of one
+    // group is given to the same XCD, so the group's pages are fetched into one L2, not eight.
+    const int G = a.group;
+    const int S = a.seq_len;
+    const int Hq = a.num_heads;
+    const int Hkv = a.num_kv_heads;
+    const int R = PFX ? a.batch * G : S * G;  // query rows of a group: (token, head) or (row, head) pairs
+    const int nrb = (R + kDmaRows - 1) / kDmaRows;
+    const int groups = PFX ? Hkv * a.pfx_chunks : a.batch * Hkv;
 #if FFKV_PREFILL_XCD
     const int wg = blockIdx.x;
     const int xcd = wg % kXcds;
     const int k_in_xcd = wg / kXcds;
     const int grp = (k_in_xcd / nrb) * kXcds + xcd;
     const int rb = k_in_xcd % nrb;
-    if (grp >= a.batch * a.num_kv_heads) return;  // padding of the grid to whole rounds of XCDs
+    if (grp >= groups) return;  // padding of the grid to whole rounds of XCDs
 #else
     const int grp = blockIdx.x / nrb;
     const int rb = blockIdx.x % nrb;
 #endif
-    const int b = grp / a.num_kv_heads;
-    const int kvh = grp % a.num_kv_heads;
-    const int G = a.group;
-    const int S = a.seq_len;
-    const int Hq = a.num_heads;
-    const int Hkv = a.num_kv_heads;
-    const int R = S * G;
+    const int b = PFX ? 0 : grp / Hkv;                 // prefill: the workgroup's row
+    const int kvh = PFX ? grp / a.pfx_chunks : grp % Hkv;
+    const int chunk = PFX ? grp % a.pfx_chunks : 0;  // prefix: pages chunk*pfx_chunk_pages ..
     const int row0 = rb * kDmaRows;
     if (row0 >= R) return;  // uniform over the workgroup
 
-    const int64_t ctx = a.paged ? static_cast<int64_t>(a.context_lens[b]) : 0;
-    int64_t       Lr = ctx + S;
-    if (a.paged && Lr > a.cap_tokens) Lr = a.cap_tokens;
-    if (Lr < 0) Lr = 0;
-    const int L = __builtin_amdgcn_readfirstlane(static_cast<int>(Lr));
-
+    // This lane's query row (MFMA column): prefill token t of row b, head h; prefix: row bq, head h, its one
+    // decode query.  It sees keys [0, kend).  Pages pg_lo .. pg_hi - 1 are the workgroup's; rows 0 .. L - 1 of
+    // them hold keys (the rest load as zeros).
     const int  r = row0 + 16 * wave + c;
     const bool col_ok = r < R;
-    const int  t = col_ok ? r / G : 0;
     const int  h = kvh * G + (col_ok ? r % G : 0);
-    int64_t    ke = ctx + t + 1;
-    ke = ke > L ? L : (ke < 0 ? 0 : ke);
-    const int     kend = col_ok ? static_cast<int>(ke) : 0;
-    const int     r_last = min(row0 + kDmaRows, R) - 1;
-    int64_t       kw = ctx + r_last / G + 1;
-    kw = kw > L ? L : (kw < 0 ? 0 : kw);
+    int        L, pg_lo, pg_hi, kend;
+    size_t     qrow;
+    int        bq = 0;
+    if constexpr (PFX)
+    {
+        const int pfx_tokens = a.pfx_blocks * kBlockSize;
+        bq = col_ok ? r / G : 0;
+        int64_t ke = static_cast<int64_t>(a.context_lens[bq]) + 1;  // the decode query sees ctx + 1 keys
+        if (ke > a.cap_tokens) ke = a.cap_tokens;
+        ke = ke > pfx_tokens ? pfx_tokens : (ke < 0 ? 0 : ke);
+        kend = col_ok ? static_cast<int>(ke) : 0;
+        qrow = static_cast<size_t>(bq) * Hq + h;
+        L = pfx_tokens;
+        pg_lo = chunk * a.pfx_chunk_pages;
+        pg_hi = min(pg_lo + a.pfx_chunk_pages, a.pfx_blocks);
+    }
+    else
+    {
+        const int64_t ctx = a.paged ? static_cast<int64_t>(a.context_lens[b]) : 0;
+        int64_t       Lr = ctx + S;
+        if (a.paged && Lr > a.cap_tokens) Lr = a.cap_tokens;
+        if (Lr < 0) Lr = 0;
+        L = __builtin_amdgcn_readfirstlane(static_cast<int>(Lr));
+        const int t = col_ok ? r / G : 0;
+        int64_t   ke = ctx + t + 1;
+        ke = ke > L ? L : (ke < 0 ? 0 : ke);
+        kend = col_ok ? static_cast<int>(ke) : 0;
+        qrow = (static_cast<size_t>(b) * S + t) * Hq + h;
+        const int r_last = min(row0 + kDmaRows, R) - 1;
+        int64_t   kw = ctx + r_last / G + 1;
+        kw = kw > L ? L : (kw < 0 ? 0 : kw);
+        pg_lo = 0;
+        pg_hi = static_cast<int>((kw + kBlockSize - 1) / kBlockSize);
+    }
     // uniform values computed through divisions: keep them scalar so the loop's branches stay scalar
-    const int  pages = __builtin_amdgcn_readfirstlane(static_cast<int>((kw + kBlockSize - 1) / kBlockSize));
-    const int  steps = (pages + KP - 1) / KP;
+    pg_lo = __builtin_amdgcn_readfirstlane(pg_lo);
+    pg_hi = __builtin_amdgcn_readfirstlane(pg_hi);
+    const int  steps = pg_hi > pg_lo ? (pg_hi - pg_lo + KP - 1) / KP : 0;
     const bool wave_active = row0 + 16 * wave < R;
 
     // ---- Q^T operands of the wave's 16 query rows ----------------------------------------------------------
     X8           qhi[KSTEPS], qlo[KSTEPS];
-    const size_t qrow = (static_cast<size_t>(b) * S + t) * Hq + h;
 #pragma unroll
     for (int j = 0; j < KSTEPS; ++j)
     {
@@ -226,7 +257,7 @@ void paged_prefill_dma(PrefillArgs a)
     wait_vm<0>();
 
     // ---- loads: wave w fetches runs w*IPW .. w*IPW + IPW - 1 (64 chunks each) of the K tile and of the V tile --
-    const FFKV_CONST int32_t* table_row =
+    const FFKV_CONST int32_t* table_row =  // prefix: row 0's table, whose first pfx_blocks entries every row shares
         a.paged ? (const FFKV_CONST int32_t*)(a.block_table + static_cast<int64_t>(b) * a.max_blocks) : nullptr;
     const uint16_t* zero_src = reinterpret_cast<const uint16_t*>(g_zero_chunks) + 8 * lane;
     // Per-lane part of each load's source, the same for every page: key row `tok` of the page, chunk `ch`
@@ -246,7 +277,7 @@ void paged_prefill_dma(PrefillArgs a)
     }
     const size_t row_bytes = static_cast<size_t>(Hkv) * D * 2;  // one key row of all kv heads
 
-    // Requests step si into `stage`; returns its page mask (bit u: page si * KP + u is present; keys on absent
+    // Requests step si into `stage`; returns its page mask (bit u: page pg_lo + si*KP + u is present; keys on absent
     // pages are masked).  Block-table entries are uniform and come through the scalar cache.  Pages whose 16
     // rows are all keys of the row load with a uniform base; the row's last, partial page (and absent pages)
     // fetch the zero block for the missing rows.
@@ -257,9 +288,9 @@ void paged_prefill_dma(PrefillArgs a)
 #pragma unroll
         for (int u = 0; u < KP; ++u)
         {
-            const int pg = si * KP + u;
+            const int pg = pg_lo + si * KP + u;
             page_off[u] = 0;
-            if (pg < pages)  // pages <= max_blocks
+            if (pg < pg_hi)  // pg_hi <= max_blocks
             {
                 bool present = true;
                 size_t r0;
@@ -298,7 +329,7 @@ void paged_prefill_dma(PrefillArgs a)
             }
             else
             {
-                const bool take = ((okm >> u) & 1) && (si * KP + u) * kBlockSize + vtok[k] < L;
+                const bool take = ((okm >> u) & 1) && (pg_lo + si * KP + u) * kBlockSize + vtok[k] < L;
                 load_lds16(take ? static_cast<const void*>(base + voff[k]) : static_cast<const void*>(zero_src), dst);
             }
         }
@@ -337,7 +368,7 @@ void paged_prefill_dma(PrefillArgs a)
 
     auto compute = [&](int si, const uint16_t* stage, int okm)
     {
-        const int pg0 = si * KP;
+        const int pg0 = pg_lo + si * KP;
         f32x4     s[KP];
 #pragma unroll
         for (int u = 0; u < KP; ++u) s[u] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -481,9 +512,25 @@ void paged_prefill_dma(PrefillArgs a)
     }
     wait_vm<0>();  // no load may still be writing this workgroup's LDS when it ends
 
-    if (col_ok)
+    const float l_tot = xor_sum(l_run);
+    if constexpr (PFX)
     {
-        const float  l_tot = xor_sum(l_run);
+        // partial of (row bq, head h) over this chunk, in the decode merge's convention: max in the log2 domain
+        if (col_ok)
+        {
+            const int64_t slot = static_cast<int64_t>(a.pfx_slot0) + static_cast<int64_t>(chunk) * a.batch + bq;
+            float*        dst = a.ws_acc + (slot * Hq + h) * D;
+#pragma unroll
+            for (int n = 0; n < NT; ++n) *reinterpret_cast<f32x4*>(dst + 16 * n + 4 * g) = acc[n];
+            if (g == 0)
+            {
+                a.ws_ml[(slot * Hq + h) * 2] = m_run == kNegInf ? kNegInf : m_run * c_log2;
+                a.ws_ml[(slot * Hq + h) * 2 + 1] = l_tot;
+            }
+        }
+    }
+    else if (col_ok)
+    {
         const float  inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
         const size_t ob = qrow * D;
 #pragma unroll
@@ -494,45 +541,48 @@ void paged_prefill_dma(PrefillArgs a)
 namespace
 {
 
-template <int CT, int QT>
+template <int CT, int QT, bool PFX>
 hipError_t launch_pfd_d(const PrefillArgs& a, hipStream_t stream)
 {
     constexpr bool BF = CT == BF16;
-    const int      rows = a.seq_len * a.group;
-    const int64_t  groups = static_cast<int64_t>(a.batch) * a.num_kv_heads;
+    const int64_t  rows = PFX ? static_cast<int64_t>(a.batch) * a.group : static_cast<int64_t>(a.seq_len) * a.group;
+    const int64_t  groups = PFX ? static_cast<int64_t>(a.num_kv_heads) * a.pfx_chunks
+                                : static_cast<int64_t>(a.batch) * a.num_kv_heads;
     const int64_t  nrb = (rows + kDmaRows - 1) / kDmaRows;
 #if FFKV_PREFILL_XCD
     const int64_t  wgs = (groups + kXcds - 1) / kXcds * kXcds * nrb;
 #else
     const int64_t  wgs = groups * nrb;
 #endif
-    const dim3     grid(static_cast<unsigned>(wgs));
+    if (wgs <= 0) return hipSuccess;
+    if (wgs > INT32_MAX) return hipErrorInvalidConfiguration;
+    const dim3 grid(static_cast<unsigned>(wgs));
     switch (a.head_dim)
     {
         case 64:
-            hipLaunchKernelGGL((paged_prefill_dma<QT, 64, BF>), grid, dim3(kDmaThreads), 0, stream, a);
+            hipLaunchKernelGGL((paged_prefill_dma<QT, 64, BF, PFX>), grid, dim3(kDmaThreads), 0, stream, a);
             break;
         case 128:
-            hipLaunchKernelGGL((paged_prefill_dma<QT, 128, BF>), grid, dim3(kDmaThreads), 0, stream, a);
+            hipLaunchKernelGGL((paged_prefill_dma<QT, 128, BF, PFX>), grid, dim3(kDmaThreads), 0, stream, a);
             break;
         default:
-            hipLaunchKernelGGL((paged_prefill_dma<QT, 256, BF>), grid, dim3(kDmaThreads), 0, stream, a);
+            hipLaunchKernelGGL((paged_prefill_dma<QT, 256, BF, PFX>), grid, dim3(kDmaThreads), 0, stream, a);
             break;
     }
     return hipGetLastError();
 }
 
-template <int CT>
+template <int CT, bool PFX>
 hipError_t launch_pfd_q(const PrefillArgs& a, hipStream_t stream)
 {
     switch (a.qo_dtype)
     {
         case F32:
-            return launch_pfd_d<CT, F32>(a, stream);
+            return launch_pfd_d<CT, F32, PFX>(a, stream);
         case F16:
-            return launch_pfd_d<CT, F16>(a, stream);
+            return launch_pfd_d<CT, F16, PFX>(a, stream);
         default:
-            return launch_pfd_d<CT, BF16>(a, stream);
+            return launch_pfd_d<CT, BF16, PFX>(a, stream);
     }
 }
 
@@ -540,7 +590,12 @@ hipError_t launch_pfd_q(const PrefillArgs& a, hipStream_t stream)
 
 hipError_t launch_prefill_dma(const PrefillArgs& a, hipStream_t stream)
 {
-    return a.cache_dtype == F16 ? launch_pfd_q<F16>(a, stream) : launch_pfd_q<BF16>(a, stream);
+    return a.cache_dtype == F16 ? launch_pfd_q<F16, false>(a, stream) : launch_pfd_q<BF16, false>(a, stream);
+}
+
+hipError_t launch_prefix_partials(const PrefillArgs& a, hipStream_t stream)
+{
+    return a.cache_dtype == F16 ? launch_pfd_q<F16, true>(a, stream) : launch_pfd_q<BF16, true>(a, stream);
 }
 
 }  // namespace ffkv

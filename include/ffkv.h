@@ -109,6 +109,29 @@ FFKV_API int ffkv_paged_decode(const void* q, void* out, int qo_dtype, const voi
                       void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * ffkv_paged_decode for a batch whose rows share a prefix of pages (the radix tree's shared blocks): entries
+ * 0 .. shared_blocks - 1 of every row's block table are the same physical pages, read from row 0's table.  The
+ * prefix is attended once for all rows as a matrix product (every row's queries of a kv head against each
+ * prefix page, split into chunks of pages), the rest of each row by the decode kernel, and the split-K merge
+ * folds both: each shared page is read once per call instead of once per row.  Results equal ffkv_paged_decode
+ * on the same inputs up to floating-point summation order (same tolerance).  Rows shorter than the prefix
+ * attend only their own tokens.  The split applies to F16/BF16 caches with group <= 16; other calls run
+ * ffkv_paged_decode unchanged.  No counterpart in the reference, whose decode reads shared blocks once per row
+ * (src/kernels/attention.cu:332-335).  Workspace: ffkv_decode_shared_prefix_workspace_bytes, or NULL as for
+ * ffkv_paged_decode.
+ */
+FFKV_API size_t ffkv_decode_shared_prefix_workspace_bytes(int batch, int num_heads, int num_kv_heads, int head_dim,
+                                                          int max_blocks, int max_context_len, int shared_blocks);
+
+FFKV_API int ffkv_paged_decode_shared_prefix(const void* q, void* out, int qo_dtype, const void* k_cache,
+                                             const void* v_cache, int cache_dtype, const float* k_scale,
+                                             const float* v_scale, const int32_t* block_table,
+                                             const int32_t* context_lens, int batch, int num_heads, int num_kv_heads,
+                                             int head_dim, int block_size, int max_blocks, int num_blocks,
+                                             int max_context_len, float scale, int shared_blocks, void* workspace,
+                                             size_t workspace_bytes, void* stream);
+
+/*
  * Causal prefill attention over the paged cache (chunked prefill with prefix reuse).  Replaces the prefill branch
  * of `firefly::kernels::attention` (kv_cache_block_table == nullptr: flash_attn_wmma_kernel,
  * src/kernels/attention.cu:22-286, dispatched at :460-474) and extends it to cached prefixes, which the

@@ -103,6 +103,40 @@ def test_workspace_bytes_monotone(ff):
 
 
 
+def _decode_shared(ff, **kw):
+    a = dict(q=16, out=16, qo_dtype=ff.DTYPE_BF16, k_cache=16, v_cache=16, cache_dtype=ff.DTYPE_BF16,
+             k_scale=None, v_scale=None, block_table=16, context_lens=16, batch=1, num_heads=32, num_kv_heads=8,
+             head_dim=128, block_size=16, max_blocks=4, num_blocks=4, max_context_len=0, scale=0.0,
+             shared_blocks=2, workspace=None, workspace_bytes=0, stream=None)
+    a.update(kw)
+    return ff.lib.ffkv_paged_decode_shared_prefix(*a.values())
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(shared_blocks=-1), -1),
+    (dict(shared_blocks=5), -1),      # beyond max_blocks
+    (dict(block_size=8), -2),
+    (dict(num_heads=30), -1),
+    (dict(q=None), -1),
+    (dict(cache_dtype=3), -1),        # int8 without scales: the plain decode's checks apply
+])
+def test_decode_shared_prefix_rejects(ff, kw, code):
+    assert _decode_shared(ff, **kw) == code
+    assert ff.lib.ffkv_last_error().decode() != ""
+
+
+def test_decode_shared_prefix_workspace(ff):
+    plain = ff.decode_workspace_bytes(120, 32, 128, 200, 0)
+    shared = ff.lib.ffkv_decode_shared_prefix_workspace_bytes(120, 32, 8, 128, 200, 0, 128)
+    # room for the prefix partials (chunks x rows x heads x (head_dim + 2) floats) on top of the plain decode's
+    assert shared > plain + 120 * 32 * 130 * 4
+    assert ff.lib.ffkv_decode_shared_prefix_workspace_bytes(120, 32, 8, 128, 200, 0, 0) == plain
+    need = ff.lib.ffkv_decode_shared_prefix_workspace_bytes(4, 32, 8, 128, 600, 0, 100)
+    assert need > ff.decode_workspace_bytes(4, 32, 128, 600, 0)
+    assert _decode_shared(ff, batch=4, max_blocks=600, shared_blocks=100, workspace=256,
+                          workspace_bytes=need - 1) == ff.ERR_WORKSPACE
+
+
 def _rope_append(ff, **kw):
     a = dict(q=16, k=16, v=16, src_dtype=ff.DTYPE_BF16, k_cache=16, v_cache=16, cache_dtype=ff.DTYPE_BF16,
              k_scale=None, v_scale=None, block_table=16, context_lens=None, batch=1, seq_len=1, num_heads=32,

@@ -1,0 +1,147 @@
+"""Decode over rows that share a prefix of pages (ffkv_paged_decode_shared_prefix) against the CPU checker's
+decode on the same appended cache, to the same bar as the plain decode (tests/test_gpu_parity.py): outputs within
+max-abs 2e-3 (16-bit KV) or 2e-2 (quantized KV) of the fp32 checker, beyond the output format's rounding.  The
+shared pages are attended once for all rows by a separate matrix-product kernel and merged with each row's own
+pages, so these cases cover the split itself: prefixes of 1 .. 128 pages, rows shorter than the prefix, rows
+ending exactly at its end, truncation by max_context_len, holes in the prefix, every head_dim and group size, and
+a workspace full of garbage reused across calls.  Cases whose cache type the split does not serve (int8, fp8)
+run the plain decode and must agree as well."""
+
+import numpy as np
+import pytest
+
+import cases
+import oracle as O
+from test_gpu_parity import half_ulp
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(ff, dev, c, shared, max_context_len=0, workspace=None, table=None):
+    import torch
+
+    import gpu_util as gu
+
+    tbl = c.block_table if table is None else table
+    print(f"case shared-prefix seed={c.seed} B={c.B} Hq={c.Hq} Hkv={c.Hkv} D={c.D} act={c.act} kv={c.kv} "
+          f"shared={shared} ctx_max={int(c.ctx.max())} cap={max_context_len}", flush=True)
+    kp, vp = c.k_pool.copy(), c.v_pool.copy()
+    ks = None if c.k_scale is None else c.k_scale.copy()
+    vs = None if c.v_scale is None else c.v_scale.copy()
+    O.append(c.k_new, c.v_new, c.act, kp, vp, c.kv, tbl, c.ctx, ks, vs)
+    _, ref = O.paged_decode(c.q, c.act, kp, vp, c.kv, tbl, c.ctx, ks, vs, max_context_len=max_context_len)
+    kd, vd = gu.to_dev(kp, c.kv, dev), gu.to_dev(vp, c.kv, dev)
+    ksd = None if ks is None else torch.from_numpy(ks).to(dev)
+    vsd = None if vs is None else torch.from_numpy(vs).to(dev)
+    bt = torch.from_numpy(np.ascontiguousarray(tbl)).to(dev)
+    cx = torch.from_numpy(c.ctx).to(dev)
+    q = gu.to_dev(c.q, c.act, dev)
+    out = ff.paged_attention_shared_prefix(q, kd, vd, bt, cx, shared, k_scale=ksd, v_scale=vsd,
+                                           max_context_len=max_context_len, workspace=workspace,
+                                           num_blocks=c.num_blocks)
+    plain = ff.paged_attention(q, kd, vd, bt, cx, k_scale=ksd, v_scale=vsd, max_context_len=max_context_len,
+                               num_blocks=c.num_blocks)
+    torch.cuda.synchronize()
+    conv = (lambda t: gu.out_to_f32(gu.to_host(t, np.uint16), c.act)) if c.act != O.DTYPE_F32 else \
+        (lambda t: t.cpu().numpy())
+    return conv(out).reshape(ref.shape), conv(plain).reshape(ref.shape), ref
+
+
+def _check(got, ref, act, tol, what):
+    diff = np.abs(got.astype(np.float64) - ref)
+    excess = float((diff - half_ulp(np.maximum(np.abs(got), np.abs(ref)), act)).max())
+    print(f"  {what}: max-abs err {diff.max():.3e}, beyond output rounding {excess:.3e} (tol {tol})", flush=True)
+    assert excess <= tol
+
+
+def _both(ff, dev, c, shared, tol=2e-3, **kw):
+    got, plain, ref = _run(ff, dev, c, shared, **kw)
+    _check(got, ref, c.act, tol, "shared-prefix decode")
+    _check(plain, ref, c.act, tol, "plain decode")
+
+
+@pytest.mark.parametrize("shared,suffix", [(1, (1, 40)), (8, (1, 200)), (32, (16, 600)), (128, (64, 1024))])
+def test_shared_prefix_bf16(ff, gpu, shared, suffix):
+    rng = np.random.default_rng(40 + shared)
+    B = 24
+    ctx = shared * 16 + rng.integers(suffix[0], suffix[1] + 1, size=B) - 1  # ctx + 1 tokens after the append
+    c = cases.make_case(40 + shared, B, 32, 8, 128, ctx, act="bf16", shared_prefix_blocks=shared)
+    _both(ff, gpu, c, shared)
+
+
+def test_c4_shape(ff, gpu):
+    """BASELINE config 4's decode: 120 rows over one 2048-token prefix, private suffixes U[64, 1024]."""
+    rng = np.random.default_rng(44)
+    ctx = 2048 + rng.integers(64, 1025, size=120) - 1
+    c = cases.make_case(44, 120, 32, 8, 128, ctx, act="bf16", shared_prefix_blocks=128)
+    _both(ff, gpu, c, 128)
+
+
+def test_rows_shorter_than_or_ending_at_the_prefix(ff, gpu):
+    """Rows that end inside the prefix (they attend only their own tokens), exactly at its end (no private page),
+    one token past it, and a one-token row."""
+    ctx = [10, 127, 128, 200, 0, 300, 143, 160]
+    c = cases.make_case(45, len(ctx), 16, 4, 128, ctx, act="bf16", shared_prefix_blocks=9, max_blocks=20)
+    # the entry point's precondition: entries 0 .. shared_blocks - 1 hold the prefix pages in every row's table
+    # (make_case fills a row's table only as far as its own tokens reach)
+    c.block_table[:, :9] = c.block_table[int(np.argmax(c.ctx)), :9]
+    _both(ff, gpu, c, 9)
+
+
+@pytest.mark.parametrize("D,G", [(64, 1), (64, 8), (128, 16), (256, 4), (256, 7)])
+def test_head_shapes(ff, gpu, D, G):
+    rng = np.random.default_rng(46 + D + G)
+    ctx = 160 + rng.integers(0, 300, size=10)
+    c = cases.make_case(46 + D + G, 10, 2 * G, 2, D, ctx, act="bf16", shared_prefix_blocks=10)
+    _both(ff, gpu, c, 10)
+
+
+@pytest.mark.parametrize("act,kv,tol", [("f16", "f16", 2e-3), ("f32", "bf16", 2e-3), ("bf16", "i8", 2e-2),
+                                        ("bf16", "fp8", 2e-2)])
+def test_dtypes(ff, gpu, act, kv, tol):
+    rng = np.random.default_rng(47)
+    ctx = 256 + rng.integers(0, 400, size=12)
+    c = cases.make_case(47, 12, 32, 8, 128, ctx, act=act, kv=kv, shared_prefix_blocks=16)
+    _both(ff, gpu, c, 16, tol=tol)
+
+
+def test_truncated_context(ff, gpu):
+    """max_context_len below some rows' lengths, and below the prefix itself."""
+    rng = np.random.default_rng(48)
+    ctx = 320 + rng.integers(0, 500, size=9)
+    c = cases.make_case(48, 9, 32, 8, 128, ctx, act="bf16", shared_prefix_blocks=20)
+    _both(ff, gpu, c, 20, max_context_len=500)
+    _both(ff, gpu, c, 20, max_context_len=200)
+
+
+def test_hole_in_the_prefix(ff, gpu):
+    """An invalid entry inside the shared prefix (every row holds it) is skipped like in the plain decode."""
+    rng = np.random.default_rng(49)
+    ctx = 200 + rng.integers(0, 300, size=8)
+    c = cases.make_case(49, 8, 16, 4, 128, ctx, act="bf16", shared_prefix_blocks=12)
+    tbl = c.block_table.copy()
+    tbl[:, 3] = -1
+    tbl[:, 7] = c.num_blocks + 3
+    _both(ff, gpu, c, 12, table=tbl)
+
+
+def test_zero_shared_blocks_is_the_plain_decode(ff, gpu):
+    rng = np.random.default_rng(50)
+    c = cases.make_case(50, 6, 32, 8, 128, rng.integers(1, 700, size=6), act="bf16")
+    got, plain, ref = _run(ff, gpu, c, 0)
+    assert np.array_equal(got, plain)
+    _check(got, ref, c.act, 2e-3, "shared_blocks = 0")
+
+
+def test_workspace_with_garbage_reused(ff, gpu):
+    """One explicit workspace, filled with garbage, serves calls of different batch sizes and prefixes."""
+    import torch
+
+    ws = ff.shared_prefix_workspace(64, 32, 8, 128, 200, 64, device=gpu)
+    ws.copy_(torch.randint(0, 256, ws.shape, dtype=torch.uint8, device=gpu))
+    rng = np.random.default_rng(51)
+    for i, (B, shared) in enumerate([(64, 64), (5, 3), (40, 64), (5, 3)]):
+        ctx = shared * 16 + rng.integers(0, 900, size=B)
+        c = cases.make_case(51 + i, B, 32, 8, 128, ctx, act="bf16", shared_prefix_blocks=shared, max_blocks=200)
+        got, _, ref = _run(ff, gpu, c, shared, workspace=ws)
+        _check(got, ref, c.act, 2e-3, f"call {i}")
