@@ -218,10 +218,16 @@ def c4_config(ff, torch, dev, stream, layers=2, calls=30, seed=4):
     od = torch.empty((Bd, 1, Hq * D), device=dev, dtype=torch.bfloat16)
     oc = torch.empty((Bc, CH, Hq * D), device=dev, dtype=torch.bfloat16)
     ws = ff.decode_workspace(Bd, Hq, D, table_np.shape[1], device=dev)
+    SB = PRE // BLOCK  # pages every table shares
+    ws_sp = ff.shared_prefix_workspace(Bd, Hq, Hkv, D, table_np.shape[1], SB, device=dev)
 
     def dec(i):
         kp, vp, _, _ = pools[i % layers]
         ff.paged_attention(qd, kp, vp, bt_d, cx_d, out=od, workspace=ws, stream=stream)
+
+    def dec_sp(i):
+        kp, vp, _, _ = pools[i % layers]
+        ff.paged_attention_shared_prefix(qd, kp, vp, bt_d, cx_d, SB, out=od, workspace=ws_sp, stream=stream)
 
     def chunk_append(i):
         kp, vp, _, _ = pools[i % layers]
@@ -234,7 +240,7 @@ def c4_config(ff, torch, dev, stream, layers=2, calls=30, seed=4):
     def step(i):
         kp, vp, _, _ = pools[i % layers]
         ff.append_kv_cache(kd, vd, kp, vp, bt_d, cx_d, stream=stream)
-        ff.paged_attention(qd, kp, vp, bt_d, cx_d, out=od, workspace=ws, stream=stream)
+        ff.paged_attention_shared_prefix(qd, kp, vp, bt_d, cx_d, SB, out=od, workspace=ws_sp, stream=stream)
         ff.append_kv_cache(kc, vc, kp, vp, bt_c, cx_c, stream=stream)
         ff.paged_prefill(qc, kp, vp, bt_c, cx_c, out=oc, stream=stream)
 
@@ -242,6 +248,7 @@ def c4_config(ff, torch, dev, stream, layers=2, calls=30, seed=4):
         chunk_append(i)  # the chunks' K/V are in the pages before any prefill reads them
     torch.cuda.synchronize()
     us_dec = _events_us(dec, calls, stream)
+    us_dsp = _events_us(dec_sp, calls, stream)
     us_app = _events_us(chunk_append, calls, stream)
     us_pre = _events_us(pre, calls, stream)
     us_step = _events_us(step, calls, stream)
@@ -262,6 +269,11 @@ def c4_config(ff, torch, dev, stream, layers=2, calls=30, seed=4):
                    "unique_TB_per_s": unique / (us_dec * 1e-6) / 1e12,
                    "unique_pct_of_peak": unique / (us_dec * 1e-6) / 1e12 / HBM_PEAK_TBS * 100,
                    "effective_TB_per_s_logical": logical / (us_dec * 1e-6) / 1e12},
+        # the same decode with the shared pages attended once for all rows (ffkv_paged_decode_shared_prefix)
+        "decode_shared_prefix": {"rows": Bd, "shared_blocks": SB, "us_per_call": us_dsp,
+                                 "unique_TB_per_s": unique / (us_dsp * 1e-6) / 1e12,
+                                 "unique_pct_of_peak": unique / (us_dsp * 1e-6) / 1e12 / HBM_PEAK_TBS * 100,
+                                 "speedup_vs_plain": us_dec / us_dsp},
         "chunk_append": {"tokens": Bc * CH, "us_per_call": us_app, "bytes": app_bytes,
                          "GB_per_s": app_bytes / (us_app * 1e-6) / 1e9},
         "prefill": {"rows": Bc, "chunk": CH, "us_per_call": us_pre, "causal_flops": flops,
