@@ -93,6 +93,19 @@ constexpr int kMfmaWaves =
                                                 : (CT == FP8 ? FFKV_MFMA_WAVES128_FP8 : FFKV_MFMA_WAVES128_I8))
                          : (kMfmaDepth<CT> > 1 ? 3 : 4));
 
+#ifndef FFKV_DECODE_TRV
+#define FFKV_DECODE_TRV 1  // V^T operands through transposed LDS reads (ds_read_b64_tr_b16)
+#endif
+
+// Position of element (token t, dim d) of a wave's V tile: 16-byte chunks XOR-swizzled by row so that the four
+// rows of one transposed read (two chunks each) sit on distinct banks.
+template <int D>
+__device__ __forceinline__ int vt_pos(int t, int d)
+{
+    const int sw = D == 64 ? 2 * ((t >> 1) & 3) : 2 * (t & 7);
+    return t * D + (((d >> 3) ^ sw) << 3) + (d & 7);
+}
+
 // Work item i (blockIdx.x) of W (gridDim.x); KV heads blockIdx.y*NW .. +NW, one per wave.
 template <int CT, int QT, int D>
 __global__ __launch_bounds__(64 * FFKV_MFMA_MAX_WAVES) __attribute__((amdgpu_waves_per_eu(kMfmaWaves<CT, QT, D>, 8)))
@@ -360,7 +373,11 @@ void paged_decode_mfma(DecodeArgs a)
         for (int j = 0; j < KSTEPS; ++j)
         {
             const u32x4 w = tok_ok ? mword(r.v, j) : u32x4{0u, 0u, 0u, 0u};
+#if FFKV_DECODE_TRV
+            *reinterpret_cast<u32x4*>(sv + vt_pos<D>(c, dim_of<CT>(j, g))) = w;
+#else
             *reinterpret_cast<u32x4*>(sv + lds_pos<D>(c, dim_of<CT>(j, g))) = w;
+#endif
         }
         s = f32x4{0.0f, 0.0f, 0.0f, 0.0f};  // lane (c, g) gets tokens 4g + i of head c
 #pragma unroll
@@ -443,11 +460,19 @@ void paged_decode_mfma(DecodeArgs a)
 #pragma unroll
         for (int n = 0; n < NT; ++n)
         {
+#if FFKV_DECODE_TRV
+            // transposed read: lane 4r + q of group g supplies dims 16n + 4q .. +3 of token 4g + r; lane c
+            // receives dim 16n + c of tokens 4g .. 4g + 3
+            const auto raw = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+                (__attribute__((address_space(3))) bf16x4*)(sv + vt_pos<D>(4 * g + (c >> 2), 16 * n + 4 * (c & 3))));
+            const typename M::x4 vt = __builtin_bit_cast(typename M::x4, raw);
+#else
             const uint32_t v0 = sv[lds_pos<D>(4 * g + 0, 16 * n + c)];
             const uint32_t v1 = sv[lds_pos<D>(4 * g + 1, 16 * n + c)];
             const uint32_t v2 = sv[lds_pos<D>(4 * g + 2, 16 * n + c)];
             const uint32_t v3 = sv[lds_pos<D>(4 * g + 3, 16 * n + c)];
             const typename M::x4 vt = __builtin_bit_cast(typename M::x4, u32x2{v0 | (v1 << 16), v2 | (v3 << 16)});
+#endif
             acc[n] = M::mma16(vt, phi, acc[n]);
             acc[n] = M::mma16(vt, plo, acc[n]);
         }
