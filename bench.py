@@ -398,6 +398,8 @@ def main(argv=None) -> int:
     ap.add_argument("--no-bulk", action="store_true", help="skip the bulk-append measurement")
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the other BASELINE configurations (C3, C4, C5 int8/fp8) and the rope+append figures")
+    ap.add_argument("--configs", default="all",
+                    help="comma-separated subset of C3,C5_int8,C5_fp8,C4,rope_append,C2_decode_step_host (default all)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run one 1 GiB device-to-device copy (a kernel of known read/write bytes, used to "
                          "scale rocprofv3 FETCH_SIZE/WRITE_SIZE counters)")
@@ -505,20 +507,25 @@ def main(argv=None) -> int:
     configs = None
     if not args.no_configs:
         rng = np.random.default_rng(SEED + 3)
-        configs = {
-            "C3": decode_config(ff, torch, dev, stream, "C3 Qwen2.5-7B layer: Hq28/Hkv4/D128 bf16, B=8, ctx 32768",
-                                8, 28, 4, 128, [32768] * 8, seed=3),
-            "C5_int8": decode_config(ff, torch, dev, stream, "C5 int8 KV (per-token scales): Hq32/Hkv8/D128, B=256, "
-                                     "ctx U[1024,8192]", 256, 32, 8, 128, rng.integers(1024, 8193, size=256),
-                                     kv="i8", seed=5),
-            "C5_fp8": decode_config(ff, torch, dev, stream, "C5 fp8 e4m3 KV (per-head scales): Hq32/Hkv8/D128, B=256, "
-                                    "ctx U[1024,8192]", 256, 32, 8, 128, rng.integers(1024, 8193, size=256),
-                                    kv="fp8", seed=6),
-            "C4": c4_config(ff, torch, dev, stream),
-            "rope_append": rope_append_config(ff, torch, dev, stream),
-            "C2_decode_step_host": decode_step_config(ff, torch, dev, stream, ctx_np, table_np, N, pools, q, k_new,
-                                                      v_new, out, ws, max_ctx),
+        makers = {
+            "C3": lambda: decode_config(ff, torch, dev, stream, "C3 Qwen2.5-7B layer: Hq28/Hkv4/D128 bf16, B=8, "
+                                        "ctx 32768", 8, 28, 4, 128, [32768] * 8, seed=3),
+            "C5_int8": lambda: decode_config(ff, torch, dev, stream, "C5 int8 KV (per-token scales): Hq32/Hkv8/D128, "
+                                             "B=256, ctx U[1024,8192]", 256, 32, 8, 128, c5_ctx[0], kv="i8", seed=5),
+            "C5_fp8": lambda: decode_config(ff, torch, dev, stream, "C5 fp8 e4m3 KV (per-head scales): Hq32/Hkv8/D128, "
+                                            "B=256, ctx U[1024,8192]", 256, 32, 8, 128, c5_ctx[1], kv="fp8", seed=6),
+            "C4": lambda: c4_config(ff, torch, dev, stream),
+            "rope_append": lambda: rope_append_config(ff, torch, dev, stream),
+            "C2_decode_step_host": lambda: decode_step_config(ff, torch, dev, stream, ctx_np, table_np, N, pools, q,
+                                                              k_new, v_new, out, ws, max_ctx),
         }
+        c5_ctx = [rng.integers(1024, 8193, size=256), rng.integers(1024, 8193, size=256)]
+        want = list(makers) if args.configs == "all" else [x for x in args.configs.split(",") if x]
+        unknown = [x for x in want if x not in makers]
+        if unknown:
+            print(f"unknown --configs entries {unknown}; choose from {list(makers)}", file=sys.stderr)
+            return 2
+        configs = {name: makers[name]() for name in want}
 
     # Layer-0 output for the parity figure and the CPU baseline on the same inputs.
     kp0, vp0 = pools[0]

@@ -89,7 +89,7 @@ bool is_gpu(const Tensor& t) { return t.device() == Device::GPU; }
 int code(DType d) { return static_cast<int>(d); }
 
 void decode(Tensor& q, Tensor& k, Tensor& v, const float* k_scale, const float* v_scale, Tensor& out,
-            void* block_table, int kv_head_num, int max_context_blocks, const int* context_lens)
+            void* block_table, int kv_head_num, int max_context_blocks, const int* context_lens, int shared_blocks = 0)
 {
     if (q.shape().size() != 4 || k.shape().size() != 4 || !is_gpu(q) || !is_gpu(k) || !is_gpu(v) || !is_gpu(out))
         return fail("PagedAttention: q must be [B, S, Hq, D] and all tensors on the GPU");
@@ -100,13 +100,16 @@ void decode(Tensor& q, Tensor& k, Tensor& v, const float* k_scale, const float* 
         return fail("PagedAttention: output must hold B*Hq*D elements of q's dtype");
     if (k.shape()[2] != kv_head_num || k.shape()[3] != D || v.shape() != k.shape() || v.dtype() != k.dtype())
         return fail("PagedAttention: k/v caches must both be [num_blocks, 16, kv_head_num, head_dim]");
-    const size_t need = ffkv_decode_workspace_bytes(B, Hq, D, max_context_blocks, 0);
+    const size_t need = shared_blocks > 0 ? ffkv_decode_shared_prefix_workspace_bytes(B, Hq, kv_head_num, D,
+                                                                                       max_context_blocks, 0,
+                                                                                       shared_blocks)
+                                          : ffkv_decode_workspace_bytes(B, Hq, D, max_context_blocks, 0);
     size_t       have = 0;
     void*        ws = workspace(need, have);
-    const int rc = ffkv_paged_decode(q.data(), out.data(), code(q.dtype()), k.data(), v.data(), code(k.dtype()),
-                                     k_scale, v_scale, reinterpret_cast<const int32_t*>(block_table), context_lens, B,
-                                     Hq, kv_head_num, D, FFKV_BLOCK_SIZE, max_context_blocks,
-                                     static_cast<int>(k.shape()[0]), 0, 0.0f, ws, have, t_stream);
+    const int rc = ffkv_paged_decode_shared_prefix(
+        q.data(), out.data(), code(q.dtype()), k.data(), v.data(), code(k.dtype()), k_scale, v_scale,
+        reinterpret_cast<const int32_t*>(block_table), context_lens, B, Hq, kv_head_num, D, FFKV_BLOCK_SIZE,
+        max_context_blocks, static_cast<int>(k.shape()[0]), 0, 0.0f, shared_blocks, ws, have, t_stream);
     report(rc, "PagedAttention failed");
 }
 
@@ -197,6 +200,15 @@ void attention(Tensor& q, Tensor& k_cache, Tensor& v_cache, const Tensor& k_scal
                        kv_cache_block_table, kv_head_num, seq_len, max_context_blocks, context_lens);
     decode(q, k_cache, v_cache, k_scale.data_as<const float>(), v_scale.data_as<const float>(), output,
            kv_cache_block_table, kv_head_num, max_context_blocks, context_lens);
+}
+
+void attention_shared_prefix(Tensor& q, Tensor& k_cache, Tensor& v_cache, Tensor& output, void* kv_cache_block_table,
+                             int kv_head_num, int max_context_blocks, const int* context_lens, int shared_blocks)
+{
+    if (kv_cache_block_table == nullptr || (q.shape().size() == 4 && q.shape()[1] != 1))
+        return fail("attention_shared_prefix: decode only (q [B, 1, Hq, D] and a block table)");
+    decode(q, k_cache, v_cache, nullptr, nullptr, output, kv_cache_block_table, kv_head_num, max_context_blocks,
+           context_lens, shared_blocks);
 }
 
 void append_kv_cache(const Tensor& k, const Tensor& v, Tensor& k_cache, Tensor& v_cache, const int* block_table,

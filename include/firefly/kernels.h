@@ -51,6 +51,16 @@ FIREFLY_API void attention(Tensor& q, Tensor& k_cache, Tensor& v_cache, const Te
                            int max_context_blocks, const int* context_lens);
 
 /**
+ * @brief Paged decode of a batch whose block tables share their first shared_blocks entries (radix-tree prefix
+ * sharing): the shared pages are attended once for all rows (ffkv_paged_decode_shared_prefix).  Same tensors and
+ * results as the decode branch of attention(); no counterpart in the reference, whose decode reads shared pages
+ * once per row.  shared_blocks = 0 is the plain decode.
+ */
+FIREFLY_API void attention_shared_prefix(Tensor& q, Tensor& k_cache, Tensor& v_cache, Tensor& output,
+                                         void* kv_cache_block_table, int kv_head_num, int max_context_blocks,
+                                         const int* context_lens, int shared_blocks);
+
+/**
  * @brief Write new K/V tokens into their pages (the reference's append_kv_cache kernel).
  *
  * k, v [B, S, Hkv, D] (F32/F16/BF16); k_cache, v_cache [num_blocks, 16, Hkv, D]; token t of row b goes to

@@ -39,6 +39,8 @@ def shim(ff):
     lib.kas_contiguous_prefill.argtypes = [vp] * 4 + [i] * 6 + [vp]
     lib.kas_paged_prefill.restype = i
     lib.kas_paged_prefill.argtypes = [vp] * 8 + [i] * 9 + [vp]
+    lib.kas_decode_shared_prefix.restype = i
+    lib.kas_decode_shared_prefix.argtypes = [vp] * 6 + [i] * 9 + [vp]
     return lib
 
 
@@ -166,3 +168,27 @@ def test_cxx_api_rope_then_append(shim, gpu, act, kv, fused):
     assert np.array_equal(conv(dv).view(np.uint8), rv.view(np.uint8))
     if c.kv == O.DTYPE_I8:
         assert np.array_equal(dks.cpu().numpy().view(np.uint32), rks.view(np.uint32))
+
+
+@pytest.mark.gpu
+def test_cxx_api_decode_shared_prefix(shim, gpu):
+    """kernels::attention_shared_prefix on 24 rows over a 32-page shared prefix, against the CPU checker."""
+    import torch
+
+    import gpu_util as gu
+
+    rng = np.random.default_rng(60)
+    ctx = 512 + rng.integers(0, 400, size=24)
+    c = cases.make_case(60, 24, 32, 8, 128, ctx, act="bf16", shared_prefix_blocks=32)
+    kp, vp, _, _, _, out32 = cases.oracle_step(c)
+    dk, dv = gu.to_dev(kp, c.kv, gpu), gu.to_dev(vp, c.kv, gpu)
+    q = gu.to_dev(c.q, c.act, gpu)
+    bt, cx = torch.from_numpy(c.block_table).to(gpu), torch.from_numpy(c.ctx).to(gpu)
+    out = torch.empty((c.B, 1, c.Hq * c.D), dtype=q.dtype, device=gpu)
+    rc = shim.kas_decode_shared_prefix(q.data_ptr(), dk.data_ptr(), dv.data_ptr(), out.data_ptr(), bt.data_ptr(),
+                                       cx.data_ptr(), c.B, c.Hq, c.Hkv, c.D, c.num_blocks, c.max_blocks, c.act, c.kv,
+                                       32, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert rc == 0, shim.kas_last_error()
+    got = out.float().cpu().numpy().reshape(out32.shape)
+    assert _excess_bf16(got, out32) <= 2e-3
