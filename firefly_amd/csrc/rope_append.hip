@@ -15,14 +15,20 @@
 // without fused multiply-add, then rounded to the tensor dtype.  (The reference computes the same quantities
 // with fast-math powf/cosf/sinf, whose error grows with the angle; it is not bit-reproducible.)
 //
-// Layout: one workgroup per token (grid-stride over tokens).  The D/2 (cos, sin) pairs of the token are
-// computed once into LDS, then its Hq + Hkv head rows are spread over the workgroup, D/16 lanes per row, each
-// lane holding 8 dims of the low half and the matching 8 dims of the high half.
+// Layout: a workgroup of 256 threads takes 256 / (D/2) tokens per iteration (grid-stride): each thread computes
+// one (cos, sin) pair of one of them into LDS (inv_freq once per thread, outside the loop), and the tokens' Hq +
+// Hkv head rows are spread over the workgroup, D/16 lanes per row, each lane holding 8 dims of the low half and
+// the matching 8 dims of the high half.  A thread issues the loads of two rows before rotating either, and the
+// first two rows' loads go out before the table's barrier, so the loads overlap the double-precision sin/cos.
 #include "ffkv_device.h"
 #include "ffkv_internal.h"
 
 namespace ffkv
 {
+
+#ifndef FFKV_ROPE_NB
+#define FFKV_ROPE_NB 1
+#endif
 
 namespace
 {
@@ -105,110 +111,141 @@ __device__ __forceinline__ void append_row(void* cache, float* scales, int h, si
 
 }  // namespace
 
-template <int SRC, int CACHE, int D, bool APPEND>
+// TPI tokens per iteration: 256 / (D/2) for bulk calls (every thread computes one (cos, sin) pair), 1 for
+// small calls, which then spread over more workgroups.
+template <int SRC, int CACHE, int D, bool APPEND, int TPI>
 __global__ __launch_bounds__(256) void rope_append_kernel(RopeArgs a)
 {
     constexpr int HALF = D / 2;
-    constexpr int LPR = D / 16;      // lanes per head row
-    constexpr int RPP = 256 / LPR;   // head rows per pass of the workgroup
-    __shared__ float s_cos[HALF], s_sin[HALF];
+    constexpr int LPR = D / 16;     // lanes per head row
+    constexpr int RPP = 256 / LPR;  // head rows per pass of the workgroup
+    constexpr int NB = FFKV_ROPE_NB; // rows per thread whose loads are issued before any of them is rotated
+    __shared__ float s_cos[TPI][HALF], s_sin[TPI][HALF];
 
     const int     lane = threadIdx.x % LPR;
     const int     rsub = threadIdx.x / LPR;
     const int64_t tokens = static_cast<int64_t>(a.batch) * a.seq_len;
-    const int     rows = a.num_heads + a.num_kv_heads;
+    const int     rows = a.num_heads + a.num_kv_heads;  // head rows of one token
+    const int     iter_rows = TPI * rows;
 
-    for (int64_t tok = blockIdx.x; tok < tokens; tok += gridDim.x)
+    // inv_freq of this thread's pair, once (:74-76)
+    const int   my_i = threadIdx.x % HALF;
+    const int   my_t = threadIdx.x / HALF;  // table row this thread fills (threads beyond TPI rows fill none)
+    const float inv_freq = static_cast<float>(pow(static_cast<double>(a.theta), -2.0 * my_i / D));
+
+    for (int64_t tok0 = static_cast<int64_t>(blockIdx.x) * TPI; tok0 < tokens; tok0 += static_cast<int64_t>(gridDim.x) * TPI)
     {
-        const int     b = static_cast<int>(tok / a.seq_len);
-        const int     t = static_cast<int>(tok % a.seq_len);
-        const int64_t pos = static_cast<int64_t>(a.context_lens ? a.context_lens[b] : 0) + t;  // rope.cu:36-37
-
-        __syncthreads();  // the previous token's rows are done with the table
-        if (threadIdx.x < HALF)
+        __syncthreads();  // the previous tokens' rows are done with the table
         {
-            const int   i = threadIdx.x;
-            const float inv_freq = static_cast<float>(pow(static_cast<double>(a.theta), -2.0 * i / D));  // :74-76
-            const float ang = static_cast<float>(pos) * inv_freq;                                          // :77
-            s_cos[i] = static_cast<float>(cos(static_cast<double>(ang)));
-            s_sin[i] = static_cast<float>(sin(static_cast<double>(ang)));
-        }
-        __syncthreads();
-
-        // Page slot of this token (uniform over the workgroup), as the append kernel computes it.
-        bool   ok = false;
-        size_t slot_row = 0;  // (phys * 16 + pos % 16) * Hkv
-        if constexpr (APPEND)
-        {
-            ok = pos >= 0 && (pos >> 4) < a.max_blocks;
-            if (ok)
+            const int64_t tok = tok0 + my_t;
+            if (my_t < TPI && tok < tokens)
             {
-                const int phys = a.block_table[static_cast<int64_t>(b) * a.max_blocks + (pos >> 4)];
-                ok = phys >= 0 && phys < a.num_blocks;
-                slot_row = (static_cast<size_t>(phys) * kBlockSize + (pos & 15)) * a.num_kv_heads;
+                const int     b = static_cast<int>(tok / a.seq_len);
+                const int     t = static_cast<int>(tok % a.seq_len);
+                const int64_t pos = static_cast<int64_t>(a.context_lens ? a.context_lens[b] : 0) + t;  // :36-37
+                const float   ang = static_cast<float>(pos) * inv_freq;                                // :77
+                s_cos[my_t][my_i] = static_cast<float>(cos(static_cast<double>(ang)));
+                s_sin[my_t][my_i] = static_cast<float>(sin(static_cast<double>(ang)));
             }
         }
 
-        for (int u = rsub; u < rows; u += RPP)
+        // Row u of the iteration: token tok0 + u / rows, head row u % rows (q heads, then kv heads).  Loads of NB
+        // rows go out first (before the table barrier for the first batch), then the rows are rotated and stored.
+        // every thread runs the first batch (possibly without rows) so that all reach the table barrier
+        for (int u0 = rsub;; u0 += NB * RPP)
         {
-            const bool   is_q = u < a.num_heads;
-            const int    h = is_q ? u : u - a.num_heads;
-            void*        base = is_q ? a.q : a.k;
-            const size_t row = (static_cast<size_t>(tok) * (is_q ? a.num_heads : a.num_kv_heads) + h) * D;
-            Raw8         rl, rh;
-            load_raw8<SRC>(base, row + 8 * lane, rl);
-            load_raw8<SRC>(base, row + HALF + 8 * lane, rh);
-            float xl[8], xh[8], yl[8], yh[8];
-            unpack8<SRC>(rl, xl);
-            unpack8<SRC>(rh, xh);
+            Raw8 rl[NB], rh[NB], vl[NB], vh[NB];
+            bool act[NB], isq[NB];
+            int  tl[NB], hh[NB];
+            size_t rowoff[NB];
 #pragma unroll
-            for (int e = 0; e < 8; ++e)
+            for (int k = 0; k < NB; ++k)
             {
-                const float c = s_cos[8 * lane + e];
-                const float s = s_sin[8 * lane + e];
-                yl[e] = rot_lo(xl[e], xh[e], c, s);
-                yh[e] = rot_hi(xl[e], xh[e], c, s);
-            }
-            pack8<SRC>(yl, rl);
-            pack8<SRC>(yh, rh);
-            store_raw8<SRC>(base, row + 8 * lane, rl);
-            store_raw8<SRC>(base, row + HALF + 8 * lane, rh);
-
-            if constexpr (APPEND)
-            {
-                // `ok` is per token and `is_q` per row: the row's lanes, the only ones the int8 reduction reads,
-                // take the same branch.
-                if (!is_q && ok)
+                const int     u = u0 + k * RPP;
+                const int     tli = u / rows;
+                const int64_t tok = tok0 + tli;
+                act[k] = u < iter_rows && tok < tokens;
+                tl[k] = tli;
+                const int hr = u % rows;
+                isq[k] = hr < a.num_heads;
+                hh[k] = isq[k] ? hr : hr - a.num_heads;
+                rowoff[k] = (static_cast<size_t>(act[k] ? tok : 0) * (isq[k] ? a.num_heads : a.num_kv_heads) + hh[k]) * D;
+                if (act[k])
                 {
-                    const size_t dst_row = slot_row + h;
+                    const void* base = isq[k] ? a.q : a.k;
+                    load_raw8<SRC>(base, rowoff[k] + 8 * lane, rl[k]);
+                    load_raw8<SRC>(base, rowoff[k] + HALF + 8 * lane, rh[k]);
+                    if constexpr (APPEND)
+                    {
+                        if (!isq[k])
+                        {
+                            load_raw8<SRC>(a.v, rowoff[k] + 8 * lane, vl[k]);
+                            load_raw8<SRC>(a.v, rowoff[k] + HALF + 8 * lane, vh[k]);
+                        }
+                    }
+                }
+            }
+            if (u0 == rsub) __syncthreads();  // the table of these tokens is written (first batch: every thread)
+#pragma unroll
+            for (int k = 0; k < NB; ++k)
+            {
+                if (!act[k]) continue;
+                float xl[8], xh[8], yl[8], yh[8];
+                unpack8<SRC>(rl[k], xl);
+                unpack8<SRC>(rh[k], xh);
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                {
+                    const float c = s_cos[tl[k]][8 * lane + e];
+                    const float s = s_sin[tl[k]][8 * lane + e];
+                    yl[e] = rot_lo(xl[e], xh[e], c, s);
+                    yh[e] = rot_hi(xl[e], xh[e], c, s);
+                }
+                pack8<SRC>(yl, rl[k]);
+                pack8<SRC>(yh, rh[k]);
+                void* base = isq[k] ? a.q : a.k;
+                store_raw8<SRC>(base, rowoff[k] + 8 * lane, rl[k]);
+                store_raw8<SRC>(base, rowoff[k] + HALF + 8 * lane, rh[k]);
+
+                if constexpr (APPEND)
+                {
+                    if (isq[k]) continue;
+                    // page slot of the row's token, as the append kernel computes it
+                    const int64_t tok = tok0 + tl[k];
+                    const int     b = static_cast<int>(tok / a.seq_len);
+                    const int     t = static_cast<int>(tok % a.seq_len);
+                    const int64_t pos = static_cast<int64_t>(a.context_lens ? a.context_lens[b] : 0) + t;
+                    bool          ok = pos >= 0 && (pos >> 4) < a.max_blocks;
+                    int           phys = -1;
+                    if (ok)
+                    {
+                        phys = a.block_table[static_cast<int64_t>(b) * a.max_blocks + (pos >> 4)];
+                        ok = phys >= 0 && phys < a.num_blocks;
+                    }
+                    // `ok` is per token, the same for the row's LPR lanes (the only ones the int8 reduction reads)
+                    if (!ok) continue;
+                    const int    h = hh[k];
+                    const size_t dst_row = (static_cast<size_t>(phys) * kBlockSize + (pos & 15)) * a.num_kv_heads + h;
                     // k as stored in its dtype (the values the reference's append would read back)
-                    unpack8<SRC>(rl, yl);
-                    unpack8<SRC>(rh, yh);
+                    unpack8<SRC>(rl[k], yl);
+                    unpack8<SRC>(rh[k], yh);
                     if constexpr (SRC == CACHE)
                     {
-                        store_raw8<CACHE>(a.k_cache, dst_row * D + 8 * lane, rl);
-                        store_raw8<CACHE>(a.k_cache, dst_row * D + HALF + 8 * lane, rh);
+                        store_raw8<CACHE>(a.k_cache, dst_row * D + 8 * lane, rl[k]);
+                        store_raw8<CACHE>(a.k_cache, dst_row * D + HALF + 8 * lane, rh[k]);
+                        store_raw8<CACHE>(a.v_cache, dst_row * D + 8 * lane, vl[k]);
+                        store_raw8<CACHE>(a.v_cache, dst_row * D + HALF + 8 * lane, vh[k]);
                     }
                     else
                     {
                         append_row<CACHE, D, LPR>(a.k_cache, a.k_scale, h, dst_row, lane, yl, yh);
-                    }
-                    Raw8 vl, vh;
-                    load_raw8<SRC>(a.v, row + 8 * lane, vl);
-                    load_raw8<SRC>(a.v, row + HALF + 8 * lane, vh);
-                    if constexpr (SRC == CACHE)
-                    {
-                        store_raw8<CACHE>(a.v_cache, dst_row * D + 8 * lane, vl);
-                        store_raw8<CACHE>(a.v_cache, dst_row * D + HALF + 8 * lane, vh);
-                    }
-                    else
-                    {
-                        unpack8<SRC>(vl, xl);
-                        unpack8<SRC>(vh, xh);
+                        unpack8<SRC>(vl[k], xl);
+                        unpack8<SRC>(vh[k], xh);
                         append_row<CACHE, D, LPR>(a.v_cache, a.v_scale, h, dst_row, lane, xl, xh);
                     }
                 }
             }
+            if (u0 + NB * RPP >= iter_rows) break;
         }
     }
 }
@@ -216,24 +253,34 @@ __global__ __launch_bounds__(256) void rope_append_kernel(RopeArgs a)
 namespace
 {
 
+template <int SRC, int CACHE, bool APPEND, int D>
+hipError_t launch_ra_t(const RopeArgs& a, hipStream_t stream)
+{
+    constexpr int64_t kBulk = 256 / (D / 2);
+    const int64_t     tokens = static_cast<int64_t>(a.batch) * a.seq_len;
+    const bool        bulk = tokens >= 2048;  // small calls: one token per workgroup iteration, more workgroups
+    const int64_t     tpi = bulk ? kBulk : 1;
+    const int64_t     iters = (tokens + tpi - 1) / tpi;
+    const auto        grid = dim3(static_cast<unsigned>(iters < 16384 ? iters : 16384));
+    if (bulk)
+        hipLaunchKernelGGL((rope_append_kernel<SRC, CACHE, D, APPEND, kBulk>), grid, dim3(256), 0, stream, a);
+    else
+        hipLaunchKernelGGL((rope_append_kernel<SRC, CACHE, D, APPEND, 1>), grid, dim3(256), 0, stream, a);
+    return hipGetLastError();
+}
+
 template <int SRC, int CACHE, bool APPEND>
 hipError_t launch_ra_d(const RopeArgs& a, hipStream_t stream)
 {
-    const int64_t tokens = static_cast<int64_t>(a.batch) * a.seq_len;
-    const auto    grid = dim3(static_cast<unsigned>(tokens < 16384 ? tokens : 16384));
     switch (a.head_dim)
     {
         case 64:
-            hipLaunchKernelGGL((rope_append_kernel<SRC, CACHE, 64, APPEND>), grid, dim3(256), 0, stream, a);
-            break;
+            return launch_ra_t<SRC, CACHE, APPEND, 64>(a, stream);
         case 128:
-            hipLaunchKernelGGL((rope_append_kernel<SRC, CACHE, 128, APPEND>), grid, dim3(256), 0, stream, a);
-            break;
+            return launch_ra_t<SRC, CACHE, APPEND, 128>(a, stream);
         default:
-            hipLaunchKernelGGL((rope_append_kernel<SRC, CACHE, 256, APPEND>), grid, dim3(256), 0, stream, a);
-            break;
+            return launch_ra_t<SRC, CACHE, APPEND, 256>(a, stream);
     }
-    return hipGetLastError();
 }
 
 template <int SRC>
