@@ -3,8 +3,9 @@
 Workload: Qwen3-8B layer shape, bf16 KV, 32 query heads, 8 KV heads (GQA 4),
 head_dim 128, block size 16, batch 64, pre-append context lengths uniform in [512, 4096], block tables a
 seeded permutation of a pool sized to total blocks + 10 %, Q/K/V ~ N(0,1).  One step = append one new K/V
-token per sequence (ffkv_append) and run decode attention over context_lens + 1 tokens (ffkv_paged_decode),
-on one layer's pool.  Steps rotate over `--layers` independent pools (as a model's layers do), so the
+token per sequence and run decode attention over context_lens + 1 tokens, on one layer's pool, issued as one
+call (ffkv_append_paged_decode: the decode kernel writes each row's new token into its page and attends it);
+`step_ms_two_calls` times the same steps as ffkv_append then ffkv_paged_decode.  Steps rotate over `--layers` independent pools (as a model's layers do), so the
 working set (~2.7 GB at 4 layers) is far beyond the 256 MB Infinity Cache and every step streams its KV from
 HBM.
 
@@ -437,6 +438,12 @@ def main(argv=None) -> int:
 
     def step(i):
         kp, vp = pools[i % args.layers]
+        # the decode step as one call: append 1 token per row, then decode (ffkv_append_paged_decode)
+        ff.append_paged_attention(k_new, v_new, q, kp, vp, table, ctx, out=out, max_context_len=max_ctx,
+                                  workspace=ws, stream=stream)
+
+    def step_separate(i):
+        kp, vp = pools[i % args.layers]
         ff.append_kv_cache(k_new, v_new, kp, vp, table, ctx, stream=stream)
         ff.paged_attention(q, kp, vp, table, ctx, out=out, max_context_len=max_ctx, workspace=ws, stream=stream)
 
@@ -458,6 +465,16 @@ def main(argv=None) -> int:
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms_per_step = wall / args.steps * 1e3
+
+    # The same steps as two calls (ffkv_append, then ffkv_paged_decode), as the reference's model issues them.
+    for i in range(args.warmup):
+        step_separate(i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step_separate(i)
+    torch.cuda.synchronize()
+    ms_per_step_separate = (time.perf_counter() - t0) / args.steps * 1e3
 
     # Per-call durations with HIP events on the launch stream (same loop, events around each call).
     n_ev = args.steps
@@ -556,6 +573,7 @@ def main(argv=None) -> int:
         "decode_tokens_per_s": B / (ms_per_step * 1e-3),
         "decode_tokens_per_s_qwen3_8b_36_layers": B / (ms_per_step * 1e-3 * 36),
         "decode_call_ms": dec_ms,
+        "step_ms_two_calls": ms_per_step_separate,
         "append_call_us": app_ms * 1e3,
         "append_bulk": bulk,
         "roofline": {"kernel": "ffkv_paged_decode (paged_decode_mfma + paged_decode_mfma_merge)", "bound": "hbm",

@@ -62,6 +62,9 @@ def _load() -> ctypes.CDLL:
     lib.ffkv_paged_decode_shared_prefix.restype = i32
     lib.ffkv_paged_decode_shared_prefix.argtypes = [vp, vp, i32, vp, vp, i32, vp, vp, vp, vp, i32, i32, i32, i32,
                                                     i32, i32, i32, i32, f32, i32, vp, sz, vp]
+    lib.ffkv_append_paged_decode.restype = i32
+    lib.ffkv_append_paged_decode.argtypes = [vp, vp, i32, vp, vp, i32, vp, vp, i32, vp, vp, vp, vp, i32, i32, i32,
+                                             i32, i32, i32, i32, i32, f32, vp, sz, vp]
     lib.ffkv_paged_prefill.restype = i32
     lib.ffkv_paged_prefill.argtypes = [vp, vp, i32, vp, vp, i32, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32,
                                        i32, i32, ctypes.c_float, vp]
@@ -218,6 +221,29 @@ def paged_attention_shared_prefix(q, k_cache, v_cache, block_table, context_lens
                                               _ptr(block_table), _ptr(context_lens), B, Hq, Hkv, D, BLOCK_SIZE,
                                               max_blocks, N, max_context_len, float(scale), int(shared_blocks),
                                               _ptr(workspace), ws_bytes, _stream(stream)))
+    return out
+
+
+def append_paged_attention(k_new, v_new, q, k_cache, v_cache, block_table, context_lens, out=None, k_scale=None,
+                           v_scale=None, max_context_len: int = 0, scale: float = 0.0, workspace=None,
+                           num_blocks: int | None = None, stream=None):
+    """``append_kv_cache(k_new, v_new, ...)`` (one token per row) then ``paged_attention``, as one call
+    (``ffkv_append_paged_decode``; a single launch for 16-bit caches fed in their own dtype)."""
+    import torch
+
+    B = q.shape[0]
+    Hq, D = q.shape[-2], q.shape[-1]
+    Hkv = k_cache.shape[2]
+    if out is None:
+        out = torch.empty((B, 1, Hq * D), dtype=q.dtype, device=q.device)
+    max_blocks = block_table.shape[-1]
+    N = k_cache.shape[0] if num_blocks is None else num_blocks
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    check(lib.ffkv_append_paged_decode(_ptr(k_new), _ptr(v_new), torch_dtype_code(k_new), _ptr(q), _ptr(out),
+                                       torch_dtype_code(q), _ptr(k_cache), _ptr(v_cache), torch_dtype_code(k_cache),
+                                       _ptr(k_scale), _ptr(v_scale), _ptr(block_table), _ptr(context_lens), B, Hq,
+                                       Hkv, D, BLOCK_SIZE, max_blocks, N, max_context_len, float(scale),
+                                       _ptr(workspace), ws_bytes, _stream(stream)))
     return out
 
 

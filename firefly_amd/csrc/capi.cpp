@@ -376,7 +376,7 @@ int decode_impl(const void* q, void* out, int qo_dtype, const void* k_cache, con
                 const float* k_scale, const float* v_scale, const int32_t* block_table, const int32_t* context_lens,
                 int batch, int num_heads, int num_kv_heads, int head_dim, int block_size, int max_blocks,
                 int num_blocks, int max_context_len, float scale, int shared_blocks, void* workspace,
-                size_t workspace_bytes, void* stream)
+                size_t workspace_bytes, void* stream, const void* k_new = nullptr, const void* v_new = nullptr)
 {
     if (block_size != FFKV_BLOCK_SIZE) return fail(FFKV_ERR_UNSUPPORTED, "block_size must be 16, got %d", block_size);
     if (!is_act(qo_dtype)) return fail(FFKV_ERR_UNSUPPORTED, "unsupported q/out dtype %d", qo_dtype);
@@ -515,6 +515,22 @@ int decode_impl(const void* q, void* out, int qo_dtype, const void* k_cache, con
         p.ws_acc = a.ws_acc;
         e = ffkv::launch_prefix_partials(p, s);
     }
+    if (k_new != nullptr && e == hipSuccess)
+    {
+        if (mfma && skip == 0)
+        {
+            a.k_new = k_new;  // the decode kernel writes the step's token into its page and attends it
+            a.v_new = v_new;
+        }
+        else
+        {
+            ffkv::AppendArgs ap{k_new,        v_new,        const_cast<void*>(k_cache), const_cast<void*>(v_cache),
+                                const_cast<float*>(k_scale), const_cast<float*>(v_scale), block_table,
+                                context_lens, cache_dtype,  cache_dtype,  batch, 1, num_kv_heads, head_dim,
+                                max_blocks,   num_blocks};
+            e = ffkv::launch_append(ap, s);
+        }
+    }
     if (e == hipSuccess) e = mfma ? ffkv::launch_decode_mfma(a, s) : ffkv::launch_decode(a, s);
     if (owned)
     {
@@ -536,6 +552,35 @@ int ffkv_paged_decode(const void* q, void* out, int qo_dtype, const void* k_cach
     return decode_impl(q, out, qo_dtype, k_cache, v_cache, cache_dtype, k_scale, v_scale, block_table, context_lens,
                        batch, num_heads, num_kv_heads, head_dim, block_size, max_blocks, num_blocks, max_context_len,
                        scale, 0, workspace, workspace_bytes, stream);
+}
+
+int ffkv_append_paged_decode(const void* k_new, const void* v_new, int src_dtype, const void* q, void* out,
+                             int qo_dtype, void* k_cache, void* v_cache, int cache_dtype, float* k_scale,
+                             float* v_scale, const int32_t* block_table, const int32_t* context_lens, int batch,
+                             int num_heads, int num_kv_heads, int head_dim, int block_size, int max_blocks,
+                             int num_blocks, int max_context_len, float scale, void* workspace,
+                             size_t workspace_bytes, void* stream)
+{
+    if (!is_act(src_dtype)) return fail(FFKV_ERR_UNSUPPORTED, "unsupported source dtype %d", src_dtype);
+    if (batch > 0 && (!k_new || !v_new)) return fail(FFKV_ERR_INVALID_ARGUMENT, "null k_new or v_new pointer");
+    if (batch > 0 && (!aligned16(k_new) || !aligned16(v_new)))
+        return fail(FFKV_ERR_INVALID_ARGUMENT, "k_new and v_new must be 16-byte aligned");
+    // One launch when the step's k/v already have the cache's 16-bit type; otherwise the append kernel, then the
+    // decode.
+    const bool fused = src_dtype == cache_dtype && (cache_dtype == FFKV_DTYPE_BF16 || cache_dtype == FFKV_DTYPE_F16);
+    if (!fused)
+    {
+        const int rc = ffkv_append(k_new, v_new, src_dtype, k_cache, v_cache, cache_dtype, k_scale, v_scale,
+                                   block_table, context_lens, batch, 1, num_kv_heads, head_dim, block_size,
+                                   max_blocks, num_blocks, stream);
+        if (rc != FFKV_OK) return rc;
+        return ffkv_paged_decode(q, out, qo_dtype, k_cache, v_cache, cache_dtype, k_scale, v_scale, block_table,
+                                 context_lens, batch, num_heads, num_kv_heads, head_dim, block_size, max_blocks,
+                                 num_blocks, max_context_len, scale, workspace, workspace_bytes, stream);
+    }
+    return decode_impl(q, out, qo_dtype, k_cache, v_cache, cache_dtype, k_scale, v_scale, block_table, context_lens,
+                       batch, num_heads, num_kv_heads, head_dim, block_size, max_blocks, num_blocks, max_context_len,
+                       scale, 0, workspace, workspace_bytes, stream, k_new, v_new);
 }
 
 size_t ffkv_decode_shared_prefix_workspace_bytes(int batch, int num_heads, int num_kv_heads, int head_dim,

@@ -121,6 +121,11 @@ struct DecodeArgs
     int            skip_blocks;
     int            pfx_chunks;
     int            pfx_slot0;
+    // Fused append (16-bit caches, k/v in the cache dtype): [batch, 1, num_kv_heads, head_dim]; the item holding a
+    // row's last page takes the new token from here and writes it to its page slot (the first wave copies the
+    // tokens of rows cut short by cap_tokens).
+    const void*    k_new;
+    const void*    v_new;
 };
 
 hipError_t launch_append(const AppendArgs& a, hipStream_t stream);

@@ -55,6 +55,7 @@ struct PageRegs
     int   pb;  // global index of the row's first page
     int   nb;  // pages of the row
     int   lp;  // attended tokens of the row
+    int   ns;  // fused append: slot of the row's new token in this page, else -1
     float ks;  // int8 caches: K and V scale of token c (lane c of each lane group)
     float vs;
 };
@@ -137,14 +138,17 @@ void paged_decode_mfma(DecodeArgs a)
     {
         int w0, base, total;
         int toks, n, excl;  // per lane
+        int whole;          // per lane: the row's new token (position context_lens) is attended (not truncated)
     };
     auto load_win = [&](int w0, int base)
     {
         const int r = w0 + lane;
         int       t = 0;
+        int       whole = 0;
         if (r < B)
         {
             int64_t L = static_cast<int64_t>(a.context_lens[r]) + 1;  // +1: the token appended this step (:320)
+            whole = L <= a.cap_tokens;
             if (L > a.cap_tokens) L = a.cap_tokens;
             t = L < 0 ? 0 : static_cast<int>(L);
         }
@@ -160,7 +164,7 @@ void paged_decode_mfma(DecodeArgs a)
             const int o = __shfl_up(incl, off, 64);
             if (lane >= off) incl += o;
         }
-        return Win{w0, base, uniform(__shfl(incl, 63, 64)), t, n, incl - n};
+        return Win{w0, base, uniform(__shfl(incl, 63, 64)), t, n, incl - n, whole};
     };
 
     // ---- total pages P (every wave on its own, no barriers) -------------------------------------------------
@@ -178,6 +182,30 @@ void paged_decode_mfma(DecodeArgs a)
                                    f32x4{0.0f, 0.0f, 0.0f, 0.0f});
             a.ws_meta[2 * r] = -1;
             a.ws_meta[2 * r + 1] = -1;
+        }
+        if constexpr (kElemBytes<CT> == 2)
+        {
+            // Fused append, rows cut short by max_context_len: their new token is not attended, so no page
+            // holding it is staged; the first wave copies it to its slot here, as ffkv_append would.
+            uint64_t cut = first_wg && a.k_new != nullptr ? __ballot(w.w0 + lane < B && !w.whole) : 0;
+            while (cut != 0)
+            {
+                const int r = w.w0 + __ffsll(static_cast<long long>(cut)) - 1;
+                cut &= cut - 1;
+                const int64_t pos = a.context_lens[r];
+                if (pos < 0 || (pos >> 4) >= a.max_blocks) continue;
+                const int phys = a.block_table[static_cast<int64_t>(r) * a.max_blocks + (pos >> 4)];
+                if (phys < 0 || phys >= a.num_blocks) continue;
+                const size_t dst = (static_cast<size_t>(phys) * kBlockSize + (pos & 15)) * a.num_kv_heads * D;
+                const size_t src = static_cast<size_t>(r) * a.num_kv_heads * D;
+                for (int e = 8 * lane; e < a.num_kv_heads * D; e += 8 * 64)
+                {
+                    *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(const_cast<void*>(a.k_cache)) + dst + e) =
+                        *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.k_new) + src + e);
+                    *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(const_cast<void*>(a.v_cache)) + dst + e) =
+                        *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.v_new) + src + e);
+                }
+            }
         }
         P += w.total;
         if (w.w0 + 64 >= B) break;
@@ -209,14 +237,16 @@ void paged_decode_mfma(DecodeArgs a)
     {
         int            b, pb, nb, lp;
         const int32_t* table;
+        int            ns;  // fused append: slot of the new token in the row's last page, or -1
     };
     Win  win = win0;  // window of the most advanced row found so far
     auto row_at = [&](int b)  // row b, which lies in `win`
     {
         const int l = b - win.w0;
-        return LRow{b, win.base + __builtin_amdgcn_readlane(win.excl, l), __builtin_amdgcn_readlane(win.n, l),
-                    __builtin_amdgcn_readlane(win.toks, l),
-                    a.block_table + static_cast<int64_t>(b) * a.max_blocks + a.skip_blocks};
+        const int toks = __builtin_amdgcn_readlane(win.toks, l);
+        const int ns = a.k_new != nullptr && toks > 0 && __builtin_amdgcn_readlane(win.whole, l) ? (toks - 1) & 15 : -1;
+        return LRow{b, win.base + __builtin_amdgcn_readlane(win.excl, l), __builtin_amdgcn_readlane(win.n, l), toks,
+                    a.block_table + static_cast<int64_t>(b) * a.max_blocks + a.skip_blocks, ns};
     };
     auto find_page = [&](int x)  // row holding page x (x < P), moving `win` forward from its current window
     {
@@ -279,6 +309,7 @@ void paged_decode_mfma(DecodeArgs a)
         r.lp = lrow.lp;
         r.phys = phys;
         r.ok = phys >= 0 && phys < a.num_blocks;  // uniform: a masked page is skipped
+        r.ns = pg == lrow.nb - 1 ? lrow.ns : -1;  // fused append: the new token sits in the row's last page
         if (!r.ok) return;
         const size_t row_c = (static_cast<size_t>(phys) * kBlockSize + c) * a.num_kv_heads + kvh;
         if constexpr (CT == I8)
@@ -291,6 +322,12 @@ void paged_decode_mfma(DecodeArgs a)
         {
             const char* kp = static_cast<const char*>(a.k_cache) + row_c * D * 2;
             const char* vp = static_cast<const char*>(a.v_cache) + row_c * D * 2;
+            if (c == r.ns)  // fused append: the new token comes from the step's k / v (same dtype as the cache)
+            {
+                const size_t src = (static_cast<size_t>(lrow.b) * a.num_kv_heads + kvh) * D * 2;
+                kp = static_cast<const char*>(a.k_new) + src;
+                vp = static_cast<const char*>(a.v_new) + src;
+            }
 #pragma unroll
             for (int j = 0; j < KSTEPS; ++j)
             {
@@ -368,6 +405,21 @@ void paged_decode_mfma(DecodeArgs a)
     // so the next page can be loaded into r right after.
     auto stage_page = [&](int n_tok, const PageRegs<NW>& r, f32x4& s)
     {
+        if constexpr (kElemBytes<CT> == 2)
+        {
+            if (c == r.ns)  // fused append: write the new token's row into its page slot (what ffkv_append writes)
+            {
+                const size_t row_c = (static_cast<size_t>(r.phys) * kBlockSize + c) * a.num_kv_heads + kvh;
+                char*        kp = static_cast<char*>(const_cast<void*>(a.k_cache)) + row_c * D * 2;
+                char*        vp = static_cast<char*>(const_cast<void*>(a.v_cache)) + row_c * D * 2;
+#pragma unroll
+                for (int j = 0; j < KSTEPS; ++j)
+                {
+                    *reinterpret_cast<u32x4*>(kp + dim_of<CT>(j, g) * 2) = r.k[j];
+                    *reinterpret_cast<u32x4*>(vp + dim_of<CT>(j, g) * 2) = r.v[j];
+                }
+            }
+        }
         const bool tok_ok = c < n_tok;  // V[t = c], zero for slots past the row's last token
 #pragma unroll
         for (int j = 0; j < KSTEPS; ++j)

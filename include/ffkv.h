@@ -109,6 +109,24 @@ FFKV_API int ffkv_paged_decode(const void* q, void* out, int qo_dtype, const voi
                       void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * ffkv_append of one token per row (seq_len 1) followed by ffkv_paged_decode, as one call: the decode step of
+ * the reference's model (src/model/qwen_model.cu:138-146, append launch then kernels::attention).  k_new / v_new
+ * [batch, 1, num_kv_heads, head_dim] in src_dtype; the other arguments as for the two functions.  When the
+ * step's k/v already have the cache's 16-bit type it is a single launch: the decode work item that holds a
+ * row's last page reads the new token from k_new / v_new instead of the page, attends it, and writes it to its
+ * page slot (rows cut short by max_context_len get the token copied to its slot without attending it).
+ * Otherwise it runs the two functions in turn.  Either way the pages are
+ * bit-identical to ffkv_append's and the output is ffkv_paged_decode's on them.  No counterpart in the
+ * reference (two launches there).
+ */
+FFKV_API int ffkv_append_paged_decode(const void* k_new, const void* v_new, int src_dtype, const void* q, void* out,
+                                      int qo_dtype, void* k_cache, void* v_cache, int cache_dtype, float* k_scale,
+                                      float* v_scale, const int32_t* block_table, const int32_t* context_lens,
+                                      int batch, int num_heads, int num_kv_heads, int head_dim, int block_size,
+                                      int max_blocks, int num_blocks, int max_context_len, float scale,
+                                      void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * ffkv_paged_decode for a batch whose rows share a prefix of pages (the radix tree's shared blocks): entries
  * 0 .. shared_blocks - 1 of every row's block table are the same physical pages, read from row 0's table.  The
  * prefix is attended once for all rows as a matrix product (every row's queries of a kv head against each
