@@ -650,24 +650,44 @@ __global__ __launch_bounds__(256) void paged_decode_mfma_merge(DecodeArgs a)
     float     m = kNegInf, l = 0.0f, o[PER];
 #pragma unroll
     for (int k = 0; k < PER; ++k) o[k] = 0.0f;
-    for (int i = wave; i < pieces; i += 4)
+    // Wave w folds pieces w, w + 4, ...; the loads of FOLD pieces go out together before any is folded, so a
+    // row of up to 4 * FOLD pieces costs one round trip to memory instead of one per piece.
+    constexpr int FOLD = 4;
+    for (int i0 = wave; i0 < pieces; i0 += 4 * FOLD)
     {
-        const int64_t slot = i < a.pfx_chunks ? static_cast<int64_t>(a.pfx_slot0) + static_cast<int64_t>(i) * a.batch + b
-                                              : static_cast<int64_t>(i_lo + i - a.pfx_chunks) + b;
-        const float   ms = a.ws_ml[(slot * a.num_heads + h) * 2];
-        const float   ls = a.ws_ml[(slot * a.num_heads + h) * 2 + 1];
-        const float*  src = a.ws_acc + (slot * a.num_heads + h) * D + lane * PER;
-        float         x[PER];
+        float ms[FOLD], ls[FOLD], x[FOLD][PER];
 #pragma unroll
-        for (int k = 0; k < PER; ++k) x[k] = src[k];
-        if (ms == kNegInf) continue;  // segment without a valid page
-        const float mn = fmaxf(m, ms);
-        const float wa = __builtin_amdgcn_exp2f(m - mn);
-        const float wb = __builtin_amdgcn_exp2f(ms - mn);
-        l = l * wa + ls * wb;
+        for (int f = 0; f < FOLD; ++f)
+        {
+            const int i = i0 + 4 * f;
+            ms[f] = kNegInf;
+            ls[f] = 0.0f;
 #pragma unroll
-        for (int k = 0; k < PER; ++k) o[k] = o[k] * wa + x[k] * wb;
-        m = mn;
+            for (int k = 0; k < PER; ++k) x[f][k] = 0.0f;
+            if (i < pieces)
+            {
+                const int64_t slot = i < a.pfx_chunks
+                                         ? static_cast<int64_t>(a.pfx_slot0) + static_cast<int64_t>(i) * a.batch + b
+                                         : static_cast<int64_t>(i_lo + i - a.pfx_chunks) + b;
+                ms[f] = a.ws_ml[(slot * a.num_heads + h) * 2];
+                ls[f] = a.ws_ml[(slot * a.num_heads + h) * 2 + 1];
+                const float* src = a.ws_acc + (slot * a.num_heads + h) * D + lane * PER;
+#pragma unroll
+                for (int k = 0; k < PER; ++k) x[f][k] = src[k];
+            }
+        }
+#pragma unroll
+        for (int f = 0; f < FOLD; ++f)
+        {
+            if (ms[f] == kNegInf) continue;  // segment without a valid page (or past the row's pieces)
+            const float mn = fmaxf(m, ms[f]);
+            const float wa = __builtin_amdgcn_exp2f(m - mn);
+            const float wb = __builtin_amdgcn_exp2f(ms[f] - mn);
+            l = l * wa + ls[f] * wb;
+#pragma unroll
+            for (int k = 0; k < PER; ++k) o[k] = o[k] * wa + x[f][k] * wb;
+            m = mn;
+        }
     }
     if (lane == 0)
     {
