@@ -627,8 +627,10 @@ void paged_decode_mfma(DecodeArgs a)
 // Combine the partials of rows split over several work items.
 // One workgroup of four waves per (row, head): wave w folds segments i_lo + w, i_lo + w + 4, ... into an online
 // (max, denominator, output) state (lane = D/64 dims), then the four states are combined through LDS.
-template <int QT, int D>
-__global__ __launch_bounds__(256) void paged_decode_mfma_merge(DecodeArgs a)
+// MW waves per (row, head): 4 for short piece lists, 16 when rows are few and long (C3-like) and each row has
+// tens of pieces.
+template <int QT, int D, int MW>
+__global__ __launch_bounds__(64 * MW) void paged_decode_mfma_merge(DecodeArgs a)
 {
     constexpr int PER = D / 64;  // dims per lane
     const int     b = blockIdx.x;
@@ -636,8 +638,8 @@ __global__ __launch_bounds__(256) void paged_decode_mfma_merge(DecodeArgs a)
     const int     lane = threadIdx.x & 63;
     const int     wave = threadIdx.x >> 6;
     const size_t  ob = (static_cast<size_t>(b) * a.num_heads + h) * D;
-    __shared__ float s_m[4], s_l[4];
-    __shared__ float s_o[4][D];
+    __shared__ float s_m[MW], s_l[MW];
+    __shared__ float s_o[MW][D];
 
     const int i_lo = a.ws_meta[2 * b];
     const int i_hi = a.ws_meta[2 * b + 1];
@@ -650,16 +652,16 @@ __global__ __launch_bounds__(256) void paged_decode_mfma_merge(DecodeArgs a)
     float     m = kNegInf, l = 0.0f, o[PER];
 #pragma unroll
     for (int k = 0; k < PER; ++k) o[k] = 0.0f;
-    // Wave w folds pieces w, w + 4, ...; the loads of FOLD pieces go out together before any is folded, so a
-    // row of up to 4 * FOLD pieces costs one round trip to memory instead of one per piece.
+    // Wave w folds pieces w, w + MW, ...; the loads of FOLD pieces go out together before any is folded, so a
+    // row of up to MW * FOLD pieces costs one round trip to memory instead of one per piece.
     constexpr int FOLD = 4;
-    for (int i0 = wave; i0 < pieces; i0 += 4 * FOLD)
+    for (int i0 = wave; i0 < pieces; i0 += MW * FOLD)
     {
         float ms[FOLD], ls[FOLD], x[FOLD][PER];
 #pragma unroll
         for (int f = 0; f < FOLD; ++f)
         {
-            const int i = i0 + 4 * f;
+            const int i = i0 + MW * f;
             ms[f] = kNegInf;
             ls[f] = 0.0f;
 #pragma unroll
@@ -700,12 +702,14 @@ __global__ __launch_bounds__(256) void paged_decode_mfma_merge(DecodeArgs a)
     if (threadIdx.x < D)
     {
         const int d = threadIdx.x;
-        float     M = fmaxf(fmaxf(s_m[0], s_m[1]), fmaxf(s_m[2], s_m[3]));
-        float     L = 0.0f, O = 0.0f;
+        float     M = kNegInf;
+#pragma unroll
+        for (int w = 0; w < MW; ++w) M = fmaxf(M, s_m[w]);
+        float L = 0.0f, O = 0.0f;
         if (M != kNegInf)
         {
 #pragma unroll
-            for (int w = 0; w < 4; ++w)
+            for (int w = 0; w < MW; ++w)
             {
                 const float wt = __builtin_amdgcn_exp2f(s_m[w] - M);
                 L += s_l[w] * wt;
@@ -730,8 +734,11 @@ hipError_t launch_m3(const DecodeArgs& a0, hipStream_t stream)
     hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(items), static_cast<unsigned>(gy)), dim3(64 * nw), 0, stream, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((paged_decode_mfma_merge<QT, D>),
-                       dim3(static_cast<unsigned>(a.batch), static_cast<unsigned>(a.num_heads)), dim3(256), 0, stream, a);
+    const dim3 mgrid(static_cast<unsigned>(a.batch), static_cast<unsigned>(a.num_heads));
+    if (a.batch <= 16)  // few rows over the same items: tens of pieces per row
+        hipLaunchKernelGGL((paged_decode_mfma_merge<QT, D, 16>), mgrid, dim3(1024), 0, stream, a);
+    else
+        hipLaunchKernelGGL((paged_decode_mfma_merge<QT, D, 4>), mgrid, dim3(256), 0, stream, a);
     return hipGetLastError();
 }
 
