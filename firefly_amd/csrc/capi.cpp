@@ -408,10 +408,8 @@ int decode_impl(const void* q, void* out, int qo_dtype, const void* k_cache, con
         return fail(FFKV_ERR_INVALID_ARGUMENT, "shared_blocks %d outside 0 .. max_blocks %d", shared_blocks,
                     max_blocks);
     const bool mfma = ffkv::decode_use_mfma(cache_dtype, group);
-    // shared-prefix split: matrix-core decode over 16-bit caches (otherwise the plain decode, same results)
-    const int skip = mfma && (cache_dtype == FFKV_DTYPE_BF16 || cache_dtype == FFKV_DTYPE_F16)
-                         ? std::min(shared_blocks, static_cast<int>(ceil_div(cap, FFKV_BLOCK_SIZE)))
-                         : 0;
+    // shared-prefix split: matrix-core decode (16- and 8-bit caches; fp32 caches take the plain decode, same results)
+    const int skip = mfma ? std::min(shared_blocks, static_cast<int>(ceil_div(cap, FFKV_BLOCK_SIZE))) : 0;
     int pfx_chunks = 0, pfx_chunk_pages = 0;
     if (skip > 0) ffkv::prefix_chunking(batch, group, num_kv_heads, skip, pfx_chunks, pfx_chunk_pages);
     const int  chunk = ffkv::decode_chunk(batch, num_kv_heads, cap);
@@ -492,6 +490,8 @@ int decode_impl(const void* q, void* out, int qo_dtype, const void* k_cache, con
         p.q = q;
         p.k_cache = k_cache;
         p.v_cache = v_cache;
+        p.k_scale = k_scale;
+        p.v_scale = v_scale;
         p.block_table = block_table;
         p.context_lens = context_lens;
         p.qo_dtype = qo_dtype;

@@ -34,6 +34,10 @@ namespace ffkv
 #ifndef FFKV_PREFILL_DMA
 #define FFKV_PREFILL_DMA 1  // 16-bit caches take paged_prefill_dma (global->LDS loads, transposed LDS reads)
 #endif
+
+#ifndef FFKV_PREFILL_DMA8
+#define FFKV_PREFILL_DMA8 1  // so do int8 / fp8 caches (codes converted at operand-read time)
+#endif
 constexpr int kPfWaves = FFKV_PREFILL_WAVES;
 constexpr int kPfThreads = 64 * kPfWaves;
 constexpr int kPfRows = 16 * kPfWaves;  // query rows per workgroup
@@ -446,7 +450,7 @@ hipError_t launch_pf_q(const PrefillArgs& a, hipStream_t stream)
 hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream)
 {
 #if FFKV_PREFILL_DMA
-    if (a.cache_dtype == F16 || a.cache_dtype == BF16) return launch_prefill_dma(a, stream);
+    if (a.cache_dtype == F16 || a.cache_dtype == BF16 || FFKV_PREFILL_DMA8) return launch_prefill_dma(a, stream);
 #endif
     switch (a.cache_dtype)
     {

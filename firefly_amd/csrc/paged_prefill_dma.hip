@@ -1,5 +1,5 @@
-// paged_prefill_dma.hip - chunked / paged prefill attention over 16-bit (f16 / bf16) caches on gfx950, with the
-// K/V pages streamed into LDS by asynchronous global->LDS loads.
+// paged_prefill_dma.hip - chunked / paged prefill attention on gfx950, with the K/V pages streamed into LDS by
+// asynchronous global->LDS loads (16-bit caches, and 8-bit int8 / fp8 e4m3 codes converted at operand-read time).
 //
 // Same contract and arithmetic as paged_prefill_mfma (paged_prefill.hip), which replaces the reference's prefill
 // branch of kernels::attention (flash_attn_wmma_kernel, src/kernels/attention.cu:22-286, dispatched at :460-474)
@@ -21,6 +21,13 @@
 // K reads (16 rows, one chunk) nor the transposed V reads (4 rows, two chunks per 16-lane group) collide in LDS
 // banks; the loads apply the same swizzle by choosing which chunk each lane fetches.
 //
+// 8-bit caches load their codes the same way (half the bytes per page) and convert them when an operand is read:
+// the K operand is an 8-byte read of 8 codes, the V^T operand one ds_read_b64_tr_b8 (within each 16-lane group,
+// lanes 2r and 2r + 1 supply the two halves of key row r's 16 dims, and lane j receives dim j of rows 0..7,
+// which are the 8 keys of one k-slot group), both turned into 8 MFMA-type values by the gfx950 conversions.
+// int8 per-token scales (fp32 [N, 16, Hkv]) travel with their page into the stage by 4-byte loads; fp8 per-head
+// scales fold into the score scale and the output.
+//
 // Keys past the row's end and keys on invalid pages are fetched from a zero block instead, so masked keys meet
 // zero V rows (their probabilities are exactly zero) and no lane reads outside the cache.
 #include "mfma_common.h"
@@ -41,26 +48,34 @@ constexpr int kXcds = 8;  // MI355X: workgroups are dealt to 8 XCDs (separate L2
 #define FFKV_PREFILL_XCD 1
 #endif
 
+#ifndef FFKV_PREFILL_I8_BF
+#define FFKV_PREFILL_I8_BF 0  // int8 with bf16 q: f16 MFMAs with q split (measured faster than bf16 MFMAs with P split)
+#endif
+
 #ifndef FFKV_PREFILL_DMA_KP128
 #define FFKV_PREFILL_DMA_KP128 2  // pages per step at head_dim 128
 #endif
 
 #define FFKV_LDS __attribute__((address_space(3)))
+
+using i32x2 = int __attribute__((ext_vector_type(2)));
 #define FFKV_CONST __attribute__((address_space(4)))  // read-only for the kernel's lifetime: scalar loads
 
 // Source of the chunks of keys that are not loaded: 64 lanes x 16 bytes of zeros (never written).
 __device__ __align__(16) uint32_t g_zero_chunks[256];
 
-template <int D>
+template <int D, int EB, bool SC>  // EB: bytes per cached element (2, or 1 for int8 / fp8 codes); SC: int8 scales
 struct DmaCfg
 {
     static constexpr int KP = D == 64 ? 4 : (D == 128 ? FFKV_PREFILL_DMA_KP128 : 2);  // pages per step
-    static constexpr int CPT = D / 8;                                                  // chunks per key row
-    static constexpr int CHUNKS = kBlockSize * CPT;                                    // chunks per page
-    static constexpr int TILE = KP * kBlockSize * D;          // elements of a step's K (or V) tile
-    static constexpr int IPR = KP * CHUNKS / 64;              // load instructions per tile
-    static constexpr int IPW = IPR / kDmaWaves;               // K (and V) load instructions per wave and step
-    static_assert(IPW >= 1 && IPR % kDmaWaves == 0, "every wave loads whole 64-chunk runs of K and of V");
+    static constexpr int RB = D * EB;                  // bytes of one key row (one kv head)
+    static constexpr int CPT = RB / 16;                // 16-byte chunks per key row
+    static constexpr int CHUNKS = kBlockSize * CPT;    // chunks per page
+    static constexpr int TILEB = KP * kBlockSize * RB; // bytes of a step's K (or V) tile
+    static constexpr int SCB = SC ? 2 * KP * kBlockSize * 4 : 0;  // int8 scales of the step: K then V
+    static constexpr int IPR = KP * CHUNKS / 64;       // 64-chunk load runs per tile
+    static constexpr int RPW = 2 * IPR / kDmaWaves;    // runs per wave and step (K runs first, then V)
+    static_assert(RPW >= 1 && (2 * IPR) % kDmaWaves == 0, "every wave loads whole 64-chunk runs");
     static_assert(CHUNKS % 64 == 0, "a 64-chunk run stays inside one page");
 };
 
@@ -76,6 +91,21 @@ __device__ __forceinline__ int v_swizzle(int t)
 __device__ __forceinline__ int k_swizzle(int t)
 {
     return (t & 7) ^ ((t >> 3) << 1);
+}
+
+// 8-bit K rows (D bytes): the 16 rows of one 8-byte operand read (same chunk) on distinct banks.
+template <int D>
+__device__ __forceinline__ int k8_swizzle(int t)
+{
+    return D == 64 ? (t >> 2) & 3 : (D == 128 ? (t >> 1) & 7 : t & 15);
+}
+
+// 8-bit V rows: one transposed read takes chunk n of rows 4g .. 4g + 3 of two pages u0, u0 + 1 (u = page within
+// the step); their chunk positions sit on distinct banks.
+template <int D>
+__device__ __forceinline__ int v8_swizzle(int t, int u)
+{
+    return D == 64 ? (u & 1) : (D == 128 ? (((t >> 1) & 3) | ((u & 1) << 2)) : ((t & 3) | ((u & 1) << 2)));
 }
 
 // One 16-byte global -> LDS load per lane: lane l's 16 bytes from `src` land at LDS address `dst` + 16 * l (dst
@@ -110,6 +140,18 @@ __device__ __forceinline__ void load_lds16(const void* base, uint32_t offset, co
 #pragma clang diagnostic pop
 }
 
+// One 4-byte global -> LDS load per lane (lane l's word lands at `dst` + 4 * l).
+__device__ __forceinline__ void load_lds4(const void* src, const FFKV_LDS void* dst)
+{
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off"
+                 :
+                 : "v"(src), "s"(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(dst)))
+                 : "memory", "m0");
+#pragma clang diagnostic pop
+}
+
 template <int VM>
 __device__ __forceinline__ void wait_vm()
 {
@@ -123,11 +165,15 @@ __device__ __forceinline__ void wait_vm()
 // pages shared by every row (pages 0 .. pfx_blocks - 1 of row 0's block table, which all rows hold): one query
 // per (row, head), attending keys 0 .. min(ctx + 1, prefix) - 1, written as (max, denominator, unnormalised
 // output) to the decode workspace for the decode merge to fold in.
-template <int QT, int D, bool BF, bool PFX>
+template <int QT, int D, int CT, bool PFX>
 __global__ __launch_bounds__(kDmaThreads) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 4 : 1)))
 void paged_prefill_dma(PrefillArgs a)
 {
-    using C = DmaCfg<D>;
+    constexpr int  EB = kElemBytes<CT>;
+    constexpr bool Q8 = EB == 1;
+    // int8 codes take bf16 MFMAs beside a bf16 q (exact: 8 significant bits), so q needs no hi / lo split
+    constexpr bool BF = CT == I8 ? (FFKV_PREFILL_I8_BF && QT != F16) : kBF<CT, QT>;
+    using C = DmaCfg<D, EB, CT == I8>;  // the scale bytes (and their loads, counted in the waits) only for int8
     using M = MType<BF>;
     using X8 = typename M::x8;
     constexpr int  KP = C::KP;
@@ -135,10 +181,10 @@ void paged_prefill_dma(PrefillArgs a)
     constexpr int  NT = D / 16;
     constexpr bool NEED_LO = !((QT == BF16 && BF) || (QT == F16 && !BF));
 
-    // three stages, each [K tile | V tile] of KP pages, key-major with swizzled chunks
-    __shared__ __align__(16) uint16_t s_st0[2 * C::TILE];
-    __shared__ __align__(16) uint16_t s_st1[2 * C::TILE];
-    __shared__ __align__(16) uint16_t s_st2[2 * C::TILE];
+    // three stages, each [K tile | V tile | int8 scales] of KP pages, key-major with swizzled chunks
+    __shared__ __align__(16) uint8_t s_st0[2 * C::TILEB + C::SCB];
+    __shared__ __align__(16) uint8_t s_st1[2 * C::TILEB + C::SCB];
+    __shared__ __align__(16) uint8_t s_st2[2 * C::TILEB + C::SCB];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -259,37 +305,47 @@ void paged_prefill_dma(PrefillArgs a)
     // ---- loads: wave w fetches runs w*IPW .. w*IPW + IPW - 1 (64 chunks each) of the K tile and of the V tile --
     const FFKV_CONST int32_t* table_row =  // prefix: row 0's table, whose first pfx_blocks entries every row shares
         a.paged ? (const FFKV_CONST int32_t*)(a.block_table + static_cast<int64_t>(b) * a.max_blocks) : nullptr;
-    const uint16_t* zero_src = reinterpret_cast<const uint16_t*>(g_zero_chunks) + 8 * lane;
-    // Per-lane part of each load's source, the same for every page: key row `tok` of the page, chunk `ch`
-    // (swizzled to where this lane's 16 bytes land), as a byte offset from the page's (row, kv head) base.
-    uint32_t voff[2 * C::IPW];
-    int      vtok[2 * C::IPW];
+    const char* zero_src = reinterpret_cast<const char*>(g_zero_chunks) + 16 * lane;
+    // Wave w loads runs w*RPW .. w*RPW + RPW - 1 of the step (runs 0 .. IPR - 1 are K, the rest V).  Per-lane part
+    // of each load's source, the same for every page: key row `tok` of the page, chunk `ch` (swizzled to where
+    // this lane's 16 bytes land), as a byte offset from the page's (row, kv head) base.
+    uint32_t voff[C::RPW];
+    int      vtok[C::RPW];
 #pragma unroll
-    for (int k = 0; k < 2 * C::IPW; ++k)
+    for (int k = 0; k < C::RPW; ++k)
     {
-        const bool is_v = k >= C::IPW;
-        const int  run = wave * C::IPW + (is_v ? k - C::IPW : k);  // 64-chunk run within the tile
-        const int  p = run * 64 % C::CHUNKS + lane;                  // chunk position within the page
+        const int  run = wave * C::RPW + k;
+        const bool is_v = run >= C::IPR;                  // uniform
+        const int  lr = is_v ? run - C::IPR : run;          // run within its tile
+        const int  u = lr * 64 / C::CHUNKS;                 // page of the step
+        const int  p = lr * 64 % C::CHUNKS + lane;          // chunk position within the page
         const int  tok = p / C::CPT;
-        const int  ch = (p % C::CPT) ^ (is_v ? v_swizzle<D>(tok) : k_swizzle(tok));
+        int        sw;
+        if constexpr (Q8)
+            sw = is_v ? v8_swizzle<D>(tok, u) : k8_swizzle<D>(tok);
+        else
+            sw = is_v ? v_swizzle<D>(tok) : k_swizzle(tok);
+        const int ch = (p % C::CPT) ^ sw;
         vtok[k] = tok;
-        voff[k] = static_cast<uint32_t>((tok * Hkv * D + 8 * ch) * 2);
+        voff[k] = static_cast<uint32_t>(tok * Hkv * C::RB + 16 * ch);
     }
-    const size_t row_bytes = static_cast<size_t>(Hkv) * D * 2;  // one key row of all kv heads
+    const size_t row_bytes = static_cast<size_t>(Hkv) * C::RB;  // one key row of all kv heads
 
     // Requests step si into `stage`; returns its page mask (bit u: page pg_lo + si*KP + u is present; keys on absent
     // pages are masked).  Block-table entries are uniform and come through the scalar cache.  Pages whose 16
     // rows are all keys of the row load with a uniform base; the row's last, partial page (and absent pages)
     // fetch the zero block for the missing rows.
-    auto issue = [&](int si, uint16_t* stage) -> int
+    auto issue = [&](int si, uint8_t* stage) -> int
     {
         int    okm = 0, full = 0;
         size_t page_off[KP];  // byte offset of (page row 0, kv head kvh) in the caches
+        int    page_row[KP];  // paged: physical page (present pages); int8 scales are indexed by it
 #pragma unroll
         for (int u = 0; u < KP; ++u)
         {
             const int pg = pg_lo + si * KP + u;
             page_off[u] = 0;
+            page_row[u] = 0;
             if (pg < pg_hi)  // pg_hi <= max_blocks
             {
                 bool present = true;
@@ -298,13 +354,14 @@ void paged_prefill_dma(PrefillArgs a)
                 {
                     const int phys = table_row[pg];
                     present = phys >= 0 && phys < a.num_blocks;
+                    page_row[u] = present ? phys : 0;
                     r0 = static_cast<size_t>(present ? phys : 0) * kBlockSize;
                 }
                 else
                 {
                     r0 = static_cast<size_t>(b) * S + static_cast<size_t>(pg) * kBlockSize;
                 }
-                page_off[u] = r0 * row_bytes + static_cast<size_t>(kvh) * D * 2;
+                page_off[u] = r0 * row_bytes + static_cast<size_t>(kvh) * C::RB;
                 if (present)
                 {
                     okm |= 1 << u;
@@ -313,16 +370,17 @@ void paged_prefill_dma(PrefillArgs a)
             }
         }
 #pragma unroll
-        for (int k = 0; k < 2 * C::IPW; ++k)
+        for (int k = 0; k < C::RPW; ++k)
         {
-            const bool  is_v = k >= C::IPW;
-            const int   run = wave * C::IPW + (is_v ? k - C::IPW : k);
-            const int   u = run * 64 / C::CHUNKS;  // page of the step (uniform)
+            const int   run = wave * C::RPW + k;
+            const bool  is_v = run >= C::IPR;  // uniform
+            const int   lr = is_v ? run - C::IPR : run;
+            const int   u = lr * 64 / C::CHUNKS;  // page of the step (uniform)
             size_t      poff = page_off[0];  // page_off[u] without a dynamic index (u is uniform but not constant)
 #pragma unroll
             for (int uu = 1; uu < KP; ++uu) poff = u == uu ? page_off[uu] : poff;
             const char* base = static_cast<const char*>(is_v ? a.v_cache : a.k_cache) + poff;
-            const FFKV_LDS void* dst = (const FFKV_LDS void*)(stage + (is_v ? C::TILE : 0) + run * 64 * 8);
+            const FFKV_LDS void* dst = (const FFKV_LDS void*)(stage + (is_v ? C::TILEB : 0) + lr * 64 * 16);
             if ((full >> u) & 1)
             {
                 load_lds16(base, voff[k], dst);
@@ -333,6 +391,27 @@ void paged_prefill_dma(PrefillArgs a)
                 load_lds16(take ? static_cast<const void*>(base + voff[k]) : static_cast<const void*>(zero_src), dst);
             }
         }
+        if constexpr (CT == I8)
+        {
+            // the step's per-token scales, K then V: lane l of run s takes scale l + 64 s (every wave issues the same
+            // loads, so every wave's wait counts match; the copies write the same values)
+#pragma unroll
+            for (int sr = 0; sr < C::SCB / 256; ++sr)
+            {
+                const int  e = lane + 64 * sr;
+                const bool is_v = e >= KP * kBlockSize;
+                const int  u = (e / kBlockSize) % KP;
+                const int  t = e % kBlockSize;
+                int        pr = page_row[0];
+#pragma unroll
+                for (int uu = 1; uu < KP; ++uu) pr = u == uu ? page_row[uu] : pr;
+                const bool take = ((okm >> u) & 1) && (pg_lo + si * KP + u) * kBlockSize + t < L;
+                const float* src = (is_v ? a.v_scale : a.k_scale) +
+                                   (static_cast<size_t>(pr) * kBlockSize + t) * Hkv + kvh;
+                load_lds4(take ? static_cast<const void*>(src) : static_cast<const void*>(zero_src),
+                          (const FFKV_LDS void*)(stage + 2 * C::TILEB + 256 * sr));
+            }
+        }
         return okm;
     };
 
@@ -341,7 +420,13 @@ void paged_prefill_dma(PrefillArgs a)
     // with c = scale * log2(e).  The reference moves (and acc / l_run are rescaled) only when a new maximum
     // exceeds it by more than 8 / c, so p stays below 2^8 and most steps rescale nothing; numerator and
     // denominator share the reference, so the result is the same softmax.
-    const float c_log2 = a.scale_log2;
+    float c_log2 = a.scale_log2;
+    float v_head_scale = 1.0f;
+    if constexpr (CT == FP8)  // per-head scales: K's into the score scale, V's onto the output
+    {
+        c_log2 *= a.k_scale[kvh];
+        v_head_scale = a.v_scale[kvh];
+    }
     const float thr_raw = 8.0f / c_log2;
     float       m_run = kNegInf;
     float       l_run = 0.0f;
@@ -355,18 +440,26 @@ void paged_prefill_dma(PrefillArgs a)
     for (int off = 1; off < 16; off <<= 1) kmin = min(kmin, __shfl_xor(kmin, off, 64));
     kmin = __builtin_amdgcn_readfirstlane(kmin);
 
-    // K operand of k-step j: key c, dims 32j + 8g .. +8 at lds_pos<D>(c, 32j + 8g) = c*D + 8*(g ^ s01) + 32*(j ^ s2)
-    // with the row swizzle sw = 4*s2 + s01: an even and an odd base plus the constant 32j.
+    // 16-bit K operand of k-step j: key c, dims 32j + 8g .. +8 at element lds_pos<D>(c, 32j + 8g) =
+    // c*D + 8*(g ^ s01) + 32*(j ^ s2) with the row swizzle sw = 4*s2 + s01: an even and an odd base plus 32j.
     const int ksw = k_swizzle(c);
-    const int kb_even = c * D + 8 * (g ^ (ksw & 3)) + 32 * (ksw >> 2);
-    const int kb_odd = c * D + 8 * (g ^ (ksw & 3)) - 32 * (ksw >> 2);
-    // V^T operand via transposed reads: this lane supplies dims 16n + 4q .. +3 of key row 4g + rr of a page
+    const int kb_even = 2 * (c * D + 8 * (g ^ (ksw & 3)) + 32 * (ksw >> 2));  // bytes
+    const int kb_odd = 2 * (c * D + 8 * (g ^ (ksw & 3)) - 32 * (ksw >> 2));
+    // 16-bit V^T operand via transposed reads: this lane supplies dims 16n + 4q .. +3 of key row 4g + rr of a page
     const int vrow = 4 * g + (c >> 2);
-    const int vq = c & 3;
     const int vsw = v_swizzle<D>(vrow) >> 1;
-    const int vbase = C::TILE + vrow * D + 4 * vq;
+    const int vbase = C::TILEB + 2 * (vrow * D + 4 * (c & 3));  // bytes
+    // 8-bit K operand: 8 codes of key c at dims 32j + 8g: chunk 2j + g/2 (swizzled), half g & 1
+    const int k8sw = k8_swizzle<D>(c);
+    const int k8base = c * C::RB + 8 * (g & 1);
+    // 8-bit V^T operand: lanes 2r, 2r + 1 supply the halves of chunk n of row r; rows 0..3 are keys 4g .. 4g + 3 of
+    // page u0, rows 4..7 the same keys of page u0 + 1 (k-slots 8g + r)
+    const int v8key = 4 * g + ((c >> 1) & 3);
+    const int v8pg = (c >> 1) >> 2;  // 0: page u0, 1: page u0 + 1
+    const int v8sw = v8_swizzle<D>(v8key, v8pg);
+    const int v8base = C::TILEB + v8pg * kBlockSize * C::RB + v8key * C::RB + 8 * (c & 1);
 
-    auto compute = [&](int si, const uint16_t* stage, int okm)
+    auto compute = [&](int si, const uint8_t* stage, int okm)
     {
         const int pg0 = pg_lo + si * KP;
         f32x4     s[KP];
@@ -374,8 +467,17 @@ void paged_prefill_dma(PrefillArgs a)
         for (int u = 0; u < KP; ++u) s[u] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
         auto kread = [&](int j, int u) -> X8
         {
-            const int ka = ((j & 1) ? kb_odd : kb_even) + 32 * j;
-            return __builtin_bit_cast(X8, *reinterpret_cast<const u32x4*>(stage + u * kBlockSize * D + ka));
+            if constexpr (Q8)
+            {
+                const int   ka = u * kBlockSize * C::RB + k8base + (((2 * j + (g >> 1)) ^ k8sw) << 4);
+                const u32x2 w = *reinterpret_cast<const u32x2*>(stage + ka);
+                return __builtin_bit_cast(X8, codes_to_m<CT, BF>(w[0], w[1]));
+            }
+            else
+            {
+                const int ka = ((j & 1) ? kb_odd : kb_even) + 64 * j;
+                return __builtin_bit_cast(X8, *reinterpret_cast<const u32x4*>(stage + u * kBlockSize * C::RB + ka));
+            }
         };
         X8 kc[KP];
 #pragma unroll
@@ -394,6 +496,12 @@ void paged_prefill_dma(PrefillArgs a)
             }
 #pragma unroll
             for (int u = 0; u < KP; ++u) kc[u] = kn[u];
+        }
+        if constexpr (CT == I8)  // per-token K scales of keys 4g .. 4g + 3 of each page
+        {
+#pragma unroll
+            for (int u = 0; u < KP; ++u)
+                s[u] *= *reinterpret_cast<const f32x4*>(stage + 2 * C::TILEB + (u * kBlockSize + 4 * g) * 4);
         }
         float sc[KP * 4];
         float mt = kNegInf;
@@ -439,16 +547,38 @@ void paged_prefill_dma(PrefillArgs a)
             pv[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[e], c_log2, mneg));
             l_run += pv[e];
         }
+        if constexpr (CT == I8)  // per-token V scales multiply P (the denominator keeps the unscaled p)
+        {
+#pragma unroll
+            for (int u = 0; u < KP; ++u)
+            {
+                const f32x4 vsc = *reinterpret_cast<const f32x4*>(
+                    stage + 2 * C::TILEB + ((KP + u) * kBlockSize + 4 * g) * 4);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) pv[4 * u + i] *= vsc[i];
+            }
+        }
 
         auto vread = [&](int n, int u0) -> X8  // V^T operand of output tile n over pages u0, u0 + 1
         {
-            const int  off = vbase + 16 * (n ^ vsw);
-            const auto a0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((FFKV_LDS bf16x4*)(stage + u0 * kBlockSize * D + off));
-            const auto a1 =
-                __builtin_amdgcn_ds_read_tr16_b64_v4bf16((FFKV_LDS bf16x4*)(stage + (u0 + 1) * kBlockSize * D + off));
-            const u32x2 w0 = __builtin_bit_cast(u32x2, a0);
-            const u32x2 w1 = __builtin_bit_cast(u32x2, a1);
-            return __builtin_bit_cast(X8, u32x4{w0[0], w0[1], w1[0], w1[1]});
+            if constexpr (Q8)
+            {
+                const auto raw = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+                    (FFKV_LDS i32x2*)(stage + u0 * kBlockSize * C::RB + v8base + ((n ^ v8sw) << 4)));
+                const u32x2 w = __builtin_bit_cast(u32x2, raw);
+                return __builtin_bit_cast(X8, codes_to_m<CT, BF>(w[0], w[1]));
+            }
+            else
+            {
+                const int  off = vbase + 32 * (n ^ vsw);
+                const auto a0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+                    (FFKV_LDS bf16x4*)(stage + u0 * kBlockSize * C::RB + off));
+                const auto a1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+                    (FFKV_LDS bf16x4*)(stage + (u0 + 1) * kBlockSize * C::RB + off));
+                const u32x2 w0 = __builtin_bit_cast(u32x2, a0);
+                const u32x2 w1 = __builtin_bit_cast(u32x2, a1);
+                return __builtin_bit_cast(X8, u32x4{w0[0], w0[1], w1[0], w1[1]});
+            }
         };
 #pragma unroll
         for (int u0 = 0; u0 < KP; u0 += 2)
@@ -490,10 +620,11 @@ void paged_prefill_dma(PrefillArgs a)
 
     // ---- pipeline: stage si % 3 ----------------------------------------------------------------------------
     // Every step issues the same number of loads (steps past the end fetch the zero block into a stage nobody
-    // reads), so "step si has landed" is always vmcnt <= the 2 * IPW loads of step si + 1.
-    auto body = [&](int si, uint16_t* cur, int okm_cur, uint16_t* nxt, int& okm_nxt)
+    // reads), so "step si has landed" is always vmcnt <= the loads of step si + 1.
+    constexpr int LPS = C::RPW + C::SCB / 256;  // loads per wave and step
+    auto body = [&](int si, uint8_t* cur, int okm_cur, uint8_t* nxt, int& okm_nxt)
     {
-        wait_vm<2 * C::IPW>();
+        wait_vm<LPS>();
         __builtin_amdgcn_s_barrier();  // step si visible to all; every wave is past step si - 1 (stage of si + 2)
         okm_nxt = issue(si + 2, nxt);
         if (wave_active) compute(si, cur, okm_cur);
@@ -521,7 +652,7 @@ void paged_prefill_dma(PrefillArgs a)
             const int64_t slot = static_cast<int64_t>(a.pfx_slot0) + static_cast<int64_t>(chunk) * a.batch + bq;
             float*        dst = a.ws_acc + (slot * Hq + h) * D;
 #pragma unroll
-            for (int n = 0; n < NT; ++n) *reinterpret_cast<f32x4*>(dst + 16 * n + 4 * g) = acc[n];
+            for (int n = 0; n < NT; ++n) *reinterpret_cast<f32x4*>(dst + 16 * n + 4 * g) = acc[n] * v_head_scale;
             if (g == 0)
             {
                 a.ws_ml[(slot * Hq + h) * 2] = m_run == kNegInf ? kNegInf : m_run * c_log2;
@@ -531,7 +662,7 @@ void paged_prefill_dma(PrefillArgs a)
     }
     else if (col_ok)
     {
-        const float  inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+        const float  inv = l_tot > 0.0f ? v_head_scale / l_tot : 0.0f;
         const size_t ob = qrow * D;
 #pragma unroll
         for (int n = 0; n < NT; ++n) store_out4<QT>(a.out, ob + 16 * n + 4 * g, acc[n] * inv);
@@ -544,15 +675,14 @@ namespace
 template <int CT, int QT, bool PFX>
 hipError_t launch_pfd_d(const PrefillArgs& a, hipStream_t stream)
 {
-    constexpr bool BF = CT == BF16;
-    const int64_t  rows = PFX ? static_cast<int64_t>(a.batch) * a.group : static_cast<int64_t>(a.seq_len) * a.group;
-    const int64_t  groups = PFX ? static_cast<int64_t>(a.num_kv_heads) * a.pfx_chunks
-                                : static_cast<int64_t>(a.batch) * a.num_kv_heads;
-    const int64_t  nrb = (rows + kDmaRows - 1) / kDmaRows;
+    const int64_t rows = PFX ? static_cast<int64_t>(a.batch) * a.group : static_cast<int64_t>(a.seq_len) * a.group;
+    const int64_t groups = PFX ? static_cast<int64_t>(a.num_kv_heads) * a.pfx_chunks
+                               : static_cast<int64_t>(a.batch) * a.num_kv_heads;
+    const int64_t nrb = (rows + kDmaRows - 1) / kDmaRows;
 #if FFKV_PREFILL_XCD
-    const int64_t  wgs = (groups + kXcds - 1) / kXcds * kXcds * nrb;
+    const int64_t wgs = (groups + kXcds - 1) / kXcds * kXcds * nrb;
 #else
-    const int64_t  wgs = groups * nrb;
+    const int64_t wgs = groups * nrb;
 #endif
     if (wgs <= 0) return hipSuccess;
     if (wgs > INT32_MAX) return hipErrorInvalidConfiguration;
@@ -560,13 +690,13 @@ hipError_t launch_pfd_d(const PrefillArgs& a, hipStream_t stream)
     switch (a.head_dim)
     {
         case 64:
-            hipLaunchKernelGGL((paged_prefill_dma<QT, 64, BF, PFX>), grid, dim3(kDmaThreads), 0, stream, a);
+            hipLaunchKernelGGL((paged_prefill_dma<QT, 64, CT, PFX>), grid, dim3(kDmaThreads), 0, stream, a);
             break;
         case 128:
-            hipLaunchKernelGGL((paged_prefill_dma<QT, 128, BF, PFX>), grid, dim3(kDmaThreads), 0, stream, a);
+            hipLaunchKernelGGL((paged_prefill_dma<QT, 128, CT, PFX>), grid, dim3(kDmaThreads), 0, stream, a);
             break;
         default:
-            hipLaunchKernelGGL((paged_prefill_dma<QT, 256, BF, PFX>), grid, dim3(kDmaThreads), 0, stream, a);
+            hipLaunchKernelGGL((paged_prefill_dma<QT, 256, CT, PFX>), grid, dim3(kDmaThreads), 0, stream, a);
             break;
     }
     return hipGetLastError();
@@ -586,16 +716,29 @@ hipError_t launch_pfd_q(const PrefillArgs& a, hipStream_t stream)
     }
 }
 
+template <bool PFX>
+hipError_t launch_pfd(const PrefillArgs& a, hipStream_t stream)
+{
+    // 8-bit caches read their scales in every workgroup (int8 per token, fp8 per head)
+    if ((a.cache_dtype == I8 || a.cache_dtype == FP8) && (a.k_scale == nullptr || a.v_scale == nullptr))
+        return hipErrorInvalidValue;
+    switch (a.cache_dtype)
+    {
+        case F16:
+            return launch_pfd_q<F16, PFX>(a, stream);
+        case BF16:
+            return launch_pfd_q<BF16, PFX>(a, stream);
+        case I8:
+            return launch_pfd_q<I8, PFX>(a, stream);
+        default:
+            return launch_pfd_q<FP8, PFX>(a, stream);
+    }
+}
+
 }  // namespace
 
-hipError_t launch_prefill_dma(const PrefillArgs& a, hipStream_t stream)
-{
-    return a.cache_dtype == F16 ? launch_pfd_q<F16, false>(a, stream) : launch_pfd_q<BF16, false>(a, stream);
-}
+hipError_t launch_prefill_dma(const PrefillArgs& a, hipStream_t stream) { return launch_pfd<false>(a, stream); }
 
-hipError_t launch_prefix_partials(const PrefillArgs& a, hipStream_t stream)
-{
-    return a.cache_dtype == F16 ? launch_pfd_q<F16, true>(a, stream) : launch_pfd_q<BF16, true>(a, stream);
-}
+hipError_t launch_prefix_partials(const PrefillArgs& a, hipStream_t stream) { return launch_pfd<true>(a, stream); }
 
 }  // namespace ffkv

@@ -133,7 +133,7 @@ FFKV_API int ffkv_append_paged_decode(const void* k_new, const void* v_new, int 
  * prefix page, split into chunks of pages), the rest of each row by the decode kernel, and the split-K merge
  * folds both: each shared page is read once per call instead of once per row.  Results equal ffkv_paged_decode
  * on the same inputs up to floating-point summation order (same tolerance).  Rows shorter than the prefix
- * attend only their own tokens.  The split applies to F16/BF16 caches with group <= 16; other calls run
+ * attend only their own tokens.  The split applies to F16/BF16/I8/FP8 caches with group <= 16; fp32 caches run
  * ffkv_paged_decode unchanged.  No counterpart in the reference, whose decode reads shared blocks once per row
  * (src/kernels/attention.cu:332-335).  Workspace: ffkv_decode_shared_prefix_workspace_bytes, or NULL as for
  * ffkv_paged_decode.

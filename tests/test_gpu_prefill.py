@@ -98,6 +98,20 @@ def test_prefill_head_shapes(ff, gpu, D, G):
     _check(*_run(ff, gpu, c, qn), c.act, 2e-3)
 
 
+@pytest.mark.parametrize("kv", ["i8", "fp8"])
+@pytest.mark.parametrize("D,G", [(64, 4), (128, 7), (256, 2)])
+def test_prefill_quantized_head_shapes(ff, gpu, kv, D, G):
+    c, qn = _case(320 + D + G, 3, 2 * G, 2, D, [5, 90, 200], 40, kv=kv)
+    _check(*_run(ff, gpu, c, qn), c.act, 2e-2)
+
+
+@pytest.mark.parametrize("kv", ["i8", "fp8"])
+def test_prefill_quantized_long_chunk(ff, gpu, kv):
+    """A 512-token chunk over a 1500-token prefix on an 8-bit cache (many steps, partial last pages)."""
+    c, qn = _case(410, 2, 32, 8, 128, [1500, 64], 512, kv=kv)
+    _check(*_run(ff, gpu, c, qn), c.act, 2e-2)
+
+
 def test_prefill_long_chunk_over_long_prefix(ff, gpu):
     """A 512-token chunk after a 1500-token prefix (many workgroups per row, the causal limit varying)."""
     c, qn = _case(400, 2, 32, 8, 128, [1500, 64], 512)

@@ -4,8 +4,8 @@ max-abs 2e-3 (16-bit KV) or 2e-2 (quantized KV) of the fp32 checker, beyond the 
 shared pages are attended once for all rows by a separate matrix-product kernel and merged with each row's own
 pages, so these cases cover the split itself: prefixes of 1 .. 128 pages, rows shorter than the prefix, rows
 ending exactly at its end, truncation by max_context_len, holes in the prefix, every head_dim and group size, and
-a workspace full of garbage reused across calls.  Cases whose cache type the split does not serve (int8, fp8)
-run the plain decode and must agree as well."""
+a workspace full of garbage reused across calls, and 8-bit caches (int8 per-token scales travel with the
+prefix pages, fp8 per-head scales fold into the score scale and the output)."""
 
 import numpy as np
 import pytest
@@ -97,7 +97,7 @@ def test_head_shapes(ff, gpu, D, G):
 
 
 @pytest.mark.parametrize("act,kv,tol", [("f16", "f16", 2e-3), ("f32", "bf16", 2e-3), ("bf16", "i8", 2e-2),
-                                        ("bf16", "fp8", 2e-2)])
+                                        ("bf16", "fp8", 2e-2), ("f16", "i8", 2e-2), ("f32", "fp8", 2e-2)])
 def test_dtypes(ff, gpu, act, kv, tol):
     rng = np.random.default_rng(47)
     ctx = 256 + rng.integers(0, 400, size=12)
@@ -114,15 +114,17 @@ def test_truncated_context(ff, gpu):
     _both(ff, gpu, c, 20, max_context_len=200)
 
 
-def test_hole_in_the_prefix(ff, gpu):
-    """An invalid entry inside the shared prefix (every row holds it) is skipped like in the plain decode."""
+@pytest.mark.parametrize("kv,tol", [("bf16", 2e-3), ("i8", 2e-2), ("fp8", 2e-2)])
+def test_hole_in_the_prefix(ff, gpu, kv, tol):
+    """An invalid entry inside the shared prefix (every row holds it) is skipped like in the plain decode (for
+    int8 its per-token scales are not read either)."""
     rng = np.random.default_rng(49)
     ctx = 200 + rng.integers(0, 300, size=8)
-    c = cases.make_case(49, 8, 16, 4, 128, ctx, act="bf16", shared_prefix_blocks=12)
+    c = cases.make_case(49, 8, 16, 4, 128, ctx, act="bf16", kv=kv, shared_prefix_blocks=12)
     tbl = c.block_table.copy()
     tbl[:, 3] = -1
     tbl[:, 7] = c.num_blocks + 3
-    _both(ff, gpu, c, 12, table=tbl)
+    _both(ff, gpu, c, 12, tol=tol, table=tbl)
 
 
 def test_zero_shared_blocks_is_the_plain_decode(ff, gpu):
