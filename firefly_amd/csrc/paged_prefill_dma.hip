@@ -14,6 +14,11 @@
 // main loop is unrolled by three, so the compiler can tell which stage a load writes and does not hold the
 // compute of one stage behind the loads into another.
 //
+// At head_dim <= 128 a workgroup is four waves of 32 query rows (two row groups of 16 MFMA columns): every K and
+// V^T operand read from LDS feeds two matrix products, which halves the LDS reads and the per-step scalar work per
+// query row.  Within a step the scores' products go out first; the scalar address work of the next step's loads
+// (block-table reads, page offsets) then runs while they execute instead of ahead of them.
+//
 // Both tiles stay row-major (key-major).  The K operand of S^T = K Q^T reads 8 consecutive dims of one key as
 // before; the V^T operand of O^T += V^T P^T needs 8 consecutive keys of one dim, which ds_read_b64_tr_b16 gives
 // directly: within each 16-lane group, lane 4r + q supplies the address of dims 4q .. 4q + 3 of key row r, and
@@ -38,10 +43,12 @@ namespace ffkv
 namespace
 {
 
-constexpr int kDmaWaves = 8;
-constexpr int kDmaThreads = 64 * kDmaWaves;
-constexpr int kDmaRows = 16 * kDmaWaves;  // query rows per workgroup
-constexpr int kDmaStages = 3;
+constexpr int kDmaRows = 128;  // query rows per workgroup: 8 waves x 16 rows (RG = 1) or 4 waves x 32 rows (RG = 2)
+#ifndef FFKV_PREFILL_STAGES
+#define FFKV_PREFILL_STAGES 3  // LDS stages of the load pipeline: steps in flight behind the computed one, + 1
+#endif
+constexpr int kDmaStages = FFKV_PREFILL_STAGES;
+static_assert(kDmaStages == 3 || kDmaStages == 4, "three or four stages");
 constexpr int kXcds = 8;  // MI355X: workgroups are dealt to 8 XCDs (separate L2s) in turn
 
 #ifndef FFKV_PREFILL_XCD
@@ -50,6 +57,10 @@ constexpr int kXcds = 8;  // MI355X: workgroups are dealt to 8 XCDs (separate L2
 
 #ifndef FFKV_PREFILL_I8_BF
 #define FFKV_PREFILL_I8_BF 0  // int8 with bf16 q: f16 MFMAs with q split (measured faster than bf16 MFMAs with P split)
+#endif
+
+#ifndef FFKV_PREFILL_RG
+#define FFKV_PREFILL_RG 2  // row groups of 16 query rows per wave at head_dim <= 128 (head_dim 256 takes 1)
 #endif
 
 #ifndef FFKV_PREFILL_DMA_KP128
@@ -64,7 +75,8 @@ using i32x2 = int __attribute__((ext_vector_type(2)));
 // Source of the chunks of keys that are not loaded: 64 lanes x 16 bytes of zeros (never written).
 __device__ __align__(16) uint32_t g_zero_chunks[256];
 
-template <int D, int EB, bool SC>  // EB: bytes per cached element (2, or 1 for int8 / fp8 codes); SC: int8 scales
+// EB: bytes per cached element (2, or 1 for int8 / fp8 codes); SC: int8 scales; W: waves per workgroup
+template <int D, int EB, bool SC, int W>
 struct DmaCfg
 {
     static constexpr int KP = D == 64 ? 4 : (D == 128 ? FFKV_PREFILL_DMA_KP128 : 2);  // pages per step
@@ -74,8 +86,8 @@ struct DmaCfg
     static constexpr int TILEB = KP * kBlockSize * RB; // bytes of a step's K (or V) tile
     static constexpr int SCB = SC ? 2 * KP * kBlockSize * 4 : 0;  // int8 scales of the step: K then V
     static constexpr int IPR = KP * CHUNKS / 64;       // 64-chunk load runs per tile
-    static constexpr int RPW = 2 * IPR / kDmaWaves;    // runs per wave and step (K runs first, then V)
-    static_assert(RPW >= 1 && (2 * IPR) % kDmaWaves == 0, "every wave loads whole 64-chunk runs");
+    static constexpr int RPW = 2 * IPR / W;            // runs per wave and step (K runs first, then V)
+    static_assert(RPW >= 1 && (2 * IPR) % W == 0, "every wave loads whole 64-chunk runs");
     static_assert(CHUNKS % 64 == 0, "a 64-chunk run stays inside one page");
 };
 
@@ -165,15 +177,19 @@ __device__ __forceinline__ void wait_vm()
 // pages shared by every row (pages 0 .. pfx_blocks - 1 of row 0's block table, which all rows hold): one query
 // per (row, head), attending keys 0 .. min(ctx + 1, prefix) - 1, written as (max, denominator, unnormalised
 // output) to the decode workspace for the decode merge to fold in.
-template <int QT, int D, int CT, bool PFX>
-__global__ __launch_bounds__(kDmaThreads) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 4 : 1)))
+// RG: row groups per wave.  A wave holds RG x 16 query rows; every K and V^T operand it reads from LDS feeds RG
+// matrix products, so RG = 2 halves the LDS reads and the per-step scalar work per query row (4 waves of 32 rows
+// instead of 8 waves of 16, two waves per SIMD).
+template <int QT, int D, int CT, bool PFX, int RG>
+__global__ __launch_bounds__(512 / RG) __attribute__((amdgpu_waves_per_eu(RG == 2 ? 2 : (D <= 128 ? 4 : 1))))
 void paged_prefill_dma(PrefillArgs a)
 {
+    constexpr int  W = 8 / RG;  // waves per workgroup
     constexpr int  EB = kElemBytes<CT>;
     constexpr bool Q8 = EB == 1;
     // int8 codes take bf16 MFMAs beside a bf16 q (exact: 8 significant bits), so q needs no hi / lo split
     constexpr bool BF = CT == I8 ? (FFKV_PREFILL_I8_BF && QT != F16) : kBF<CT, QT>;
-    using C = DmaCfg<D, EB, CT == I8>;  // the scale bytes (and their loads, counted in the waits) only for int8
+    using C = DmaCfg<D, EB, CT == I8, W>;  // the scale bytes (and their loads, counted in the waits) only for int8
     using M = MType<BF>;
     using X8 = typename M::x8;
     constexpr int  KP = C::KP;
@@ -181,10 +197,11 @@ void paged_prefill_dma(PrefillArgs a)
     constexpr int  NT = D / 16;
     constexpr bool NEED_LO = !((QT == BF16 && BF) || (QT == F16 && !BF));
 
-    // three stages, each [K tile | V tile | int8 scales] of KP pages, key-major with swizzled chunks
+    // three (or four) stages, each [K tile | V tile | int8 scales] of KP pages, key-major with swizzled chunks
     __shared__ __align__(16) uint8_t s_st0[2 * C::TILEB + C::SCB];
     __shared__ __align__(16) uint8_t s_st1[2 * C::TILEB + C::SCB];
     __shared__ __align__(16) uint8_t s_st2[2 * C::TILEB + C::SCB];
+    __shared__ __align__(16) uint8_t s_st3[kDmaStages == 4 ? 2 * C::TILEB + C::SCB : 16];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -218,40 +235,56 @@ void paged_prefill_dma(PrefillArgs a)
     const int row0 = rb * kDmaRows;
     if (row0 >= R) return;  // uniform over the workgroup
 
-    // This lane's query row (MFMA column): prefill token t of row b, head h; prefix: row bq, head h, its one
-    // decode query.  It sees keys [0, kend).  Pages pg_lo .. pg_hi - 1 are the workgroup's; rows 0 .. L - 1 of
-    // them hold keys (the rest load as zeros).
-    const int  r = row0 + 16 * wave + c;
-    const bool col_ok = r < R;
-    const int  h = kvh * G + (col_ok ? r % G : 0);
-    int        L, pg_lo, pg_hi, kend;
-    size_t     qrow;
-    int        bq = 0;
+    // This lane's query rows (MFMA columns), one per row group gi: row r = row0 + 16 (RG wave + gi) + c is
+    // prefill token t of row b, head h, or for the prefix its decode query of row bq, head h.  It sees keys
+    // [0, kend).  Pages pg_lo .. pg_hi - 1 are the workgroup's; rows 0 .. L - 1 of them hold keys (the rest load
+    // as zeros).
+    bool   col_ok[RG];
+    int    hq[RG], kend[RG], bq[RG];
+    size_t qrow[RG];
+    int    L, pg_lo, pg_hi;
+    int64_t ctx = 0;
     if constexpr (PFX)
     {
-        const int pfx_tokens = a.pfx_blocks * kBlockSize;
-        bq = col_ok ? r / G : 0;
-        int64_t ke = static_cast<int64_t>(a.context_lens[bq]) + 1;  // the decode query sees ctx + 1 keys
-        if (ke > a.cap_tokens) ke = a.cap_tokens;
-        ke = ke > pfx_tokens ? pfx_tokens : (ke < 0 ? 0 : ke);
-        kend = col_ok ? static_cast<int>(ke) : 0;
-        qrow = static_cast<size_t>(bq) * Hq + h;
-        L = pfx_tokens;
+        L = a.pfx_blocks * kBlockSize;
         pg_lo = chunk * a.pfx_chunk_pages;
         pg_hi = min(pg_lo + a.pfx_chunk_pages, a.pfx_blocks);
     }
     else
     {
-        const int64_t ctx = a.paged ? static_cast<int64_t>(a.context_lens[b]) : 0;
-        int64_t       Lr = ctx + S;
+        ctx = a.paged ? static_cast<int64_t>(a.context_lens[b]) : 0;
+        int64_t Lr = ctx + S;
         if (a.paged && Lr > a.cap_tokens) Lr = a.cap_tokens;
         if (Lr < 0) Lr = 0;
         L = __builtin_amdgcn_readfirstlane(static_cast<int>(Lr));
-        const int t = col_ok ? r / G : 0;
-        int64_t   ke = ctx + t + 1;
-        ke = ke > L ? L : (ke < 0 ? 0 : ke);
-        kend = col_ok ? static_cast<int>(ke) : 0;
-        qrow = (static_cast<size_t>(b) * S + t) * Hq + h;
+    }
+#pragma unroll
+    for (int gi = 0; gi < RG; ++gi)
+    {
+        const int r = row0 + 16 * (RG * wave + gi) + c;
+        col_ok[gi] = r < R;
+        hq[gi] = kvh * G + (col_ok[gi] ? r % G : 0);
+        if constexpr (PFX)
+        {
+            bq[gi] = col_ok[gi] ? r / G : 0;
+            int64_t ke = static_cast<int64_t>(a.context_lens[bq[gi]]) + 1;  // the decode query sees ctx + 1 keys
+            if (ke > a.cap_tokens) ke = a.cap_tokens;
+            ke = ke > L ? L : (ke < 0 ? 0 : ke);
+            kend[gi] = col_ok[gi] ? static_cast<int>(ke) : 0;
+            qrow[gi] = static_cast<size_t>(bq[gi]) * Hq + hq[gi];
+        }
+        else
+        {
+            bq[gi] = 0;
+            const int t = col_ok[gi] ? r / G : 0;
+            int64_t   ke = ctx + t + 1;
+            ke = ke > L ? L : (ke < 0 ? 0 : ke);
+            kend[gi] = col_ok[gi] ? static_cast<int>(ke) : 0;
+            qrow[gi] = (static_cast<size_t>(b) * S + t) * Hq + hq[gi];
+        }
+    }
+    if constexpr (!PFX)
+    {
         const int r_last = min(row0 + kDmaRows, R) - 1;
         int64_t   kw = ctx + r_last / G + 1;
         kw = kw > L ? L : (kw < 0 ? 0 : kw);
@@ -262,47 +295,50 @@ void paged_prefill_dma(PrefillArgs a)
     pg_lo = __builtin_amdgcn_readfirstlane(pg_lo);
     pg_hi = __builtin_amdgcn_readfirstlane(pg_hi);
     const int  steps = pg_hi > pg_lo ? (pg_hi - pg_lo + KP - 1) / KP : 0;
-    const bool wave_active = row0 + 16 * wave < R;
+    const bool wave_active = row0 + 16 * RG * wave < R;
 
-    // ---- Q^T operands of the wave's 16 query rows ----------------------------------------------------------
-    X8           qhi[KSTEPS], qlo[KSTEPS];
+    // ---- Q^T operands of the wave's RG x 16 query rows -----------------------------------------------------
+    X8 qhi[RG][KSTEPS], qlo[RG][KSTEPS];
 #pragma unroll
-    for (int j = 0; j < KSTEPS; ++j)
-    {
-        const int d0 = 32 * j + 8 * g;
-        if constexpr (!NEED_LO)
+    for (int gi = 0; gi < RG; ++gi)
+#pragma unroll
+        for (int j = 0; j < KSTEPS; ++j)
         {
-            u32x4 w = u32x4{0u, 0u, 0u, 0u};
-            if (col_ok) w = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.q) + qrow * D + d0);
-            qhi[j] = __builtin_bit_cast(X8, w);
-            qlo[j] = qhi[j];
-        }
-        else
-        {
-            float x[8];
-            if (col_ok)
-                load_q8<QT>(a.q, qrow * D + d0, x);
-            else
-#pragma unroll
-                for (int e = 0; e < 8; ++e) x[e] = 0.0f;
-            uint32_t hi[8], lo[8];
-#pragma unroll
-            for (int e = 0; e < 8; ++e)
+            const int d0 = 32 * j + 8 * g;
+            if constexpr (!NEED_LO)
             {
-                hi[e] = M::bits(x[e]);
-                lo[e] = M::bits(x[e] - M::value(hi[e]));
+                u32x4 w = u32x4{0u, 0u, 0u, 0u};
+                if (col_ok[gi])
+                    w = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.q) + qrow[gi] * D + d0);
+                qhi[gi][j] = __builtin_bit_cast(X8, w);
+                qlo[gi][j] = qhi[gi][j];
             }
-            qhi[j] = __builtin_bit_cast(X8, u32x4{hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16), hi[4] | (hi[5] << 16),
-                                                  hi[6] | (hi[7] << 16)});
-            qlo[j] = __builtin_bit_cast(X8, u32x4{lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16), lo[4] | (lo[5] << 16),
-                                                  lo[6] | (lo[7] << 16)});
+            else
+            {
+                float x[8];
+                if (col_ok[gi])
+                    load_q8<QT>(a.q, qrow[gi] * D + d0, x);
+                else
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) x[e] = 0.0f;
+                uint32_t hi[8], lo[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                {
+                    hi[e] = M::bits(x[e]);
+                    lo[e] = M::bits(x[e] - M::value(hi[e]));
+                }
+                qhi[gi][j] = __builtin_bit_cast(X8, u32x4{hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16),
+                                                          hi[4] | (hi[5] << 16), hi[6] | (hi[7] << 16)});
+                qlo[gi][j] = __builtin_bit_cast(X8, u32x4{lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16),
+                                                          lo[4] | (lo[5] << 16), lo[6] | (lo[7] << 16)});
+            }
         }
-    }
 
     // Nothing else is in flight from here on but the page loads: the pipeline's waits count only those.
     wait_vm<0>();
 
-    // ---- loads: wave w fetches runs w*IPW .. w*IPW + IPW - 1 (64 chunks each) of the K tile and of the V tile --
+    // ---- loads: wave w fetches runs w*RPW .. w*RPW + RPW - 1 (64 chunks each) of the K tile and of the V tile --
     const FFKV_CONST int32_t* table_row =  // prefix: row 0's table, whose first pfx_blocks entries every row shares
         a.paged ? (const FFKV_CONST int32_t*)(a.block_table + static_cast<int64_t>(b) * a.max_blocks) : nullptr;
     const char* zero_src = reinterpret_cast<const char*>(g_zero_chunks) + 16 * lane;
@@ -331,56 +367,69 @@ void paged_prefill_dma(PrefillArgs a)
     }
     const size_t row_bytes = static_cast<size_t>(Hkv) * C::RB;  // one key row of all kv heads
 
+    // Per-run constants of this wave's loads (uniform): source tensor at kv head kvh, page of the step, LDS
+    // destination.  A page's byte offset is row_base + index * page_bytes, with index the physical page (paged) or
+    // the page of the row (contiguous keys).
+    const char* run_src[C::RPW];
+    int         run_u[C::RPW];
+    int         run_dst[C::RPW];
+#pragma unroll
+    for (int k = 0; k < C::RPW; ++k)
+    {
+        const int  run = wave * C::RPW + k;
+        const bool is_v = run >= C::IPR;
+        const int  lr = is_v ? run - C::IPR : run;
+        run_u[k] = lr * 64 / C::CHUNKS;
+        run_src[k] = static_cast<const char*>(is_v ? a.v_cache : a.k_cache) + static_cast<size_t>(kvh) * C::RB;
+        run_dst[k] = (is_v ? C::TILEB : 0) + lr * 64 * 16;
+    }
+    const uint32_t page_bytes = static_cast<uint32_t>(kBlockSize * row_bytes);
+    const uint64_t row_base = a.paged ? 0 : static_cast<uint64_t>(b) * S * row_bytes;
+
     // Requests step si into `stage`; returns its page mask (bit u: page pg_lo + si*KP + u is present; keys on absent
     // pages are masked).  Block-table entries are uniform and come through the scalar cache.  Pages whose 16
     // rows are all keys of the row load with a uniform base; the row's last, partial page (and absent pages)
-    // fetch the zero block for the missing rows.
+    // fetch the zero block for the missing rows.  The scalar work is kept short: it runs once per step in every
+    // wave, in order with the wave's matrix and vector work.
     auto issue = [&](int si, uint8_t* stage) -> int
     {
-        int    okm = 0, full = 0;
-        size_t page_off[KP];  // byte offset of (page row 0, kv head kvh) in the caches
-        int    page_row[KP];  // paged: physical page (present pages); int8 scales are indexed by it
+        int      okm = 0, full = 0;
+        uint64_t page_off[KP];
+        uint32_t page_row[KP];  // physical page of present pages (int8 scales are indexed by it), else 0
 #pragma unroll
         for (int u = 0; u < KP; ++u)
         {
             const int pg = pg_lo + si * KP + u;
-            page_off[u] = 0;
-            page_row[u] = 0;
+            uint32_t  idx = 0;
+            bool      present = false;
             if (pg < pg_hi)  // pg_hi <= max_blocks
             {
-                bool present = true;
-                size_t r0;
                 if (a.paged)
                 {
-                    const int phys = table_row[pg];
-                    present = phys >= 0 && phys < a.num_blocks;
-                    page_row[u] = present ? phys : 0;
-                    r0 = static_cast<size_t>(present ? phys : 0) * kBlockSize;
+                    idx = static_cast<uint32_t>(table_row[pg]);
+                    present = idx < static_cast<uint32_t>(a.num_blocks);  // negative entries are absent
                 }
                 else
                 {
-                    r0 = static_cast<size_t>(b) * S + static_cast<size_t>(pg) * kBlockSize;
-                }
-                page_off[u] = r0 * row_bytes + static_cast<size_t>(kvh) * C::RB;
-                if (present)
-                {
-                    okm |= 1 << u;
-                    if ((pg + 1) * kBlockSize <= L) full |= 1 << u;
+                    idx = static_cast<uint32_t>(pg);
+                    present = true;
                 }
             }
+            idx = present ? idx : 0u;
+            page_row[u] = idx;
+            page_off[u] = row_base + static_cast<uint64_t>(idx) * page_bytes;
+            okm |= present ? 1 << u : 0;
+            full |= present && (pg + 1) * kBlockSize <= L ? 1 << u : 0;
         }
 #pragma unroll
         for (int k = 0; k < C::RPW; ++k)
         {
-            const int   run = wave * C::RPW + k;
-            const bool  is_v = run >= C::IPR;  // uniform
-            const int   lr = is_v ? run - C::IPR : run;
-            const int   u = lr * 64 / C::CHUNKS;  // page of the step (uniform)
-            size_t      poff = page_off[0];  // page_off[u] without a dynamic index (u is uniform but not constant)
+            const int u = run_u[k];
+            uint64_t  poff = page_off[0];  // page_off[u] without a dynamic index (u is uniform but not constant)
 #pragma unroll
             for (int uu = 1; uu < KP; ++uu) poff = u == uu ? page_off[uu] : poff;
-            const char* base = static_cast<const char*>(is_v ? a.v_cache : a.k_cache) + poff;
-            const FFKV_LDS void* dst = (const FFKV_LDS void*)(stage + (is_v ? C::TILEB : 0) + lr * 64 * 16);
+            const char*          base = run_src[k] + poff;
+            const FFKV_LDS void* dst = (const FFKV_LDS void*)(stage + run_dst[k]);
             if ((full >> u) & 1)
             {
                 load_lds16(base, voff[k], dst);
@@ -402,7 +451,7 @@ void paged_prefill_dma(PrefillArgs a)
                 const bool is_v = e >= KP * kBlockSize;
                 const int  u = (e / kBlockSize) % KP;
                 const int  t = e % kBlockSize;
-                int        pr = page_row[0];
+                uint32_t   pr = page_row[0];
 #pragma unroll
                 for (int uu = 1; uu < KP; ++uu) pr = u == uu ? page_row[uu] : pr;
                 const bool take = ((okm >> u) & 1) && (pg_lo + si * KP + u) * kBlockSize + t < L;
@@ -428,14 +477,21 @@ void paged_prefill_dma(PrefillArgs a)
         v_head_scale = a.v_scale[kvh];
     }
     const float thr_raw = 8.0f / c_log2;
-    float       m_run = kNegInf;
-    float       l_run = 0.0f;
-    f32x4       acc[NT];
+    float       m_run[RG], l_run[RG];
+    f32x4       acc[RG][NT];
 #pragma unroll
-    for (int n = 0; n < NT; ++n) acc[n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int gi = 0; gi < RG; ++gi)
+    {
+        m_run[gi] = kNegInf;
+        l_run[gi] = 0.0f;
+#pragma unroll
+        for (int n = 0; n < NT; ++n) acc[gi][n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
 
     // Smallest causal limit over the wave's active columns: steps wholly below it need no mask.
-    int kmin = col_ok ? kend : INT32_MAX;
+    int kmin = INT32_MAX;
+#pragma unroll
+    for (int gi = 0; gi < RG; ++gi) kmin = col_ok[gi] ? min(kmin, kend[gi]) : kmin;
 #pragma unroll
     for (int off = 1; off < 16; off <<= 1) kmin = min(kmin, __shfl_xor(kmin, off, 64));
     kmin = __builtin_amdgcn_readfirstlane(kmin);
@@ -459,12 +515,13 @@ void paged_prefill_dma(PrefillArgs a)
     const int v8sw = v8_swizzle<D>(v8key, v8pg);
     const int v8base = C::TILEB + v8pg * kBlockSize * C::RB + v8key * C::RB + 8 * (c & 1);
 
-    auto compute = [&](int si, const uint8_t* stage, int okm)
+    // S^T tiles of a step: scores of the wave's RG x 16 columns against the step's KP pages
+    auto qk = [&](const uint8_t* stage, f32x4 (&s)[RG][KP])
     {
-        const int pg0 = pg_lo + si * KP;
-        f32x4     s[KP];
 #pragma unroll
-        for (int u = 0; u < KP; ++u) s[u] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int gi = 0; gi < RG; ++gi)
+#pragma unroll
+            for (int u = 0; u < KP; ++u) s[gi][u] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
         auto kread = [&](int j, int u) -> X8
         {
             if constexpr (Q8)
@@ -479,6 +536,7 @@ void paged_prefill_dma(PrefillArgs a)
                 return __builtin_bit_cast(X8, *reinterpret_cast<const u32x4*>(stage + u * kBlockSize * C::RB + ka));
             }
         };
+        // every K operand read from LDS feeds the products of all RG row groups
         X8 kc[KP];
 #pragma unroll
         for (int u = 0; u < KP; ++u) kc[u] = kread(0, u);
@@ -490,10 +548,12 @@ void paged_prefill_dma(PrefillArgs a)
             for (int u = 0; u < KP; ++u) kn[u] = j + 1 < KSTEPS ? kread(j + 1, u) : kc[u];  // next k-step in flight
 #pragma unroll
             for (int u = 0; u < KP; ++u)
-            {
-                s[u] = M::mma32(kc[u], qhi[j], s[u]);
-                if constexpr (NEED_LO) s[u] = M::mma32(kc[u], qlo[j], s[u]);
-            }
+#pragma unroll
+                for (int gi = 0; gi < RG; ++gi)
+                {
+                    s[gi][u] = M::mma32(kc[u], qhi[gi][j], s[gi][u]);
+                    if constexpr (NEED_LO) s[gi][u] = M::mma32(kc[u], qlo[gi][j], s[gi][u]);
+                }
 #pragma unroll
             for (int u = 0; u < KP; ++u) kc[u] = kn[u];
         }
@@ -501,51 +561,67 @@ void paged_prefill_dma(PrefillArgs a)
         {
 #pragma unroll
             for (int u = 0; u < KP; ++u)
-                s[u] *= *reinterpret_cast<const f32x4*>(stage + 2 * C::TILEB + (u * kBlockSize + 4 * g) * 4);
+            {
+                const f32x4 ksc = *reinterpret_cast<const f32x4*>(stage + 2 * C::TILEB + (u * kBlockSize + 4 * g) * 4);
+#pragma unroll
+                for (int gi = 0; gi < RG; ++gi) s[gi][u] *= ksc;
+            }
         }
-        float sc[KP * 4];
-        float mt = kNegInf;
-        if (okm == (1 << KP) - 1 && (pg0 + KP) * kBlockSize <= kmin)  // uniform: every key visible to every column
+    };
+
+    // Online softmax of a step's scores and O^T += V^T P^T from its stage.
+    auto softmax_pv = [&](int si, const uint8_t* stage, int okm, const f32x4 (&s)[RG][KP])
+    {
+        const int pg0 = pg_lo + si * KP;
+        // uniform: every key of the step is visible to every column of the wave
+        const bool unmasked = okm == (1 << KP) - 1 && (pg0 + KP) * kBlockSize <= kmin;
+        float      pv[RG][KP * 4];
+#pragma unroll
+        for (int gi = 0; gi < RG; ++gi)
         {
+            float sc[KP * 4];
+            float mt = kNegInf;
+            if (unmasked)
+            {
 #pragma unroll
-            for (int u = 0; u < KP; ++u)
+                for (int u = 0; u < KP; ++u)
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
-                {
-                    sc[4 * u + i] = s[u][i];
-                    mt = fmaxf(mt, sc[4 * u + i]);
-                }
-        }
-        else
-        {
-            const int kr = kend - pg0 * kBlockSize - 4 * g;  // key 4g + i of page u is visible iff 16u + i < kr
+                    for (int i = 0; i < 4; ++i)
+                    {
+                        sc[4 * u + i] = s[gi][u][i];
+                        mt = fmaxf(mt, sc[4 * u + i]);
+                    }
+            }
+            else
+            {
+                const int kr = kend[gi] - pg0 * kBlockSize - 4 * g;  // key 4g + i of page u visible iff 16u + i < kr
 #pragma unroll
-            for (int u = 0; u < KP; ++u)
+                for (int u = 0; u < KP; ++u)
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
-                {
-                    const bool vis = ((okm >> u) & 1) && u * kBlockSize + i < kr;
-                    sc[4 * u + i] = vis ? s[u][i] : kNegInf;
-                    mt = fmaxf(mt, sc[4 * u + i]);
-                }
-        }
-        mt = xor_max(mt);
-        const bool upd = mt > m_run + thr_raw;  // false while the column has seen no key (mt = -inf)
-        if (__any(upd))
-        {
-            const float alpha = upd ? __builtin_amdgcn_exp2f((m_run - mt) * c_log2) : 1.0f;  // 0 on the first key
-            l_run *= alpha;
+                    for (int i = 0; i < 4; ++i)
+                    {
+                        const bool vis = ((okm >> u) & 1) && u * kBlockSize + i < kr;
+                        sc[4 * u + i] = vis ? s[gi][u][i] : kNegInf;
+                        mt = fmaxf(mt, sc[4 * u + i]);
+                    }
+            }
+            mt = xor_max(mt);
+            const bool upd = mt > m_run[gi] + thr_raw;  // false while the column has seen no key (mt = -inf)
+            if (__any(upd))
+            {
+                const float alpha = upd ? __builtin_amdgcn_exp2f((m_run[gi] - mt) * c_log2) : 1.0f;  // 0 at first
+                l_run[gi] *= alpha;
 #pragma unroll
-            for (int n = 0; n < NT; ++n) acc[n] *= alpha;
-            m_run = upd ? mt : m_run;
-        }
-        const float mneg = m_run == kNegInf ? 0.0f : -m_run * c_log2;  // a column with no key: every p is 0
-        float       pv[KP * 4];
+                for (int n = 0; n < NT; ++n) acc[gi][n] *= alpha;
+                m_run[gi] = upd ? mt : m_run[gi];
+            }
+            const float mneg = m_run[gi] == kNegInf ? 0.0f : -m_run[gi] * c_log2;  // no key yet: every p is 0
 #pragma unroll
-        for (int e = 0; e < KP * 4; ++e)
-        {
-            pv[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[e], c_log2, mneg));
-            l_run += pv[e];
+            for (int e = 0; e < KP * 4; ++e)
+            {
+                pv[gi][e] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[e], c_log2, mneg));
+                l_run[gi] += pv[gi][e];
+            }
         }
         if constexpr (CT == I8)  // per-token V scales multiply P (the denominator keeps the unscaled p)
         {
@@ -555,7 +631,9 @@ void paged_prefill_dma(PrefillArgs a)
                 const f32x4 vsc = *reinterpret_cast<const f32x4*>(
                     stage + 2 * C::TILEB + ((KP + u) * kBlockSize + 4 * g) * 4);
 #pragma unroll
-                for (int i = 0; i < 4; ++i) pv[4 * u + i] *= vsc[i];
+                for (int gi = 0; gi < RG; ++gi)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) pv[gi][4 * u + i] *= vsc[i];
             }
         }
 
@@ -583,89 +661,124 @@ void paged_prefill_dma(PrefillArgs a)
 #pragma unroll
         for (int u0 = 0; u0 < KP; u0 += 2)
         {
-            // P^T operand: pairs of p rounded to the MFMA type (packed conversions); for bf16 also the residual
+            // P^T operands: pairs of p rounded to the MFMA type (packed conversions); for bf16 also the residual
             // p - hi, which keeps 16 significant bits in two products (f16's 11 bits suffice in one).
-            uint32_t ph[4], pl[4];
+            X8 phi[RG], plo[RG];
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
+            for (int gi = 0; gi < RG; ++gi)
             {
-                const f32x2 v = f32x2{pv[4 * u0 + 2 * e], pv[4 * u0 + 2 * e + 1]};
-                if constexpr (BF)
+                uint32_t ph[4], pl[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
                 {
-                    ph[e] = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
-                    const f32x2 r = f32x2{v[0] - __builtin_bit_cast(float, ph[e] << 16),
-                                          v[1] - __builtin_bit_cast(float, ph[e] & 0xffff0000u)};
-                    pl[e] = __builtin_bit_cast(uint32_t, __builtin_convertvector(r, bf16x2));
+                    const f32x2 v = f32x2{pv[gi][4 * u0 + 2 * e], pv[gi][4 * u0 + 2 * e + 1]};
+                    if constexpr (BF)
+                    {
+                        ph[e] = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+                        const f32x2 r = f32x2{v[0] - __builtin_bit_cast(float, ph[e] << 16),
+                                              v[1] - __builtin_bit_cast(float, ph[e] & 0xffff0000u)};
+                        pl[e] = __builtin_bit_cast(uint32_t, __builtin_convertvector(r, bf16x2));
+                    }
+                    else
+                    {
+                        ph[e] = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, h2));
+                        pl[e] = 0u;
+                    }
                 }
-                else
-                {
-                    ph[e] = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, h2));
-                }
+                phi[gi] = __builtin_bit_cast(X8, u32x4{ph[0], ph[1], ph[2], ph[3]});
+                plo[gi] = __builtin_bit_cast(X8, u32x4{pl[0], pl[1], pl[2], pl[3]});
             }
-            const X8 phi = __builtin_bit_cast(X8, u32x4{ph[0], ph[1], ph[2], ph[3]});
-            X8       plo{};
-            if constexpr (BF) plo = __builtin_bit_cast(X8, u32x4{pl[0], pl[1], pl[2], pl[3]});
+            // every V^T operand read from LDS feeds the products of all RG row groups
             X8 vcur = vread(0, u0);
 #pragma unroll
             for (int n = 0; n < NT; ++n)
             {
                 X8 vnxt{};
                 if (n + 1 < NT) vnxt = vread(n + 1, u0);  // next tile's reads in flight behind this tile's products
-                acc[n] = M::mma32(vcur, phi, acc[n]);
-                if constexpr (BF) acc[n] = M::mma32(vcur, plo, acc[n]);
+#pragma unroll
+                for (int gi = 0; gi < RG; ++gi)
+                {
+                    acc[gi][n] = M::mma32(vcur, phi[gi], acc[gi][n]);
+                    if constexpr (BF) acc[gi][n] = M::mma32(vcur, plo[gi], acc[gi][n]);
+                }
                 vcur = vnxt;
             }
         }
     };
 
-    // ---- pipeline: stage si % 3 ----------------------------------------------------------------------------
+    // ---- pipeline: stage si % NS ---------------------------------------------------------------------------
     // Every step issues the same number of loads (steps past the end fetch the zero block into a stage nobody
-    // reads), so "step si has landed" is always vmcnt <= the loads of step si + 1.
+    // reads), so "step si has landed" is always vmcnt <= the loads of steps si + 1 .. si + NS - 2.
+    constexpr int NS = kDmaStages;
     constexpr int LPS = C::RPW + C::SCB / 256;  // loads per wave and step
+    // The scores' products are issued before the next loads' scalar address work, which then runs while they
+    // execute.
     auto body = [&](int si, uint8_t* cur, int okm_cur, uint8_t* nxt, int& okm_nxt)
     {
-        wait_vm<LPS>();
-        __builtin_amdgcn_s_barrier();  // step si visible to all; every wave is past step si - 1 (stage of si + 2)
-        okm_nxt = issue(si + 2, nxt);
-        if (wave_active) compute(si, cur, okm_cur);
+        wait_vm<(NS - 2) * LPS>();
+        __builtin_amdgcn_s_barrier();  // step si visible to all; every wave is past step si - 1 (stage of si+NS-1)
+        f32x4 sx[RG][KP];
+        if (wave_active) qk(cur, sx);
+        okm_nxt = issue(si + NS - 1, nxt);
+        if (wave_active) softmax_pv(si, cur, okm_cur, sx);
     };
 
     int okm0 = issue(0, s_st0);
     int okm1 = issue(1, s_st1);
-    int okm2 = 0;
-    for (int si = 0; si < steps; si += kDmaStages)
+    int okm2 = 0, okm3 = 0;
+    if constexpr (NS == 4) okm2 = issue(2, s_st2);
+    for (int si = 0; si < steps; si += NS)
     {
-        body(si, s_st0, okm0, s_st2, okm2);
-        if (si + 1 >= steps) break;
-        body(si + 1, s_st1, okm1, s_st0, okm0);
-        if (si + 2 >= steps) break;
-        body(si + 2, s_st2, okm2, s_st1, okm1);
+        if constexpr (NS == 3)
+        {
+            body(si, s_st0, okm0, s_st2, okm2);
+            if (si + 1 >= steps) break;
+            body(si + 1, s_st1, okm1, s_st0, okm0);
+            if (si + 2 >= steps) break;
+            body(si + 2, s_st2, okm2, s_st1, okm1);
+        }
+        else
+        {
+            body(si, s_st0, okm0, s_st3, okm3);
+            if (si + 1 >= steps) break;
+            body(si + 1, s_st1, okm1, s_st0, okm0);
+            if (si + 2 >= steps) break;
+            body(si + 2, s_st2, okm2, s_st1, okm1);
+            if (si + 3 >= steps) break;
+            body(si + 3, s_st3, okm3, s_st2, okm2);
+        }
     }
     wait_vm<0>();  // no load may still be writing this workgroup's LDS when it ends
 
-    const float l_tot = xor_sum(l_run);
-    if constexpr (PFX)
-    {
-        // partial of (row bq, head h) over this chunk, in the decode merge's convention: max in the log2 domain
-        if (col_ok)
-        {
-            const int64_t slot = static_cast<int64_t>(a.pfx_slot0) + static_cast<int64_t>(chunk) * a.batch + bq;
-            float*        dst = a.ws_acc + (slot * Hq + h) * D;
 #pragma unroll
-            for (int n = 0; n < NT; ++n) *reinterpret_cast<f32x4*>(dst + 16 * n + 4 * g) = acc[n] * v_head_scale;
-            if (g == 0)
+    for (int gi = 0; gi < RG; ++gi)
+    {
+        const float l_tot = xor_sum(l_run[gi]);
+        if constexpr (PFX)
+        {
+            // partial of (row bq, head hq) over this chunk, in the decode merge's convention: max in the log2 domain
+            if (col_ok[gi])
             {
-                a.ws_ml[(slot * Hq + h) * 2] = m_run == kNegInf ? kNegInf : m_run * c_log2;
-                a.ws_ml[(slot * Hq + h) * 2 + 1] = l_tot;
+                const int64_t slot =
+                    static_cast<int64_t>(a.pfx_slot0) + static_cast<int64_t>(chunk) * a.batch + bq[gi];
+                float* dst = a.ws_acc + (slot * Hq + hq[gi]) * D;
+#pragma unroll
+                for (int n = 0; n < NT; ++n)
+                    *reinterpret_cast<f32x4*>(dst + 16 * n + 4 * g) = acc[gi][n] * v_head_scale;
+                if (g == 0)
+                {
+                    a.ws_ml[(slot * Hq + hq[gi]) * 2] = m_run[gi] == kNegInf ? kNegInf : m_run[gi] * c_log2;
+                    a.ws_ml[(slot * Hq + hq[gi]) * 2 + 1] = l_tot;
+                }
             }
         }
-    }
-    else if (col_ok)
-    {
-        const float  inv = l_tot > 0.0f ? v_head_scale / l_tot : 0.0f;
-        const size_t ob = qrow * D;
+        else if (col_ok[gi])
+        {
+            const float  inv = l_tot > 0.0f ? v_head_scale / l_tot : 0.0f;
+            const size_t ob = qrow[gi] * D;
 #pragma unroll
-        for (int n = 0; n < NT; ++n) store_out4<QT>(a.out, ob + 16 * n + 4 * g, acc[n] * inv);
+            for (int n = 0; n < NT; ++n) store_out4<QT>(a.out, ob + 16 * n + 4 * g, acc[gi][n] * inv);
+        }
     }
 }
 
@@ -687,16 +800,17 @@ hipError_t launch_pfd_d(const PrefillArgs& a, hipStream_t stream)
     if (wgs <= 0) return hipSuccess;
     if (wgs > INT32_MAX) return hipErrorInvalidConfiguration;
     const dim3 grid(static_cast<unsigned>(wgs));
+    constexpr int RG = FFKV_PREFILL_RG;  // head_dim 256: one row group (two would not fit the registers)
     switch (a.head_dim)
     {
         case 64:
-            hipLaunchKernelGGL((paged_prefill_dma<QT, 64, CT, PFX>), grid, dim3(kDmaThreads), 0, stream, a);
+            hipLaunchKernelGGL((paged_prefill_dma<QT, 64, CT, PFX, RG>), grid, dim3(512 / RG), 0, stream, a);
             break;
         case 128:
-            hipLaunchKernelGGL((paged_prefill_dma<QT, 128, CT, PFX>), grid, dim3(kDmaThreads), 0, stream, a);
+            hipLaunchKernelGGL((paged_prefill_dma<QT, 128, CT, PFX, RG>), grid, dim3(512 / RG), 0, stream, a);
             break;
         default:
-            hipLaunchKernelGGL((paged_prefill_dma<QT, 256, CT, PFX>), grid, dim3(kDmaThreads), 0, stream, a);
+            hipLaunchKernelGGL((paged_prefill_dma<QT, 256, CT, PFX, 1>), grid, dim3(512), 0, stream, a);
             break;
     }
     return hipGetLastError();
