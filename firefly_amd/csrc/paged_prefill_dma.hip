@@ -800,7 +800,9 @@ hipError_t launch_pfd_d(const PrefillArgs& a, hipStream_t stream)
     if (wgs <= 0) return hipSuccess;
     if (wgs > INT32_MAX) return hipErrorInvalidConfiguration;
     const dim3 grid(static_cast<unsigned>(wgs));
-    constexpr int RG = FFKV_PREFILL_RG;  // head_dim 256: one row group (two would not fit the registers)
+    // head_dim 256: one row group (two would not fit the registers).  Prefix partials: one row group, so their
+    // few hundred workgroups still put two waves on every SIMD.
+    constexpr int RG = PFX ? 1 : FFKV_PREFILL_RG;
     switch (a.head_dim)
     {
         case 64:
