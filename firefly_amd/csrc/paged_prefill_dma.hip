@@ -621,7 +621,7 @@ void paged_prefill_dma(PrefillArgs a)
                         mt = fmaxf(mt, sc[4 * u + i]);
                     }
             }
-            mt = xor_max(mt);
+            mt = swap_max(mt);
             const bool upd = mt > m_run[gi] + thr_raw;  // false while the column has seen no key (mt = -inf)
             if (__any(upd))
             {
@@ -771,7 +771,7 @@ void paged_prefill_dma(PrefillArgs a)
 #pragma unroll
     for (int gi = 0; gi < RG; ++gi)
     {
-        const float l_tot = xor_sum(l_run[gi]);
+        const float l_tot = swap_sum(l_run[gi]);
         if constexpr (PFX)
         {
             // partial of (row bq, head hq) over this chunk, in the decode merge's convention: max in the log2 domain
