@@ -130,8 +130,7 @@ struct DecodeArgs
 
 hipError_t launch_append(const AppendArgs& a, hipStream_t stream);
 hipError_t launch_rope_append(const RopeArgs& a, hipStream_t stream);      // rotate q/k, then append when k_cache set
-hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream);          // matrix-core prefill (any cache dtype)
-hipError_t launch_prefill_dma(const PrefillArgs& a, hipStream_t stream);      // 16-bit caches, global->LDS loads
+hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream);  // matrix-core prefill (16- and 8-bit caches)
 hipError_t launch_prefix_partials(const PrefillArgs& a, hipStream_t stream);  // shared-prefix decode partials
 hipError_t launch_decode(const DecodeArgs& a, hipStream_t stream);       // generic kernel (any cache dtype)
 hipError_t launch_decode_mfma(const DecodeArgs& a, hipStream_t stream);  // matrix-core kernel (16-bit/8-bit caches)

@@ -211,6 +211,36 @@ void attention_shared_prefix(Tensor& q, Tensor& k_cache, Tensor& v_cache, Tensor
            context_lens, shared_blocks);
 }
 
+void append_kv_cache_attention(const Tensor& k, const Tensor& v, Tensor& q, Tensor& k_cache, Tensor& v_cache,
+                               Tensor& output, void* kv_cache_block_table, int kv_head_num, int max_context_blocks,
+                               const int* context_lens)
+{
+    if (q.shape().size() != 4 || q.shape()[1] != 1 || k.shape().size() != 4 || k.shape()[1] != 1 ||
+        v.shape() != k.shape() || k_cache.shape().size() != 4 || !is_gpu(q) || !is_gpu(k) || !is_gpu(v) ||
+        !is_gpu(k_cache) || !is_gpu(v_cache) || !is_gpu(output) || kv_cache_block_table == nullptr)
+        return fail("append_kv_cache_attention: decode step only (q [B, 1, Hq, D], k / v [B, 1, Hkv, D], a block "
+                    "table, all tensors on the GPU)");
+    const int B = static_cast<int>(q.shape()[0]);
+    const int Hq = static_cast<int>(q.shape()[2]);
+    const int D = static_cast<int>(q.shape()[3]);
+    if (k.shape()[0] != B || k.shape()[2] != kv_head_num || k.shape()[3] != D)
+        return fail("append_kv_cache_attention: k / v must be [B, 1, kv_head_num, head_dim]");
+    if (output.numel() < static_cast<int64_t>(B) * Hq * D || output.dtype() != q.dtype())
+        return fail("append_kv_cache_attention: output must hold B*Hq*D elements of q's dtype");
+    if (k_cache.shape()[2] != kv_head_num || k_cache.shape()[3] != D || v_cache.shape() != k_cache.shape() ||
+        v_cache.dtype() != k_cache.dtype())
+        return fail("append_kv_cache_attention: k/v caches must both be [num_blocks, 16, kv_head_num, head_dim]");
+    const size_t need = ffkv_decode_workspace_bytes(B, Hq, D, max_context_blocks, 0);
+    size_t       have = 0;
+    void*        ws = workspace(need, have);
+    const int    rc = ffkv_append_paged_decode(
+        k.data(), v.data(), code(k.dtype()), q.data(), output.data(), code(q.dtype()), k_cache.data(), v_cache.data(),
+        code(k_cache.dtype()), nullptr, nullptr, reinterpret_cast<const int32_t*>(kv_cache_block_table), context_lens,
+        B, Hq, kv_head_num, D, FFKV_BLOCK_SIZE, max_context_blocks, static_cast<int>(k_cache.shape()[0]), 0, 0.0f, ws,
+        have, t_stream);
+    report(rc, "append_kv_cache_attention failed");
+}
+
 void append_kv_cache(const Tensor& k, const Tensor& v, Tensor& k_cache, Tensor& v_cache, const int* block_table,
                      const int* context_lens, int max_blocks)
 {

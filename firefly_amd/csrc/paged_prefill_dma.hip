@@ -1,14 +1,23 @@
 // paged_prefill_dma.hip - chunked / paged prefill attention on gfx950, with the K/V pages streamed into LDS by
 // asynchronous global->LDS loads (16-bit caches, and 8-bit int8 / fp8 e4m3 codes converted at operand-read time).
 //
-// Same contract and arithmetic as paged_prefill_mfma (paged_prefill.hip), which replaces the reference's prefill
-// branch of kernels::attention (flash_attn_wmma_kernel, src/kernels/attention.cu:22-286, dispatched at :460-474)
-// and extends it to queries over a cached prefix: query token t of row b at position ctx[b] + t attends keys
-// 0 .. ctx[b] + t; without a block table the keys are the chunk's contiguous [B, S, Hkv, D] tensors (ctx = 0).
+// Replaces the reference's prefill branch of kernels::attention (flash_attn_wmma_kernel,
+// src/kernels/attention.cu:22-286, dispatched at :460-474 and routed from src/model/qwen_model.cu:147-151), which
+// attends only to the chunk's own contiguous K/V with a causal mask (key n > query m masked, :173-174), and extends
+// it to queries over a cached prefix: query token t of row b at position ctx[b] + t attends keys 0 .. ctx[b] + t
+// read from the paged cache (prefix and chunk, after the chunk's append).  Without a block table the keys are the
+// chunk's contiguous [B, S, Hkv, D] tensors and ctx = 0: exactly the reference's causal prefill.  With S = 1 it is
+// the decode attention.
 //
-// What differs is how pages reach LDS.  16-bit pages need no conversion, so every 16-byte chunk of a step's K and
-// V pages goes from HBM straight into LDS with global_load_lds_dwordx4 (each lane's 16 bytes land at the
-// instruction's LDS base + 16 * lane), with no staging registers and no LDS stores by the waves.  Three stages
+// Mapping: a workgroup serves 128 query rows of one (row b, kv head); a query row is a (token, head-in-group) pair,
+// so the GQA heads of a kv head share every K/V page.  Each wave owns 16 query rows per row group as the 16
+// columns of its MFMA tiles: S^T[key, row] = K Q^T with K (16 keys x 32 dims) as the A operand from LDS and Q^T in
+// registers, an online softmax per column (causal limit per column) over a step of pages, and O^T += V^T P^T as
+// 16x16x32 products over 32 keys with P^T straight from the score registers.
+//
+// Pages reach LDS without passing through registers: every 16-byte chunk of a step's K and V pages goes from HBM
+// straight into LDS with global_load_lds_dwordx4 (each lane's 16 bytes land at the instruction's LDS base +
+// 16 * lane), with no staging registers and no LDS stores by the waves.  Three stages
 // rotate: step i + 2 is requested as soon as every wave has finished step i - 1, so two steps of loads are in
 // flight behind the step being computed, with one barrier per step.  Each stage is its own LDS object and the
 // main loop is unrolled by three, so the compiler can tell which stage a load writes and does not hold the
@@ -19,8 +28,8 @@
 // query row.  Within a step the scores' products go out first; the scalar address work of the next step's loads
 // (block-table reads, page offsets) then runs while they execute instead of ahead of them.
 //
-// Both tiles stay row-major (key-major).  The K operand of S^T = K Q^T reads 8 consecutive dims of one key as
-// before; the V^T operand of O^T += V^T P^T needs 8 consecutive keys of one dim, which ds_read_b64_tr_b16 gives
+// Both tiles stay row-major (key-major).  The K operand of S^T = K Q^T reads 8 consecutive dims of one key;
+// the V^T operand of O^T += V^T P^T needs 8 consecutive keys of one dim, which ds_read_b64_tr_b16 gives
 // directly: within each 16-lane group, lane 4r + q supplies the address of dims 4q .. 4q + 3 of key row r, and
 // lane j receives dim j of rows 0..3.  16-byte chunks of a key row are XOR-swizzled by row so that neither the
 // K reads (16 rows, one chunk) nor the transposed V reads (4 rows, two chunks per 16-lane group) collide in LDS
@@ -871,7 +880,7 @@ hipError_t launch_pfd(const PrefillArgs& a, hipStream_t stream)
 
 }  // namespace
 
-hipError_t launch_prefill_dma(const PrefillArgs& a, hipStream_t stream) { return launch_pfd<false>(a, stream); }
+hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream) { return launch_pfd<false>(a, stream); }
 
 hipError_t launch_prefix_partials(const PrefillArgs& a, hipStream_t stream) { return launch_pfd<true>(a, stream); }
 

@@ -61,6 +61,18 @@ FIREFLY_API void attention_shared_prefix(Tensor& q, Tensor& k_cache, Tensor& v_c
                                          const int* context_lens, int shared_blocks);
 
 /**
+ * @brief The decode step's append_kv_cache(k, v, ...) followed by the decode branch of attention(q, ...), as one
+ * call (ffkv_append_paged_decode): k / v [B, 1, kv_head_num, head_dim] are the step's new tokens, written to the
+ * pages at context_lens[b] exactly as append_kv_cache writes them, and q [B, 1, Hq, head_dim] attends
+ * context_lens[b] + 1 keys.  One kernel launch when k / v have the cache's 16-bit dtype, the two calls otherwise.
+ * The reference runs the pair as two launches (src/model/qwen_model.cu:138-146); 16-bit caches only here (the
+ * quantized caches take the scale-taking append_kv_cache and attention overloads).
+ */
+FIREFLY_API void append_kv_cache_attention(const Tensor& k, const Tensor& v, Tensor& q, Tensor& k_cache,
+                                           Tensor& v_cache, Tensor& output, void* kv_cache_block_table,
+                                           int kv_head_num, int max_context_blocks, const int* context_lens);
+
+/**
  * @brief Write new K/V tokens into their pages (the reference's append_kv_cache kernel).
  *
  * k, v [B, S, Hkv, D] (F32/F16/BF16); k_cache, v_cache [num_blocks, 16, Hkv, D]; token t of row b goes to

@@ -70,6 +70,26 @@ int kas_decode_shared_prefix(void* q, void* k_cache, void* v_cache, void* out, c
     return 0;
 }
 
+// The decode step as one call: kernels::append_kv_cache_attention(k_new, v_new, q, ...), k_new / v_new
+// [B, 1, Hkv, D] in dtype kd, q / out in dtype qd, caches [N, 16, Hkv, D] in dtype cd.
+int kas_append_attention(void* k_new, void* v_new, int kd, void* q, void* k_cache, void* v_cache, void* out,
+                         const int* block_table, const int* context_lens, int B, int Hq, int Hkv, int D, int N,
+                         int max_blocks, int qd, int cd, void* stream)
+{
+    kernels::set_default_stream(static_cast<hipStream_t>(stream));
+    const DType qt = static_cast<DType>(qd), ct = static_cast<DType>(cd), kt = static_cast<DType>(kd);
+    Tensor      tk = Tensor::from_external(k_new, {B, 1, Hkv, D}, kt, Device::GPU);
+    Tensor      tv = Tensor::from_external(v_new, {B, 1, Hkv, D}, kt, Device::GPU);
+    Tensor      tq = Tensor::from_external(q, {B, 1, Hq, D}, qt, Device::GPU);
+    Tensor      kc = Tensor::from_external(k_cache, {N, 16, Hkv, D}, ct, Device::GPU);
+    Tensor      vc = Tensor::from_external(v_cache, {N, 16, Hkv, D}, ct, Device::GPU);
+    Tensor      to = Tensor::from_external(out, {B, 1, Hq * D}, qt, Device::GPU);
+    kernels::append_kv_cache_attention(tk, tv, tq, kc, vc, to, const_cast<int*>(block_table), Hkv, max_blocks,
+                                       context_lens);
+    if (!kernels::last_error().empty()) return g_err = kernels::last_error(), -1;
+    return 0;
+}
+
 // The reference's per-layer sequence with the rotary embedding (src/model/qwen_model.cu:136-143): fused == 1
 // calls kernels::rope_append_kv_cache, else kernels::apply_rope then kernels::append_kv_cache.  q [B,S,Hq,D],
 // k/v [B,S,Hkv,D] in dtype qd (q and k rotated in place); caches [N,16,Hkv,D] in dtype cd.

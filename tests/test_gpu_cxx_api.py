@@ -41,6 +41,8 @@ def shim(ff):
     lib.kas_paged_prefill.argtypes = [vp] * 8 + [i] * 9 + [vp]
     lib.kas_decode_shared_prefix.restype = i
     lib.kas_decode_shared_prefix.argtypes = [vp] * 6 + [i] * 9 + [vp]
+    lib.kas_append_attention.restype = i
+    lib.kas_append_attention.argtypes = [vp, vp, i] + [vp] * 6 + [i] * 8 + [vp]
     return lib
 
 
@@ -192,3 +194,34 @@ def test_cxx_api_decode_shared_prefix(shim, gpu):
     assert rc == 0, shim.kas_last_error()
     got = out.float().cpu().numpy().reshape(out32.shape)
     assert _excess_bf16(got, out32) <= 2e-3
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("act,kv", [("bf16", "bf16"), ("f16", "f16"), ("f32", "bf16")])
+def test_cxx_api_append_kv_cache_attention(shim, gpu, act, kv):
+    """kernels::append_kv_cache_attention (the decode step in one call; one launch when k / v have the cache's
+    dtype, append then decode otherwise): pages bit-exact with the CPU checker's append, output within 2e-3."""
+    import torch
+
+    import gpu_util as gu
+
+    rng = np.random.default_rng(61)
+    ctx = rng.integers(0, 900, size=20)
+    c = cases.make_case(61, 20, 32, 8, 128, ctx, act=act, kv=kv)
+    kp, vp, _, _, _, out32 = cases.oracle_step(c)
+    dk, dv = gu.to_dev(c.k_pool, c.kv, gpu), gu.to_dev(c.v_pool, c.kv, gpu)
+    q, kn, vn = gu.to_dev(c.q, c.act, gpu), gu.to_dev(c.k_new, c.act, gpu), gu.to_dev(c.v_new, c.act, gpu)
+    bt, cx = torch.from_numpy(c.block_table).to(gpu), torch.from_numpy(c.ctx).to(gpu)
+    out = torch.empty((c.B, 1, c.Hq * c.D), dtype=q.dtype, device=gpu)
+    rc = shim.kas_append_attention(kn.data_ptr(), vn.data_ptr(), c.act, q.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+                                   out.data_ptr(), bt.data_ptr(), cx.data_ptr(), c.B, c.Hq, c.Hkv, c.D, c.num_blocks,
+                                   c.max_blocks, c.act, c.kv, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert rc == 0, shim.kas_last_error()
+    assert np.array_equal(gu.to_host(dk, np.uint16).view(np.uint8), kp.view(np.uint8))
+    assert np.array_equal(gu.to_host(dv, np.uint16).view(np.uint8), vp.view(np.uint8))
+    from test_gpu_parity import half_ulp
+
+    got = out.float().cpu().numpy().reshape(out32.shape)
+    diff = np.abs(got.astype(np.float64) - out32)
+    assert float((diff - half_ulp(np.maximum(np.abs(got), np.abs(out32)), c.act)).max()) <= 2e-3
