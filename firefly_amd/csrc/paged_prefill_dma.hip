@@ -203,8 +203,11 @@ __device__ __forceinline__ void wait_vm()
 // RG: row groups per wave.  A wave holds RG x 16 query rows; every K and V^T operand it reads from LDS feeds RG
 // matrix products, so RG = 2 halves the LDS reads and the per-step scalar work per query row (4 waves of 32 rows
 // instead of 8 waves of 16, two waves per SIMD).
+// Register budget: 256 at two row groups (two waves per SIMD); one row group at head_dim <= 128 takes 128 (four waves
+// per SIMD), or 168 for int8 codes, whose scales and conversions would spill at 128.
 template <int QT, int D, int CT, bool PFX, int RG>
-__global__ __launch_bounds__(512 / RG) __attribute__((amdgpu_waves_per_eu(RG == 2 ? 2 : (D <= 128 ? 4 : 1))))
+__global__ __launch_bounds__(512 / RG)
+__attribute__((amdgpu_waves_per_eu(RG == 2 ? 2 : (D <= 128 ? (CT == I8 ? 3 : 4) : 1))))
 void paged_prefill_dma(PrefillArgs a)
 {
     constexpr int  W = 8 / RG;  // waves per workgroup
