@@ -380,13 +380,22 @@ def cpu_baseline(ctx, table, N, k_pool, v_pool, q, gpu_out, seconds: float = 10.
         if time.perf_counter() - t0 > seconds and len(runs) >= 3:
             break
     t = float(np.median(runs))
+    # the same call on one core (two runs, after the threaded ones)
+    one = []
+    for _ in range(2):
+        s = time.perf_counter()
+        O.paged_decode(qn, O.DTYPE_BF16, kp, vp, O.DTYPE_BF16, table, ctx, threads=1)
+        one.append(time.perf_counter() - s)
+    t1 = float(min(one))
     got = gpu_out.float().cpu().numpy().reshape(out32.shape)
     err = float(np.abs(got - out32).max())
     tbs = decode_bytes(ctx) / t / 1e12
     return ({"value": tbs, "unit": "TB/s", "cores": threads, "kind": "port",
              "tokens_per_s": len(ctx) / t, "ms_per_call": t * 1e3,
+             "single_core": {"value": decode_bytes(ctx) / t1 / 1e12, "ms_per_call": t1 * 1e3},
              "sample": f"full layer-0 decode call of the workload (B={len(ctx)}, {int(sum(ctx)) + len(ctx)} "
-                       f"context tokens), median of {len(runs)} runs"}, err)
+                       f"context tokens), median of {len(runs)} runs on {threads} threads; single_core: best of "
+                       f"2 runs on 1 thread"}, err)
 
 
 def main(argv=None) -> int:

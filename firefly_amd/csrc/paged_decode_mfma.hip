@@ -81,10 +81,15 @@ struct PageRegs
 #define FFKV_MFMA_WAVES128_I8 2
 #endif
 
+#ifndef FFKV_MFMA_DEPTH256
+#define FFKV_MFMA_DEPTH256 1  // head_dim 256: a page in flight is 64 registers (16-bit), two would spill
+#endif
+
 // Pages whose K/V loads are in flight while a wave finishes the page before them.
-template <int CT>
+template <int CT, int D>
 constexpr int kMfmaDepth =
-    kElemBytes<CT> == 2 ? FFKV_MFMA_DEPTH16 : (CT == FP8 ? FFKV_MFMA_DEPTH_FP8 : FFKV_MFMA_DEPTH_I8);
+    D == 256 ? FFKV_MFMA_DEPTH256
+             : (kElemBytes<CT> == 2 ? FFKV_MFMA_DEPTH16 : (CT == FP8 ? FFKV_MFMA_DEPTH_FP8 : FFKV_MFMA_DEPTH_I8));
 
 // Waves per SIMD the register budget is sized for (168 registers at 3, 128 at 4, 256 at 2).
 template <int CT, int QT, int D>
@@ -92,7 +97,7 @@ constexpr int kMfmaWaves =
     D == 256 ? 2
              : (D == 128 ? (kElemBytes<CT> == 2 ? FFKV_MFMA_WAVES128_16
                                                 : (CT == FP8 ? FFKV_MFMA_WAVES128_FP8 : FFKV_MFMA_WAVES128_I8))
-                         : (kMfmaDepth<CT> > 1 ? 3 : 4));
+                         : (kMfmaDepth<CT, D> > 1 ? 3 : 4));
 
 #ifndef FFKV_DECODE_TRV
 #define FFKV_DECODE_TRV 1  // V^T operands through transposed LDS reads (ds_read_b64_tr_b16)
@@ -118,7 +123,7 @@ void paged_decode_mfma(DecodeArgs a)
     constexpr int  KSTEPS = D / 32;
     constexpr int  NT = D / 16;  // output tiles of 16 dims
     constexpr bool NEED_LO = !((QT == BF16 && BF) || (QT == F16 && !BF));
-    constexpr int  DEPTH = kMfmaDepth<CT>;
+    constexpr int  DEPTH = kMfmaDepth<CT, D>;
     constexpr int  NW = kElemBytes<CT> == 2 ? KSTEPS : KSTEPS / 2;
 
     __shared__ uint16_t s_v[FFKV_MFMA_MAX_WAVES][kBlockSize * D];

@@ -68,6 +68,17 @@ def test_head_shapes(ff, gpu, D, G):
     _check(ff, gpu, c, 2e-3)
 
 
+@pytest.mark.parametrize("act,kv", [("f16", "f16"), ("f32", "bf16"), ("bf16", "f16"), ("bf16", "i8"), ("f16", "i8"),
+                                    ("bf16", "fp8"), ("f32", "fp8")])
+def test_head_dim_256_dtypes(ff, gpu, act, kv):
+    """head_dim 256 keeps one page in flight per wave (two would not fit the registers), for every q / cache
+    type pair, including the ones whose q is split into two MFMA parts."""
+    rng = np.random.default_rng(256)
+    ctx = rng.integers(0, 900, size=7)
+    c = cases.make_case(256, 7, 16, 4, 256, ctx, act=act, kv=kv, input_scale=1 / math.sqrt(256))
+    _check(ff, gpu, c, 2e-3 if kv in ("f16", "bf16") else 2e-2)
+
+
 def test_config2_full(ff, gpu):
     """BASELINE config 2 at full size: Qwen3-8B layer, B=64, contexts U[512, 4096]."""
     rng = np.random.default_rng(2)
