@@ -17,11 +17,10 @@
 //
 // Pages reach LDS without passing through registers: every 16-byte chunk of a step's K and V pages goes from HBM
 // straight into LDS with global_load_lds_dwordx4 (each lane's 16 bytes land at the instruction's LDS base +
-// 16 * lane), with no staging registers and no LDS stores by the waves.  Three stages
-// rotate: step i + 2 is requested as soon as every wave has finished step i - 1, so two steps of loads are in
-// flight behind the step being computed, with one barrier per step.  Each stage is its own LDS object and the
-// main loop is unrolled by three, so the compiler can tell which stage a load writes and does not hold the
-// compute of one stage behind the loads into another.
+// 16 * lane), with no staging registers and no LDS stores by the waves.  NS stages rotate (two at head_dim 128
+// and 256, three at 64): step i + NS - 1 is requested as soon as every wave has finished step i - 1, so NS - 1
+// steps of loads are in flight behind the step being computed, with one barrier per step.  Each stage is its own LDS object and the main loop is unrolled by NS, so the compiler can tell
+// which stage a load writes and does not hold the compute of one stage behind the loads into another.
 //
 // At head_dim <= 128 a workgroup is four waves of 32 query rows (two row groups of 16 MFMA columns): every K and
 // V^T operand read from LDS feeds two matrix products, which halves the LDS reads and the per-step scalar work per
@@ -53,11 +52,20 @@ namespace
 {
 
 constexpr int kDmaRows = 128;  // query rows per workgroup: 8 waves x 16 rows (RG = 1) or 4 waves x 32 rows (RG = 2)
+// LDS stages of the load pipeline (steps in flight behind the computed one, + 1).  At head_dim 128 a step is four
+// pages (64 keys) and two stages hold as many bytes in flight as three of two pages, with half the per-step
+// scalar work, barriers and row reductions per key (C4-shaped prefill: bf16 320 -> 293 us, int8 401 -> 366 us);
+// head_dim 256 (two pages per step) is also faster with two (718 -> 689 us), head_dim 64 is even.
 #ifndef FFKV_PREFILL_STAGES
-#define FFKV_PREFILL_STAGES 3  // LDS stages of the load pipeline: steps in flight behind the computed one, + 1
+#define FFKV_PREFILL_STAGES 2  // head_dim 128 and 256
 #endif
-constexpr int kDmaStages = FFKV_PREFILL_STAGES;
-static_assert(kDmaStages == 3 || kDmaStages == 4, "three or four stages");
+#ifndef FFKV_PREFILL_STAGES64
+#define FFKV_PREFILL_STAGES64 3
+#endif
+template <int D>
+constexpr int kDmaStages = D == 64 ? FFKV_PREFILL_STAGES64 : FFKV_PREFILL_STAGES;
+static_assert(kDmaStages<64> >= 2 && kDmaStages<64> <= 4 && kDmaStages<128> >= 2 && kDmaStages<128> <= 4,
+              "two to four stages");
 constexpr int kXcds = 8;  // MI355X: workgroups are dealt to 8 XCDs (separate L2s) in turn
 
 #ifndef FFKV_PREFILL_XCD
@@ -73,7 +81,7 @@ constexpr int kXcds = 8;  // MI355X: workgroups are dealt to 8 XCDs (separate L2
 #endif
 
 #ifndef FFKV_PREFILL_DMA_KP128
-#define FFKV_PREFILL_DMA_KP128 2  // pages per step at head_dim 128
+#define FFKV_PREFILL_DMA_KP128 4  // pages per step at head_dim 128
 #endif
 
 #define FFKV_LDS __attribute__((address_space(3)))
@@ -223,11 +231,11 @@ void paged_prefill_dma(PrefillArgs a)
     constexpr int  NT = D / 16;
     constexpr bool NEED_LO = !((QT == BF16 && BF) || (QT == F16 && !BF));
 
-    // three (or four) stages, each [K tile | V tile | int8 scales] of KP pages, key-major with swizzled chunks
+    // NS stages (three by default), each [K tile | V tile | int8 scales] of KP pages, key-major, swizzled chunks
     __shared__ __align__(16) uint8_t s_st0[2 * C::TILEB + C::SCB];
     __shared__ __align__(16) uint8_t s_st1[2 * C::TILEB + C::SCB];
-    __shared__ __align__(16) uint8_t s_st2[2 * C::TILEB + C::SCB];
-    __shared__ __align__(16) uint8_t s_st3[kDmaStages == 4 ? 2 * C::TILEB + C::SCB : 16];
+    __shared__ __align__(16) uint8_t s_st2[kDmaStages<D> >= 3 ? 2 * C::TILEB + C::SCB : 16];
+    __shared__ __align__(16) uint8_t s_st3[kDmaStages<D> == 4 ? 2 * C::TILEB + C::SCB : 16];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -739,7 +747,7 @@ void paged_prefill_dma(PrefillArgs a)
     // ---- pipeline: stage si % NS ---------------------------------------------------------------------------
     // Every step issues the same number of loads (steps past the end fetch the zero block into a stage nobody
     // reads), so "step si has landed" is always vmcnt <= the loads of steps si + 1 .. si + NS - 2.
-    constexpr int NS = kDmaStages;
+    constexpr int NS = kDmaStages<D>;
     constexpr int LPS = C::RPW + C::SCB / 256;  // loads per wave and step
     // The scores' products are issued before the next loads' scalar address work, which then runs while they
     // execute.
@@ -754,12 +762,18 @@ void paged_prefill_dma(PrefillArgs a)
     };
 
     int okm0 = issue(0, s_st0);
-    int okm1 = issue(1, s_st1);
-    int okm2 = 0, okm3 = 0;
+    int okm1 = 0, okm2 = 0, okm3 = 0;
+    if constexpr (NS >= 3) okm1 = issue(1, s_st1);
     if constexpr (NS == 4) okm2 = issue(2, s_st2);
     for (int si = 0; si < steps; si += NS)
     {
-        if constexpr (NS == 3)
+        if constexpr (NS == 2)
+        {
+            body(si, s_st0, okm0, s_st1, okm1);
+            if (si + 1 >= steps) break;
+            body(si + 1, s_st1, okm1, s_st0, okm0);
+        }
+        else if constexpr (NS == 3)
         {
             body(si, s_st0, okm0, s_st2, okm2);
             if (si + 1 >= steps) break;
