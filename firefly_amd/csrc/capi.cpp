@@ -83,9 +83,9 @@ int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
 namespace ffkv
 {
 
-bool decode_use_mfma(int cache_dtype, int group)
+bool decode_use_mfma(int cache_dtype, int /*group*/)
 {
-    return !env_force_generic() && cache_dtype != FFKV_DTYPE_F32 && group <= 16;
+    return !env_force_generic() && cache_dtype != FFKV_DTYPE_F32;
 }
 
 // MFMA workspace layout: [row meta: batch x 2 int32 | (m, l): slots x num_heads x 2 fp32 | acc: slots x num_heads
@@ -389,9 +389,12 @@ int decode_impl(const void* q, void* out, int qo_dtype, const void* k_cache, con
         return fail(FFKV_ERR_INVALID_ARGUMENT, "num_heads %d is not a multiple of num_kv_heads %d", num_heads,
                     num_kv_heads);
     const int group = num_heads / num_kv_heads;
-    if (group > 16) return fail(FFKV_ERR_UNSUPPORTED, "GQA group size %d exceeds 16", group);
-    if (batch > 65535 || num_kv_heads > 65535)
-        return fail(FFKV_ERR_UNSUPPORTED, "batch and num_kv_heads must be <= 65535");
+    // the matrix-core decode takes any group (one wave per block of 16 query heads); the fp32-cache kernel 16 at most
+    if (group > 16 && !ffkv::decode_use_mfma(cache_dtype, group))
+        return fail(FFKV_ERR_UNSUPPORTED, "GQA group size %d exceeds 16 (fp32 caches, or the generic decode forced)",
+                    group);
+    if (batch > 65535 || num_heads > 65535)
+        return fail(FFKV_ERR_UNSUPPORTED, "batch and num_heads must be <= 65535");
     if (batch == 0) return ok();
     if (!q || !out || !k_cache || !v_cache || !block_table || !context_lens)
         return fail(FFKV_ERR_INVALID_ARGUMENT, "null q, out, cache, block_table or context_lens pointer");

@@ -3,9 +3,11 @@
 // Reference semantics: paged_attention_kernel (src/kernels/attention.cu:291-447): out[b, h] = softmax over the
 // context_lens[b] + 1 cached tokens of scale * q[b, h] . k_j, applied to v_j, with kv_head = h / (Hq / Hkv).
 //
-// Design (one wave = one KV head of one page range; a page = 16 tokens = one MFMA tile):
+// Design (one wave = one KV head of one page range, or one block of 16 of its query heads when the GQA group is
+// larger; a page = 16 tokens = one MFMA tile):
 //   * QK^T on MFMA: S^T[t, h] = K[t, :] . Q[h, :] with v_mfma_f32_16x16x32_{bf16,f16}; the 16 tokens of a page
-//     are the rows, the (up to 16) query heads of the GQA group the columns.  K is fed straight from its page:
+//     are the rows, (up to) 16 query heads of the GQA group the columns.  Groups over 16 heads take one wave per
+//     block of 16; the blocks of a KV head sit in the same workgroup, so their reads of a page meet in L2.  K is fed straight from its page:
 //     lane (c, g) = (lane % 16, lane / 16) loads token c's 16-byte run at dim 32j + 8g for k-step j, so one load
 //     instruction covers 64 contiguous bytes of each of the 16 tokens.  The reduction over head_dim happens in
 //     the matrix core; no cross-lane dot-product trees.
@@ -32,7 +34,7 @@
 #include "mfma_common.h"
 
 #ifndef FFKV_MFMA_MAX_WAVES
-#define FFKV_MFMA_MAX_WAVES 4  // waves (= KV heads) per workgroup
+#define FFKV_MFMA_MAX_WAVES 4  // waves (KV heads, or blocks of 16 query heads of one) per workgroup
 #endif
 
 namespace ffkv
@@ -222,9 +224,14 @@ void paged_decode_mfma(DecodeArgs a)
     const int start = static_cast<int>(static_cast<int64_t>(item) * P / W);
     const int end = static_cast<int>(static_cast<int64_t>(item + 1) * P / W);
 
-    const int kvh = blockIdx.y * (static_cast<int>(blockDim.x) >> 6) + wave;
-    if (kvh >= a.num_kv_heads) return;
+    // wave -> (KV head, block of 16 of its query heads): heads kvh * G + h0 + c for c < gc
     const int G = a.group;
+    const int HB = (G + 15) >> 4;
+    const int vh = blockIdx.y * (static_cast<int>(blockDim.x) >> 6) + wave;
+    if (vh >= a.num_kv_heads * HB) return;
+    const int kvh = vh / HB;
+    const int h0 = (vh - kvh * HB) * 16;
+    const int gc = min(16, G - h0);  // heads of this block
     uint16_t* sv = s_v[wave];
 
     float kv_scale_log2 = a.scale_log2;
@@ -363,9 +370,9 @@ void paged_decode_mfma(DecodeArgs a)
             {
                 // q is stored in the MFMA input type: its 16 bytes are the operand
                 u32x4 w = u32x4{0u, 0u, 0u, 0u};
-                if (c < G)
+                if (c < gc)
                     w = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.q) +
-                                                        (static_cast<size_t>(b) * a.num_heads + kvh * G + c) * D +
+                                                        (static_cast<size_t>(b) * a.num_heads + kvh * G + h0 + c) * D +
                                                         dim_of<CT>(j, g));
                 qhi[j] = __builtin_bit_cast(X8, w);
                 qlo[j] = qhi[j];
@@ -373,8 +380,9 @@ void paged_decode_mfma(DecodeArgs a)
             else
             {
                 float x[8];
-                if (c < G)
-                    load_q8<QT>(a.q, (static_cast<size_t>(b) * a.num_heads + kvh * G + c) * D + dim_of<CT>(j, g), x);
+                if (c < gc)
+                    load_q8<QT>(a.q, (static_cast<size_t>(b) * a.num_heads + kvh * G + h0 + c) * D + dim_of<CT>(j, g),
+                                x);
                 else
 #pragma unroll
                     for (int e = 0; e < 8; ++e) x[e] = 0.0f;
@@ -412,7 +420,7 @@ void paged_decode_mfma(DecodeArgs a)
     {
         if constexpr (kElemBytes<CT> == 2)
         {
-            if (c == r.ns)  // fused append: write the new token's row into its page slot (what ffkv_append writes)
+            if (c == r.ns && h0 == 0)  // fused append: write the new token's row into its page slot (as ffkv_append)
             {
                 const size_t row_c = (static_cast<size_t>(r.phys) * kBlockSize + c) * a.num_kv_heads + kvh;
                 char*        kp = static_cast<char*>(const_cast<void*>(a.k_cache)) + row_c * D * 2;
@@ -544,10 +552,10 @@ void paged_decode_mfma(DecodeArgs a)
     auto finish_segment = [&](int b, int pb, int nb, int seg_start, int seg_end)
     {
         const float l_tot = xor_sum(l_run);
-        const int   h = kvh * G + c;
+        const int   h = kvh * G + h0 + c;
         if (seg_start == pb && seg_end == pb + nb && a.pfx_chunks == 0)
         {
-            if (c < G)
+            if (c < gc)
             {
                 const float inv = l_tot > 0.0f ? v_head_scale / l_tot : 0.0f;
 #pragma unroll
@@ -556,7 +564,7 @@ void paged_decode_mfma(DecodeArgs a)
                                    acc[n] * inv);
             }
         }
-        else if (c < G)
+        else if (c < gc)
         {
             const int64_t slot = static_cast<int64_t>(item) + b;
             float*        dst = a.ws_acc + (slot * a.num_heads + h) * D;
@@ -732,8 +740,9 @@ template <int CT, int QT, int D>
 hipError_t launch_m3(const DecodeArgs& a0, hipStream_t stream)
 {
     DecodeArgs a = a0;
-    const int  nw = a.num_kv_heads < FFKV_MFMA_MAX_WAVES ? a.num_kv_heads : FFKV_MFMA_MAX_WAVES;
-    const int  gy = (a.num_kv_heads + nw - 1) / nw;
+    const int  vh = a.num_kv_heads * ((a.group + 15) / 16);  // one wave per KV head and block of 16 query heads
+    const int  nw = vh < FFKV_MFMA_MAX_WAVES ? vh : FFKV_MFMA_MAX_WAVES;
+    const int  gy = (vh + nw - 1) / nw;
     const auto kern = paged_decode_mfma<CT, QT, D>;
     const int  items = decode_mfma_items(reinterpret_cast<const void*>(kern), 64 * nw, gy);
     hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(items), static_cast<unsigned>(gy)), dim3(64 * nw), 0, stream, a);

@@ -95,8 +95,9 @@ FFKV_API size_t ffkv_decode_workspace_bytes(int batch, int num_heads, int head_d
  * (include/firefly/kernels.h:83-84, src/kernels/attention.cu:452-493 -> paged_attention_kernel :291-447).
  *
  * qo_dtype (q and out) is F32, F16 or BF16; cache_dtype as for ffkv_append.  scale <= 0 selects
- * 1/sqrt(head_dim) (src/kernels/attention.cu:458).  num_heads must be a multiple of num_kv_heads with a group
- * size of at most 16; head_dim 64, 128 or 256; q, out, cache and workspace pointers 16-byte aligned.  Rows are
+ * 1/sqrt(head_dim) (src/kernels/attention.cu:458).  num_heads must be a multiple of num_kv_heads (any group
+ * size for 16- and 8-bit caches, at most 16 for fp32 caches) and at most 65535; head_dim 64, 128 or 256; q,
+ * out, cache and workspace pointers 16-byte aligned.  Rows are
  * split over the context and the pieces merged; the partials live in `workspace` (ffkv_decode_workspace_bytes;
  * any initial contents), or, when workspace is NULL, in stream-ordered memory the library allocates and frees on
  * `stream`.  Calls sharing one workspace must not overlap in time (use one workspace per stream).  Rows whose
@@ -133,7 +134,7 @@ FFKV_API int ffkv_append_paged_decode(const void* k_new, const void* v_new, int 
  * prefix page, split into chunks of pages), the rest of each row by the decode kernel, and the split-K merge
  * folds both: each shared page is read once per call instead of once per row.  Results equal ffkv_paged_decode
  * on the same inputs up to floating-point summation order (same tolerance).  Rows shorter than the prefix
- * attend only their own tokens.  The split applies to F16/BF16/I8/FP8 caches with group <= 16; fp32 caches run
+ * attend only their own tokens.  The split applies to F16/BF16/I8/FP8 caches; fp32 caches run
  * ffkv_paged_decode unchanged.  No counterpart in the reference, whose decode reads shared blocks once per row
  * (src/kernels/attention.cu:332-335).  Workspace: ffkv_decode_shared_prefix_workspace_bytes, or NULL as for
  * ffkv_paged_decode.

@@ -75,7 +75,8 @@ def test_append_empty_is_ok(ff):
     (dict(head_dim=80), -2),
     (dict(qo_dtype=3), -2),
     (dict(num_heads=30), -1),         # not a multiple of num_kv_heads
-    (dict(num_heads=8 * 17), -2),     # GQA group above 16
+    (dict(num_heads=8 * 17, cache_dtype=0), -2),  # GQA group above 16 on an fp32 cache (the generic kernel)
+    (dict(num_heads=70000 * 2, num_kv_heads=70000), -2),  # more than 65535 query heads
     (dict(context_lens=None), -1),
     (dict(q=None), -1),
     (dict(cache_dtype=3), -1),

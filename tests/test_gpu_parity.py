@@ -79,6 +79,17 @@ def test_head_dim_256_dtypes(ff, gpu, act, kv):
     _check(ff, gpu, c, 2e-3 if kv in ("f16", "bf16") else 2e-2)
 
 
+@pytest.mark.parametrize("G,Hkv,D,act,kv", [(17, 2, 128, "bf16", "bf16"), (32, 1, 128, "bf16", "bf16"),
+                                             (48, 2, 128, "f16", "f16"), (24, 2, 64, "bf16", "fp8"),
+                                             (32, 2, 128, "bf16", "i8"), (20, 1, 256, "f32", "bf16")])
+def test_groups_over_16(ff, gpu, G, Hkv, D, act, kv):
+    """GQA groups above 16 query heads per KV head (MQA-style): one wave per block of 16 heads of the group."""
+    rng = np.random.default_rng(G * 10 + Hkv)
+    ctx = rng.integers(0, 800, size=6)
+    c = cases.make_case(70 + G, 6, G * Hkv, Hkv, D, ctx, act=act, kv=kv, input_scale=1 / math.sqrt(D))
+    _check(ff, gpu, c, 2e-3 if kv in ("f16", "bf16") else 2e-2)
+
+
 def test_config2_full(ff, gpu):
     """BASELINE config 2 at full size: Qwen3-8B layer, B=64, contexts U[512, 4096]."""
     rng = np.random.default_rng(2)

@@ -88,7 +88,7 @@ def test_rows_shorter_than_or_ending_at_the_prefix(ff, gpu):
     _both(ff, gpu, c, 9)
 
 
-@pytest.mark.parametrize("D,G", [(64, 1), (64, 8), (128, 16), (256, 4), (256, 7)])
+@pytest.mark.parametrize("D,G", [(64, 1), (64, 8), (128, 16), (256, 4), (256, 7), (128, 32), (64, 40)])
 def test_head_shapes(ff, gpu, D, G):
     rng = np.random.default_rng(46 + D + G)
     ctx = 160 + rng.integers(0, 300, size=10)
