@@ -1,0 +1,53 @@
+"""Seeded random shapes for the decode (with its append) and the chunked prefill, against the CPU checker, to the
+same bar as the fixed-shape parity tests: pages bit-exact, outputs within 2e-3 (16-bit caches) / 2e-2 (8-bit
+caches) / 1e-4 (fp32 decode) of the checker beyond the output's own rounding.  Each case draws the batch, the GQA
+group (1 .. 40 query heads per KV head), the KV heads, head_dim, the row lengths (empty rows included), the
+chunk length and the dtype pair from a fixed seed, so a failure names a reproducible case."""
+
+import math
+
+import numpy as np
+import pytest
+
+import cases
+from test_gpu_parity import TOL, _check as _decode_check
+from test_gpu_prefill import _case as _prefill_case, _check as _prefill_check, _run as _prefill_run
+
+pytestmark = pytest.mark.gpu
+
+DECODE_PAIRS = [("bf16", "bf16"), ("f16", "f16"), ("f32", "f32"), ("bf16", "i8"), ("bf16", "fp8"), ("f32", "bf16"),
+                ("f16", "i8"), ("f32", "fp8")]
+PREFILL_PAIRS = [("bf16", "bf16"), ("f16", "f16"), ("bf16", "i8"), ("bf16", "fp8"), ("f32", "bf16")]
+GROUPS = [1, 2, 3, 4, 5, 7, 8, 12, 16, 17, 24, 40]
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_decode(ff, gpu, seed):
+    rng = np.random.default_rng(9000 + seed)
+    act, kv = DECODE_PAIRS[seed % len(DECODE_PAIRS)]
+    G = int(rng.choice(GROUPS if kv != "f32" else [g for g in GROUPS if g <= 16]))
+    Hkv = int(rng.choice([1, 2, 4, 8]))
+    D = int(rng.choice([64, 128, 256]))
+    B = int(rng.integers(1, 41))
+    ctx = rng.integers(0, 2000, size=B)
+    ctx[rng.random(B) < 0.1] = 0  # some rows hold only the new token
+    c = cases.make_case(9000 + seed, B, G * Hkv, Hkv, D, ctx, act=act, kv=kv, input_scale=1 / math.sqrt(D))
+    cap = int(rng.integers(64, 2000)) if seed % 4 == 3 else 0  # max_context_len cuts some rows
+    _decode_check(ff, gpu, c, TOL[(act, kv)], max_context_len=cap)
+
+
+@pytest.mark.parametrize("seed", range(10))
+def test_random_prefill(ff, gpu, seed):
+    rng = np.random.default_rng(9500 + seed)
+    act, kv = PREFILL_PAIRS[seed % len(PREFILL_PAIRS)]
+    G = int(rng.choice(GROUPS))
+    Hkv = int(rng.choice([h for h in (1, 2, 4) if G * h <= 48]))
+    D = int(rng.choice([64, 128, 256]))
+    B = int(rng.integers(1, 4))
+    S = int(rng.integers(1, 300))
+    ctx = rng.integers(0, 1500, size=B)
+    # keep the single-threaded float64 checker to the size of the fixed long-chunk case (about 1.5e10 flops)
+    while S > 1 and B * S * G * Hkv * (int(ctx.max()) + S) * D * 4 > 1.5e10:
+        S //= 2
+    c, qn = _prefill_case(9500 + seed, B, G * Hkv, Hkv, D, ctx, S, act=act, kv=kv)
+    _prefill_check(*_prefill_run(ff, gpu, c, qn), c.act, 2e-3 if kv in ("bf16", "f16") else 2e-2)
