@@ -80,6 +80,10 @@ constexpr int kXcds = 8;  // MI355X: workgroups are dealt to 8 XCDs (separate L2
 #define FFKV_PREFILL_RG 2  // row groups of 16 query rows per wave at head_dim <= 128 (head_dim 256 takes 1)
 #endif
 
+#ifndef FFKV_PREFILL_DMA_KP64
+#define FFKV_PREFILL_DMA_KP64 4  // pages per step at head_dim 64
+#endif
+
 #ifndef FFKV_PREFILL_DMA_KP128
 #define FFKV_PREFILL_DMA_KP128 4  // pages per step at head_dim 128
 #endif
@@ -96,7 +100,7 @@ __device__ __align__(16) uint32_t g_zero_chunks[256];
 template <int D, int EB, bool SC, int W>
 struct DmaCfg
 {
-    static constexpr int KP = D == 64 ? 4 : (D == 128 ? FFKV_PREFILL_DMA_KP128 : 2);  // pages per step
+    static constexpr int KP = D == 64 ? FFKV_PREFILL_DMA_KP64 : (D == 128 ? FFKV_PREFILL_DMA_KP128 : 2);  // per step
     static constexpr int RB = D * EB;                  // bytes of one key row (one kv head)
     static constexpr int CPT = RB / 16;                // 16-byte chunks per key row
     static constexpr int CHUNKS = kBlockSize * CPT;    // chunks per page
