@@ -118,14 +118,18 @@ def test_prefill_long_chunk_over_long_prefix(ff, gpu):
     _check(*_run(ff, gpu, c, qn), c.act, 2e-3)
 
 
-def test_prefill_invalid_pages_and_rows_without_keys(ff, gpu):
-    c, qn = _case(500, 4, 8, 2, 128, [40, 0, 64, 20], 9)
+# both load-issue forms of the kernel: per run (bf16 q over a bf16 cache, head_dim 128) and per page (the others)
+@pytest.mark.parametrize("act,kv,D,tol", [("bf16", "bf16", 128, 2e-3), ("f16", "f16", 128, 2e-3),
+                                          ("bf16", "bf16", 64, 2e-3), ("bf16", "bf16", 256, 2e-3),
+                                          ("bf16", "i8", 128, 2e-2), ("f32", "bf16", 128, 2e-3)])
+def test_prefill_invalid_pages_and_rows_without_keys(ff, gpu, act, kv, D, tol):
+    c, qn = _case(500, 4, 8, 2, D, [40, 0, 64, 20], 9, act=act, kv=kv)
     tbl = c.block_table.copy()
     tbl[0, 1] = -1                    # a hole in row 0's prefix
     tbl[2, 0] = c.num_blocks + 5      # out of the pool
     ctx = c.ctx.copy()
     ctx[3] = -30                      # positions -30..-22: no key; the append skips them too
-    _check(*_run(ff, gpu, c, qn, tbl=tbl, ctx=ctx), c.act, 2e-3)
+    _check(*_run(ff, gpu, c, qn, tbl=tbl, ctx=ctx), c.act, tol)
 
 
 def test_prefill_shared_prefix_pages(ff, gpu):
@@ -136,6 +140,13 @@ def test_prefill_shared_prefix_pages(ff, gpu):
 @pytest.mark.parametrize("S", [5, 64, 200])
 def test_prefill_contiguous_mode_is_reference_causal_prefill(ff, gpu, S):
     c, qn = _case(700 + S, 2, 28, 4, 128, [0, 0], S)
+    _check(*_run(ff, gpu, c, qn, contiguous=True), c.act, 2e-3)
+
+
+@pytest.mark.parametrize("act,D", [("f16", 128), ("bf16", 64), ("bf16", 256), ("f16", 64)])
+def test_prefill_contiguous_mode_head_dims(ff, gpu, act, D):
+    """The contiguous mode (row offsets instead of a block table) through the per-page load issue."""
+    c, qn = _case(760 + D, 3, 8, 2, D, [0, 0, 0], 83, act=act)
     _check(*_run(ff, gpu, c, qn, contiguous=True), c.act, 2e-3)
 
 
