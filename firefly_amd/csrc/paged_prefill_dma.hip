@@ -88,6 +88,10 @@ constexpr int kXcds = 8;  // MI355X: workgroups are dealt to 8 XCDs (separate L2
 #define FFKV_PREFILL_DMA_KP128 4  // pages per step at head_dim 128
 #endif
 
+#ifndef FFKV_PREFILL_DMA_KP256
+#define FFKV_PREFILL_DMA_KP256 4  // pages per step at head_dim 256 (the shared-prefix partials take 2)
+#endif
+
 #define FFKV_LDS __attribute__((address_space(3)))
 
 using i32x2 = int __attribute__((ext_vector_type(2)));
@@ -96,11 +100,13 @@ using i32x2 = int __attribute__((ext_vector_type(2)));
 // Source of the chunks of keys that are not loaded: 64 lanes x 16 bytes of zeros (never written).
 __device__ __align__(16) uint32_t g_zero_chunks[256];
 
-// EB: bytes per cached element (2, or 1 for int8 / fp8 codes); SC: int8 scales; W: waves per workgroup
-template <int D, int EB, bool SC, int W>
+// EB: bytes per cached element (2, or 1 for int8 / fp8 codes); SC: int8 scales; W: waves per workgroup; PFX:
+// shared-prefix partials, whose head_dim 256 f16 variant spills registers at 4 pages per step
+template <int D, int EB, bool SC, int W, bool PFX>
 struct DmaCfg
 {
-    static constexpr int KP = D == 64 ? FFKV_PREFILL_DMA_KP64 : (D == 128 ? FFKV_PREFILL_DMA_KP128 : 2);  // per step
+    static constexpr int KP = D == 64 ? FFKV_PREFILL_DMA_KP64
+                                      : (D == 128 ? FFKV_PREFILL_DMA_KP128 : (PFX ? 2 : FFKV_PREFILL_DMA_KP256));
     static constexpr int RB = D * EB;                  // bytes of one key row (one kv head)
     static constexpr int CPT = RB / 16;                // 16-byte chunks per key row
     static constexpr int CHUNKS = kBlockSize * CPT;    // chunks per page
@@ -230,7 +236,7 @@ void paged_prefill_dma(PrefillArgs a)
     constexpr bool Q8 = EB == 1;
     // int8 codes take bf16 MFMAs beside a bf16 q (exact: 8 significant bits), so q needs no hi / lo split
     constexpr bool BF = CT == I8 ? (FFKV_PREFILL_I8_BF && QT != F16) : kBF<CT, QT>;
-    using C = DmaCfg<D, EB, CT == I8, W>;  // the scale bytes (and their loads, counted in the waits) only for int8
+    using C = DmaCfg<D, EB, CT == I8, W, PFX>;  // the scale bytes (and their loads, counted in the waits) only for int8
     using M = MType<BF>;
     using X8 = typename M::x8;
     constexpr int  KP = C::KP;
