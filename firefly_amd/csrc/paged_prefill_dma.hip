@@ -262,7 +262,9 @@ void paged_prefill_dma(PrefillArgs a)
     const int g = lane >> 4;
     // Workgroup -> (group, row block).  A group is (row b, kv head) for prefill and (kv head, chunk of prefix
     // pages) for prefix partials.  Consecutive workgroups go to the eight XCDs in turn; every row block of one
-    // group is given to the same XCD, so the group's pages are fetched into one L2, not eight.
+    // group is given to the same XCD, so the group's pages are fetched into one L2, not eight.  A group's row
+    // blocks are dealt last first: the later prefill tokens see the most keys, and starting the longest work
+    // first shortens the tail (1-3 % on an 8 x 512-token chunk).
     const int G = a.group;
     const int S = a.seq_len;
     const int Hq = a.num_heads;
@@ -275,7 +277,7 @@ void paged_prefill_dma(PrefillArgs a)
     const int xcd = wg % kXcds;
     const int k_in_xcd = wg / kXcds;
     const int grp = (k_in_xcd / nrb) * kXcds + xcd;
-    const int rb = k_in_xcd % nrb;
+    const int rb = nrb - 1 - k_in_xcd % nrb;
     if (grp >= groups) return;  // padding of the grid to whole rounds of XCDs
 #else
     const int grp = blockIdx.x / nrb;
