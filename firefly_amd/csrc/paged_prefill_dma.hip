@@ -262,9 +262,9 @@ void paged_prefill_dma(PrefillArgs a)
     const int g = lane >> 4;
     // Workgroup -> (group, row block).  A group is (row b, kv head) for prefill and (kv head, chunk of prefix
     // pages) for prefix partials.  Consecutive workgroups go to the eight XCDs in turn; every row block of one
-    // group is given to the same XCD, so the group's pages are fetched into one L2, not eight.  A group's row
-    // blocks are dealt last first: the later prefill tokens see the most keys, and starting the longest work
-    // first shortens the tail (1-3 % on an 8 x 512-token chunk).
+    // group is given to the same XCD, so the group's pages are fetched into one L2, not eight.  The longest work
+    // goes out first, which shortens the tail (2-5 % on an 8 x 512-token chunk): an XCD's groups by decreasing
+    // cached length, and a group's row blocks last first (the later prefill tokens see the most keys).
     const int G = a.group;
     const int S = a.seq_len;
     const int Hq = a.num_heads;
@@ -276,8 +276,24 @@ void paged_prefill_dma(PrefillArgs a)
     const int wg = blockIdx.x;
     const int xcd = wg % kXcds;
     const int k_in_xcd = wg / kXcds;
-    const int grp = (k_in_xcd / nrb) * kXcds + xcd;
     const int rb = nrb - 1 - k_in_xcd % nrb;
+    int       grp = (k_in_xcd / nrb) * kXcds + xcd;
+    const int g8 = (groups + kXcds - 1) / kXcds;  // group slots of this XCD: groups j * kXcds + xcd, j < g8
+    if (!PFX && a.paged && g8 <= 64 && g8 > 1)
+    {
+        // The XCD's groups by decreasing cached length (ties by index): lane j ranks group j * kXcds + xcd, and
+        // the workgroup takes the group ranked k_in_xcd / nrb.  Absent groups (past `groups`) rank last.
+        const int gl = lane * kXcds + xcd;
+        const int wl = lane < g8 && gl < groups ? a.context_lens[gl / a.num_kv_heads] : -2147483647 - 1;
+        int       rank = 0;
+        for (int m = 0; m < g8; ++m)
+        {
+            const int wm = __builtin_amdgcn_readlane(wl, m);
+            rank += (wm > wl || (wm == wl && m < lane)) ? 1 : 0;
+        }
+        const uint64_t hit = __ballot(lane < g8 && rank == k_in_xcd / nrb);
+        grp = hit != 0 ? (__ffsll(static_cast<long long>(hit)) - 1) * kXcds + xcd : groups;
+    }
     if (grp >= groups) return;  // padding of the grid to whole rounds of XCDs
 #else
     const int grp = blockIdx.x / nrb;

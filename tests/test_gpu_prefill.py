@@ -132,6 +132,18 @@ def test_prefill_invalid_pages_and_rows_without_keys(ff, gpu, act, kv, D, tol):
     _check(*_run(ff, gpu, c, qn, tbl=tbl, ctx=ctx), c.act, tol)
 
 
+@pytest.mark.parametrize("B,Hkv", [(40, 2), (130, 4)])
+def test_prefill_many_rows_ordered_by_length(ff, gpu, B, Hkv):
+    """Many (row, kv head) groups with repeated and negative cached lengths: each XCD takes its groups longest
+    first (ties by index), or in index order past 64 groups per XCD (B = 130, Hkv = 4)."""
+    rng = np.random.default_rng(950 + B)
+    ctx = rng.choice([0, 17, 17, 64, 90, 90, 150], size=B).astype(np.int32)
+    c, qn = _case(950 + B, B, 2 * Hkv, Hkv, 128, ctx, 5)
+    ctx2 = c.ctx.copy()
+    ctx2[1] = -7  # no key for the first positions of row 1
+    _check(*_run(ff, gpu, c, qn, ctx=ctx2), c.act, 2e-3)
+
+
 def test_prefill_shared_prefix_pages(ff, gpu):
     c, qn = _case(600, 4, 32, 8, 128, [64, 64, 80, 100], 12, shared=4)
     _check(*_run(ff, gpu, c, qn), c.act, 2e-3)
