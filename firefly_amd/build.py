@@ -74,7 +74,8 @@ def build_library(jobs: int = 8) -> Path:
 
 def build_test_shims() -> None:
     """Test-only helpers linked against libffkv.so: the C++-API shims under tests/cpp/ (kernels_api_shim.cpp for
-    tests/test_gpu_cxx_api.py, decode_step_shim.cpp for tests/test_gpu_decode_step.py)."""
+    tests/test_gpu_cxx_api.py, decode_step_shim.cpp for tests/test_gpu_decode_step.py) and engine_calls.bin
+    (tests/test_hal.py)."""
     for name in ("kernels_api_shim", "decode_step_shim"):
         src = ROOT / "tests" / "cpp" / f"{name}.cpp"
         if not src.exists():
@@ -85,6 +86,14 @@ def build_test_shims() -> None:
         res = subprocess.run(cmd, capture_output=True, text=True)
         if res.returncode != 0:
             raise RuntimeError(f"test shim build failed: {' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
+    # the reference engine's hal::Graph / hal::Result call shapes as an executable (tests/test_hal.py)
+    src = ROOT / "tests" / "cpp" / "engine_calls.cpp"
+    out = ROOT / "tests" / "cpp" / "engine_calls.bin"
+    cmd = [HIPCC, "-O1", "-std=c++20", f"-I{ROOT / 'include'}", str(src), "-o", str(out), f"-L{PKG}", "-lffkv",
+           "-Wl,-rpath,$ORIGIN/../../firefly_amd"]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"test executable build failed: {' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
 
 
 def build_oracle() -> None:

@@ -9,6 +9,8 @@
 
 #include <algorithm>
 #include <cstring>
+#include <string>
+#include <utility>
 
 #include "firefly/hal/graph.h"
 
@@ -98,7 +100,7 @@ namespace hal
 
 Graph::~Graph() { destroy(); }
 
-Graph::Graph(Graph&& other) noexcept : graph_(other.graph_), exec_(other.exec_), error_(std::move(other.error_))
+Graph::Graph(Graph&& other) noexcept : graph_(other.graph_), exec_(other.exec_)
 {
     other.graph_ = nullptr;
     other.exec_ = nullptr;
@@ -109,11 +111,8 @@ Graph& Graph::operator=(Graph&& other) noexcept
     if (this != &other)
     {
         destroy();
-        graph_ = other.graph_;
-        exec_ = other.exec_;
-        error_ = std::move(other.error_);
-        other.graph_ = nullptr;
-        other.exec_ = nullptr;
+        graph_ = std::exchange(other.graph_, nullptr);
+        exec_ = std::exchange(other.exec_, nullptr);
     }
     return *this;
 }
@@ -126,65 +125,57 @@ void Graph::destroy()
     graph_ = nullptr;
 }
 
-bool Graph::capture(hipStream_t stream, const std::function<void()>& fn)
+namespace
+{
+Status hip_error(hipError_t e, const char* what) { return unexpected(Error{e, what}); }
+Status runtime_error(std::string msg) { return unexpected(Error{-1, ErrorCategory::Runtime, msg}); }
+}  // namespace
+
+Status Graph::capture(hipStream_t stream, std::function<void()> func)
 {
     destroy();
-    error_.clear();
     hipError_t e = hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal);
-    if (e != hipSuccess)
-    {
-        error_ = std::string("hipStreamBeginCapture: ") + hipGetErrorString(e);
-        return false;
-    }
+    if (e != hipSuccess) return hip_error(e, "hipStreamBeginCapture");
+    // fn may throw: the capture is ended (and its partial graph dropped) before the error is returned
+    std::string thrown;
     try
     {
-        fn();
+        func();
     }
     catch (const std::exception& ex)
     {
-        (void)hipStreamEndCapture(stream, &graph_);
-        destroy();
-        error_ = std::string("exception during graph capture: ") + ex.what();
-        return false;
+        thrown = std::string("exception during graph capture: ") + ex.what();
     }
     catch (...)
     {
-        (void)hipStreamEndCapture(stream, &graph_);
-        destroy();
-        error_ = "unknown exception during graph capture";
-        return false;
+        thrown = "unknown exception during graph capture";
     }
     e = hipStreamEndCapture(stream, &graph_);
+    if (!thrown.empty())
+    {
+        destroy();
+        return runtime_error(thrown);
+    }
     if (e != hipSuccess)
     {
         destroy();
-        error_ = std::string("hipStreamEndCapture: ") + hipGetErrorString(e);
-        return false;
+        return hip_error(e, "hipStreamEndCapture");
     }
     e = hipGraphInstantiate(&exec_, graph_, nullptr, nullptr, 0);
     if (e != hipSuccess)
     {
         destroy();
-        error_ = std::string("hipGraphInstantiate: ") + hipGetErrorString(e);
-        return false;
+        return hip_error(e, "hipGraphInstantiate");
     }
-    return true;
+    return {};
 }
 
-bool Graph::launch(hipStream_t stream) const
+Status Graph::launch(hipStream_t stream) const
 {
-    if (!exec_)
-    {
-        error_ = "Graph: nothing captured";
-        return false;
-    }
+    if (!exec_) return runtime_error("Graph: nothing captured to launch");
     const hipError_t e = hipGraphLaunch(exec_, stream);
-    if (e != hipSuccess)
-    {
-        error_ = std::string("hipGraphLaunch: ") + hipGetErrorString(e);
-        return false;
-    }
-    return true;
+    if (e != hipSuccess) return hip_error(e, "hipGraphLaunch");
+    return {};
 }
 
 }  // namespace hal

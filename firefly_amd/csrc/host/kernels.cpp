@@ -3,11 +3,17 @@
 // Shapes and conventions follow the reference dispatcher (src/kernels/attention.cu:452-493): batch = q.shape[0],
 // num_heads = q.shape[2], head_dim = q.shape[3], scale = 1/sqrt(head_dim), the block-table row stride is the
 // max_context_blocks argument, and the launch goes to the thread's default stream.  The decode workspace (split
-// partial results) is cached per thread and grown outside of stream capture; while a stream is being captured a
-// missing or too-small workspace makes the library allocate stream-ordered memory inside the graph instead.
+// partial results) is cached per (thread, device, stream) and grown outside of stream capture; while a stream is
+// being captured a missing or too-small workspace makes the library allocate stream-ordered memory inside the graph
+// instead.
 #include <hip/hip_runtime_api.h>
 
+#include <algorithm>
 #include <iostream>
+#include <map>
+#include <mutex>
+#include <utility>
+#include <vector>
 
 #include "ffkv.h"
 #include "firefly/kernels.h"
@@ -20,14 +26,6 @@ namespace
 
 thread_local hipStream_t t_stream = nullptr;
 thread_local std::string t_error;
-
-struct Workspace
-{
-    void*  ptr = nullptr;
-    size_t bytes = 0;
-    int    device = -1;
-};
-thread_local Workspace t_ws;
 
 void report(int rc, const char* what)
 {
@@ -46,16 +44,34 @@ void fail(const std::string& msg)
     std::cerr << msg << std::endl;
 }
 
-// A workspace of at least `bytes` for the current device, or nullptr while the default stream is capturing and
-// the cached one is too small.
+// Decode workspaces (split-K partials), one per (thread, device, stream): calls on different streams never share
+// one, so a graph replayed on one stream does not race with eager calls on another.  A workspace that must grow is
+// replaced by a larger one (at least twice the size) and the old buffer is retired, never freed: a graph captured
+// while it was current has its address baked in and may still be replayed.  Retired buffers are therefore held
+// until the process ends; the geometric growth keeps them smaller in total than the live one.  Nothing here
+// synchronizes the device.
+struct Workspace
+{
+    void*  ptr = nullptr;
+    size_t bytes = 0;
+};
+thread_local std::map<std::pair<int, hipStream_t>, Workspace> t_ws;
+
+std::mutex         g_retired_mu;
+std::vector<void*> g_retired;  // never freed (see above)
+
+// A workspace of at least `bytes` for the current device and the default stream, or nullptr while that stream is
+// being captured and its workspace is too small (the library then allocates stream-ordered memory inside the
+// graph instead; allocating here would be an unsafe call during capture).
 void* workspace(size_t bytes, size_t& have)
 {
     int dev = 0;
     (void)hipGetDevice(&dev);
-    if (t_ws.ptr != nullptr && t_ws.device == dev && t_ws.bytes >= bytes)
+    Workspace& ws = t_ws[{dev, t_stream}];
+    if (ws.ptr != nullptr && ws.bytes >= bytes)
     {
-        have = t_ws.bytes;
-        return t_ws.ptr;
+        have = ws.bytes;
+        return ws.ptr;
     }
     hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
     if (hipStreamIsCapturing(t_stream, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone)
@@ -63,24 +79,20 @@ void* workspace(size_t bytes, size_t& have)
         have = 0;
         return nullptr;
     }
-    if (t_ws.ptr != nullptr)
-    {
-        int cur = 0;
-        (void)hipGetDevice(&cur);
-        (void)hipSetDevice(t_ws.device);
-        (void)hipDeviceSynchronize();
-        (void)hipFree(t_ws.ptr);
-        (void)hipSetDevice(cur);
-        t_ws = Workspace{};
-    }
-    void* p = nullptr;
-    if (hipMalloc(&p, bytes) != hipSuccess)
+    const size_t grow = std::max(bytes, 2 * ws.bytes);
+    void*        p = nullptr;
+    if (hipMalloc(&p, grow) != hipSuccess)
     {
         have = 0;
         return nullptr;
     }
-    t_ws = Workspace{p, bytes, dev};
-    have = bytes;
+    if (ws.ptr != nullptr)
+    {
+        std::lock_guard<std::mutex> lock(g_retired_mu);
+        g_retired.push_back(ws.ptr);
+    }
+    ws = Workspace{p, grow};
+    have = grow;
     return p;
 }
 

@@ -1,14 +1,17 @@
 // scheduler.cpp - block allocator and continuous-batching scheduler (the producers of KV block tables).
 //
-// Behaviour follows the reference (src/scheduler.cc) where it determines block ids and context lengths:
+// The block ids and context lengths it produces follow the reference (src/scheduler.cc):
 //   BlockAllocator   LIFO free list seeded 0..N-1 (:13-21), eviction from the prefix cache on shortage (:26-36),
 //                    blocks handed out from the back of the list (:38-42), freed blocks pushed back (:46-52)
 //   add_request      prefix match -> block_table / context_len / radix_nodes (:66-74)
-//   step             active requests get one more block when their tokens fill the last (:88-112); pending
-//                    requests, longest cached prefix first (stable sort), are admitted while a slot and the blocks
-//                    for their next prefill chunk are available (:114-160), a fully cached prompt giving back its
-//                    last matched node so at least one token is computed (:124-133)
+//   step             running requests gain the blocks their next step writes (:88-112 under
+//                    PrefillBlocks::OnePerStep); pending requests, longest cached prefix first (stable sort), are
+//                    admitted while a batch slot and the blocks of their first chunk are free (:114-160), a fully
+//                    cached prompt giving back its last matched node so at least one token is computed (:124-133)
 //   finish_request   release prefix references, insert prompt + generated tokens with the block table (:165-186)
+// Under the default PrefillBlocks::PerChunk a request part-way through its prompt gains all the blocks of its next
+// chunk before it runs; the reference gives it one block per step, which leaves later chunks of a long prompt
+// without blocks for their tokens.
 #include <algorithm>
 #include <iostream>
 
@@ -52,11 +55,13 @@ int BlockAllocator::get_free_blocks() const { return static_cast<int>(free_list_
 
 Scheduler::Scheduler() = default;
 
-void Scheduler::init(int max_context_blocks, int max_batch_size_limit, int max_prefill_chunk_size)
+void Scheduler::init(int max_context_blocks, int max_batch_size_limit, int max_prefill_chunk_size,
+                     PrefillBlocks prefill_blocks)
 {
     std::lock_guard<std::mutex> lock(mutex_);
     max_batch_ = max_batch_size_limit;
     max_chunk_ = max_prefill_chunk_size;
+    prefill_blocks_ = prefill_blocks;
     tree_ = std::make_unique<RadixTree>(&allocator_);
     allocator_.init(max_context_blocks, tree_.get());
 }
@@ -83,65 +88,76 @@ int Scheduler::free_blocks()
     return allocator_.get_free_blocks();
 }
 
+// KV positions the request's next step leaves in the cache: the next prefill chunk's end, or, once decoding, its
+// whole sequence (the step appends the newest token at context_len = total - 1).
+int Scheduler::step_tokens(const GenerationRequest& r) const
+{
+    if (!r.generated_tokens.empty()) return r.get_total_len();
+    const int left = static_cast<int>(r.prompt_tokens.size()) - r.context_len;
+    return r.context_len + std::min(left, max_chunk_);
+}
+
+// Blocks a running request must gain before its next step.  Decoding requests (and, under OnePerStep, prefilling
+// ones too) gain one block when their sequence has reached the end of the blocks they hold; under PerChunk a
+// prefilling request gains every block its next chunk writes.
+int Scheduler::blocks_to_run(const GenerationRequest& r) const
+{
+    const int have = static_cast<int>(r.block_table.size());
+    if (prefill_blocks_ == PrefillBlocks::PerChunk && r.generated_tokens.empty())
+        return std::max(0, (step_tokens(r) + block_size_ - 1) / block_size_ - have);
+    return r.get_total_len() >= have * block_size_ ? 1 : 0;
+}
+
+// Appends `blocks` new blocks to r's table (evicting from the prefix cache if the allocator must); false, and no
+// change, if they cannot be had.
+bool Scheduler::reserve(GenerationRequest& r, int blocks)
+{
+    if (blocks <= 0) return true;
+    return allocator_.allocate(blocks, r.block_table);
+}
+
+// A prompt found whole in the prefix cache still needs one forward pass for its logits: give back the last
+// matched node so that its tokens are computed again.
+void Scheduler::uncache_last_node(GenerationRequest& r)
+{
+    const std::shared_ptr<TreeNode> node = r.radix_nodes.back();
+    r.radix_nodes.pop_back();
+    r.context_len -= static_cast<int>(node->tokens.size());
+    r.block_table.resize(r.block_table.size() - node->block_indices.size());
+    node->ref_count--;
+}
+
+// Admission of a pending request: a free batch slot and the blocks of its first chunk, both available now.
+bool Scheduler::admit(GenerationRequest& r)
+{
+    if (r.context_len == static_cast<int>(r.prompt_tokens.size()) && !r.radix_nodes.empty()) uncache_last_node(r);
+    const int need = (step_tokens(r) + block_size_ - 1) / block_size_ - static_cast<int>(r.block_table.size());
+    if (static_cast<int>(active_.size()) >= max_batch_ || need > allocator_.get_free_blocks()) return false;
+    if (!reserve(r, need)) return false;
+    r.status = RequestStatus::ACTIVE;
+    return true;
+}
+
 SchedulerBatch Scheduler::step()
 {
     std::lock_guard<std::mutex> lock(mutex_);
     SchedulerBatch              batch;
 
-    // running requests: a new block once the tokens so far fill every block they have
-    for (const RequestPtr& req : active_)
+    // Running requests first, in arrival order; one whose blocks cannot be had sits this step out.
+    for (const RequestPtr& r : active_)
     {
-        const size_t have = req->block_table.size();
-        if (static_cast<size_t>(req->get_total_len()) < have * static_cast<size_t>(block_size_))
-        {
-            batch.requests.push_back(req);
-            continue;
-        }
-        std::vector<int> one;
-        if (allocator_.allocate(1, one))
-        {
-            req->block_table.push_back(one.front());
-            batch.requests.push_back(req);
-        }
+        if (reserve(*r, blocks_to_run(*r)))
+            batch.requests.push_back(r);
         else
-        {
-            std::cerr << "[Warning] Out of memory during continuous batching decode!" << std::endl;
-        }
+            std::cerr << "firefly::Scheduler: request " << r->id << " waits for a free KV block this step" << std::endl;
     }
 
-    // waiting requests, longest cached prefix first
+    // Then waiting requests, longest cached prefix first (a stable order among equals), until one does not fit.
     pending_.sort([](const RequestPtr& x, const RequestPtr& y) { return x->context_len > y->context_len; });
-    for (auto it = pending_.begin(); it != pending_.end();)
+    while (!pending_.empty() && admit(*pending_.front()))
     {
-        const RequestPtr req = *it;
-        int unmatched = static_cast<int>(req->prompt_tokens.size()) - req->context_len;
-        if (unmatched == 0 && !req->radix_nodes.empty())
-        {
-            // fully cached prompt: recompute its last node so the model produces logits
-            const std::shared_ptr<TreeNode> last = req->radix_nodes.back();
-            req->context_len -= static_cast<int>(last->tokens.size());
-            req->block_table.resize(req->block_table.size() - last->block_indices.size());
-            last->ref_count--;
-            req->radix_nodes.pop_back();
-            unmatched = static_cast<int>(req->prompt_tokens.size()) - req->context_len;
-        }
-        const int chunk = std::min(unmatched, max_chunk_);
-        const int target = req->context_len + chunk;
-        const int needed = (target + block_size_ - 1) / block_size_ - static_cast<int>(req->block_table.size());
-        if (static_cast<int>(active_.size()) < max_batch_ && needed <= allocator_.get_free_blocks())
-        {
-            std::vector<int> got;
-            if (needed == 0 || allocator_.allocate(needed, got))
-            {
-                req->block_table.insert(req->block_table.end(), got.begin(), got.end());
-                req->status = RequestStatus::ACTIVE;
-                active_.push_back(req);
-                batch.requests.push_back(req);
-                it = pending_.erase(it);
-                continue;
-            }
-        }
-        break;  // no room for this request's next chunk: stop admitting
+        batch.requests.push_back(pending_.front());
+        active_.splice(active_.end(), pending_, pending_.begin());
     }
     return batch;
 }
@@ -149,15 +165,17 @@ SchedulerBatch Scheduler::step()
 void Scheduler::finish_request(RequestPtr req)
 {
     std::lock_guard<std::mutex> lock(mutex_);
+    active_.remove(req);
     req->status = RequestStatus::FINISHED;
+    // hand the whole sequence and its blocks to the prefix cache, which owns the blocks from now on
     tree_->decrement_ref_counts(req->radix_nodes);
     req->radix_nodes.clear();
-    std::vector<int> all = req->prompt_tokens;
-    all.insert(all.end(), req->generated_tokens.begin(), req->generated_tokens.end());
-    tree_->insert(all, req->block_table);
-    req->block_table.clear();  // the prefix cache owns the blocks from now on
-    auto it = std::find(active_.begin(), active_.end(), req);
-    if (it != active_.end()) active_.erase(it);
+    std::vector<int> sequence;
+    sequence.reserve(req->prompt_tokens.size() + req->generated_tokens.size());
+    sequence.insert(sequence.end(), req->prompt_tokens.begin(), req->prompt_tokens.end());
+    sequence.insert(sequence.end(), req->generated_tokens.begin(), req->generated_tokens.end());
+    tree_->insert(sequence, req->block_table);
+    req->block_table.clear();
 }
 
 }  // namespace firefly

@@ -1,8 +1,10 @@
-// graph.h - HIP graph capture of a decode step (reference include/firefly/hal/graph.h:54-88).
+// graph.h - HIP graph capture of a decode step (reference include/firefly/hal/graph.h:17-158).
 //
-// Same use as the reference's hal::Graph: capture(stream, fn) records everything fn launches on `stream`
-// (thread-local capture mode, as the reference uses at :59), instantiates it, and launch(stream) replays it.  The
-// reference returns Result<void>; here capture/launch return true on success and error() holds the message.
+// Same interface as the reference's hal::Graph: capture(stream, fn) records everything fn launches on `stream`
+// (thread-local capture mode, as the reference uses at :59) and instantiates it; launch(stream) replays it; both
+// return Status (Result<void>) whose error() describes a failure; empty() is true while nothing is captured.  An
+// exception thrown by fn ends the capture and is returned as a Runtime error.
+//
 // The path's kernels are capture-safe: no host synchronization, no allocation when a decode workspace is given,
 // and no memset nodes (graph replays of memset nodes are avoided on purpose).
 #pragma once
@@ -10,8 +12,8 @@
 #include <hip/hip_runtime_api.h>
 
 #include <functional>
-#include <string>
 
+#include "firefly/hal/error.h"
 #include "firefly/types.h"
 
 namespace firefly::hal
@@ -27,17 +29,15 @@ public:
     Graph(const Graph&) = delete;
     Graph& operator=(const Graph&) = delete;
 
-    bool               capture(hipStream_t stream, const std::function<void()>& fn);
-    bool               launch(hipStream_t stream) const;
-    bool               captured() const { return exec_ != nullptr; }
-    const std::string& error() const { return error_; }
+    Status capture(hipStream_t stream, std::function<void()> func);
+    Status launch(hipStream_t stream) const;
+    [[nodiscard]] bool empty() const { return exec_ == nullptr; }
 
 private:
     void destroy();
 
-    hipGraph_t          graph_ = nullptr;
-    hipGraphExec_t      exec_ = nullptr;
-    mutable std::string error_;
+    hipGraph_t     graph_ = nullptr;
+    hipGraphExec_t exec_ = nullptr;
 };
 
 }  // namespace firefly::hal

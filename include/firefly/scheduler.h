@@ -5,11 +5,13 @@
 //                   on shortage it asks the radix tree to evict first.  Not internally locked (the scheduler
 //                   holds its mutex around every use).
 //   Scheduler       add_request() matches the prompt against the prefix cache (shared blocks, context_len);
-//                   step() gives active requests a new block when their tokens fill the last one and admits
-//                   pending requests (longest cached prefix first) with blocks for their next prefill chunk;
-//                   finish_request() returns the sequence and its blocks to the prefix cache.
+//                   step() gives running requests the blocks their next step writes and admits pending requests
+//                   (longest cached prefix first) with blocks for their first prefill chunk; finish_request()
+//                   returns the sequence and its blocks to the prefix cache.  PrefillBlocks selects how later
+//                   prefill chunks are sized (the reference under-sizes them).
 #pragma once
 
+#include <cstdint>
 #include <list>
 #include <memory>
 #include <mutex>
@@ -44,13 +46,26 @@ struct SchedulerBatch
     std::vector<RequestPtr> requests;
 };
 
+// How a request that is part-way through its prompt gets the blocks of its next prefill chunk.
+enum class PrefillBlocks : uint8_t
+{
+    // Before each chunk runs, the request holds a block for every position the chunk writes.  Default.
+    PerChunk,
+    // The reference's rule (src/scheduler.cc:88-99,137-149): only the admitting chunk is sized; afterwards a
+    // running request gains at most one block per step, so with chunk C a prompt longer than C + 16 tokens runs
+    // later chunks past the end of its block table (their K/V are not stored and their keys are not attended).
+    // Kept for block-id compatibility with the reference.
+    OnePerStep,
+};
+
 class FIREFLY_API Scheduler
 {
 public:
     Scheduler();
     // max_context_blocks: pool size in blocks; max_batch_size_limit: cap on active requests;
-    // max_prefill_chunk_size: tokens a pending request may prefill in one step.
-    void init(int max_context_blocks, int max_batch_size_limit, int max_prefill_chunk_size);
+    // max_prefill_chunk_size: tokens a request may prefill in one step.
+    void init(int max_context_blocks, int max_batch_size_limit, int max_prefill_chunk_size,
+              PrefillBlocks prefill_blocks = PrefillBlocks::PerChunk);
 
     void add_request(RequestPtr req);
     SchedulerBatch step();
@@ -61,6 +76,12 @@ public:
     int free_blocks();
 
 private:
+    int  step_tokens(const GenerationRequest& r) const;
+    int  blocks_to_run(const GenerationRequest& r) const;
+    bool reserve(GenerationRequest& r, int blocks);
+    void uncache_last_node(GenerationRequest& r);
+    bool admit(GenerationRequest& r);
+
     std::mutex            mutex_;
     std::list<RequestPtr> pending_;
     std::list<RequestPtr> active_;
@@ -70,6 +91,7 @@ private:
     int                        block_size_ = 16;
     int                        max_batch_ = 64;
     int                        max_chunk_ = 256;
+    PrefillBlocks              prefill_blocks_ = PrefillBlocks::PerChunk;
 };
 
 }  // namespace firefly

@@ -288,6 +288,52 @@ static void append_one(const void* src, int sdt, void* cache, int cdt, float* sc
     }
 }
 
+typedef struct
+{
+    const void *k_src, *v_src;
+    void *      k_cache, *v_cache;
+    float *     k_scale, *v_scale;
+    const int32_t* block_table;
+    const int32_t* context_lens;
+    int src_dtype, cache_dtype, batch, seq_len, num_kv_heads, head_dim, max_blocks, num_blocks;
+    int h0, h1; /* kv heads of this worker */
+} append_job;
+
+/* Heads h0 .. h1-1 of every token.  Each head owns disjoint bytes of the pages and its own int8 scales, so
+ * workers over disjoint head ranges write disjoint memory, and within a head the (b, t) order is the serial one
+ * (the last writer of a slot shared by two rows' tables wins, as in a serial run). */
+static void* append_worker(void* arg)
+{
+    const append_job* j = (const append_job*)arg;
+    float*            tmp = (float*)malloc(sizeof(float) * (size_t)j->head_dim);
+    int8_t*           qtmp = (int8_t*)malloc((size_t)j->head_dim);
+    for (int b = 0; b < j->batch; ++b)
+    {
+        int ctx0 = j->context_lens ? j->context_lens[b] : 0; /* qwen_model.cu:32 */
+        for (int t = 0; t < j->seq_len; ++t)
+        {
+            long long pos = (long long)ctx0 + t; /* :33 */
+            if (pos < 0) continue;
+            long long blk = pos / 16, off = pos % 16; /* :34-35 */
+            if (blk >= j->max_blocks) continue;
+            int phys = j->block_table[(size_t)b * (size_t)j->max_blocks + (size_t)blk]; /* :37 */
+            if (phys < 0 || phys >= j->num_blocks) continue;
+            for (int h = j->h0; h < j->h1; ++h)
+            {
+                size_t src_row = ((size_t)b * j->seq_len + t) * j->num_kv_heads + h;                /* :39 */
+                size_t dst_row = ((size_t)phys * 16 + (size_t)off) * j->num_kv_heads + (size_t)h; /* :41-42 */
+                append_one(j->k_src, j->src_dtype, j->k_cache, j->cache_dtype, j->k_scale, src_row, dst_row, dst_row,
+                           h, j->head_dim, tmp, qtmp);
+                append_one(j->v_src, j->src_dtype, j->v_cache, j->cache_dtype, j->v_scale, src_row, dst_row, dst_row,
+                           h, j->head_dim, tmp, qtmp);
+            }
+        }
+    }
+    free(tmp);
+    free(qtmp);
+    return NULL;
+}
+
 int ffo_append(const void* k_src, const void* v_src, int src_dtype, void* k_cache, void* v_cache, int cache_dtype,
                float* k_scale, float* v_scale, const int32_t* block_table, const int32_t* context_lens, int batch,
                int seq_len, int num_kv_heads, int head_dim, int block_size, int max_blocks, int num_blocks)
@@ -300,32 +346,29 @@ int ffo_append(const void* k_src, const void* v_src, int src_dtype, void* k_cach
     if (!k_src || !v_src || !k_cache || !v_cache || !block_table) return ERR_ARG;
     if ((cache_dtype == DT_I8 || cache_dtype == DT_FP8) && (!k_scale || !v_scale)) return ERR_ARG;
 
-    float*  tmp = (float*)malloc(sizeof(float) * (size_t)head_dim);
-    int8_t* qtmp = (int8_t*)malloc((size_t)head_dim);
-    for (int b = 0; b < batch; ++b)
+    append_job base = {k_src,      v_src,       k_cache,   v_cache,     k_scale,  v_scale,
+                       block_table, context_lens, src_dtype, cache_dtype, batch,    seq_len,
+                       num_kv_heads, head_dim,    max_blocks, num_blocks, 0,        num_kv_heads};
+    /* large appends run one worker per group of kv heads (the result does not depend on the split) */
+    int workers = (long long)batch * seq_len >= 4096 ? ffo_default_threads() : 1;
+    if (workers > num_kv_heads) workers = num_kv_heads;
+    if (workers <= 1)
     {
-        int ctx0 = context_lens ? context_lens[b] : 0; /* qwen_model.cu:32 */
-        for (int t = 0; t < seq_len; ++t)
-        {
-            long long pos = (long long)ctx0 + t; /* :33 */
-            if (pos < 0) continue;
-            long long blk = pos / 16, off = pos % 16; /* :34-35 */
-            if (blk >= max_blocks) continue;
-            int phys = block_table[(size_t)b * (size_t)max_blocks + (size_t)blk]; /* :37 */
-            if (phys < 0 || phys >= num_blocks) continue;
-            for (int h = 0; h < num_kv_heads; ++h)
-            {
-                size_t src_row = ((size_t)b * seq_len + t) * num_kv_heads + h;                /* :39 */
-                size_t dst_row = ((size_t)phys * 16 + (size_t)off) * num_kv_heads + (size_t)h; /* :41-42 */
-                append_one(k_src, src_dtype, k_cache, cache_dtype, k_scale, src_row, dst_row, dst_row, h, head_dim,
-                           tmp, qtmp);
-                append_one(v_src, src_dtype, v_cache, cache_dtype, v_scale, src_row, dst_row, dst_row, h, head_dim,
-                           tmp, qtmp);
-            }
-        }
+        append_worker(&base);
+        return 0;
     }
-    free(tmp);
-    free(qtmp);
+    append_job* jobs = (append_job*)malloc(sizeof(append_job) * (size_t)workers);
+    pthread_t*  tids = (pthread_t*)malloc(sizeof(pthread_t) * (size_t)workers);
+    for (int i = 0; i < workers; ++i)
+    {
+        jobs[i] = base;
+        jobs[i].h0 = (int)((long long)num_kv_heads * i / workers);
+        jobs[i].h1 = (int)((long long)num_kv_heads * (i + 1) / workers);
+        pthread_create(&tids[i], NULL, append_worker, &jobs[i]);
+    }
+    for (int i = 0; i < workers; ++i) pthread_join(tids[i], NULL);
+    free(tids);
+    free(jobs);
     return 0;
 }
 

@@ -4,7 +4,8 @@
 // include/firefly/{scheduler,radix_tree,request}.h with src/scheduler.cc and src/radix_tree.cc, into
 // oracle/_ref/libref_sched.so by `make -C oracle ref`) and against this repository's implementation (include/firefly
 // with firefly_amd/libffkv.so, by tests/conftest.py).  Tests run identical scripted operations through both and
-// compare every returned block id, context length and count.
+// compare every returned block id, context length and count.  Built over this repository (FFKV_SCHED_POLICY defined)
+// it can also select the scheduler's PrefillBlocks policy.
 //
 // The engine emulation in sd_engine_step follows the reference engine loop's bookkeeping (src/engine.cc:219-351):
 // a request without generated tokens prefills min(unmatched, chunk) tokens and produces its first token when the
@@ -68,13 +69,25 @@ extern "C" {
 
 // ---- scheduler + emulated engine -------------------------------------------------------------------------
 
-void* sd_create(int total_blocks, int max_batch, int max_chunk)
+// per_chunk = 1 selects this repository's PrefillBlocks::PerChunk (later prefill chunks get all their blocks);
+// 0 the reference's one-block-per-step rule, the only one the reference build has (it returns NULL for 1).
+void* sd_create_policy(int total_blocks, int max_batch, int max_chunk, int per_chunk)
 {
+#ifndef FFKV_SCHED_POLICY
+    if (per_chunk) return nullptr;
+#endif
     auto* s = new Serving();
     s->chunk = max_chunk;
+#ifdef FFKV_SCHED_POLICY
+    s->sched.init(total_blocks, max_batch, max_chunk, per_chunk ? PrefillBlocks::PerChunk : PrefillBlocks::OnePerStep);
+#else
     s->sched.init(total_blocks, max_batch, max_chunk);
+#endif
     return s;
 }
+
+// The reference's rule, in both builds (block ids comparable with the reference).
+void* sd_create(int total_blocks, int max_batch, int max_chunk) { return sd_create_policy(total_blocks, max_batch, max_chunk, 0); }
 
 void sd_destroy(void* h) { delete static_cast<Serving*>(h); }
 

@@ -100,7 +100,8 @@ int dss_step(void* h, int eager, int layers, void** q, void** k_new, void** v_ne
         if (!kernels::last_error().empty()) return s->err = kernels::last_error(), -1;
         return 0;
     }
-    if (!s->graph.capture(st, body)) return s->err = s->graph.error(), -1;
+    auto result = s->graph.capture(st, body);
+    if (!result) return s->err = result.error().description(), -1;
     if (!kernels::last_error().empty()) return s->err = kernels::last_error(), -1;
     return 0;
 }
@@ -108,7 +109,8 @@ int dss_step(void* h, int eager, int layers, void** q, void** k_new, void** v_ne
 int dss_launch(void* h, void* stream)
 {
     auto* s = static_cast<Step*>(h);
-    if (!s->graph.launch(static_cast<hipStream_t>(stream))) return s->err = s->graph.error(), -1;
+    auto result = s->graph.launch(static_cast<hipStream_t>(stream));
+    if (!result) return s->err = result.error().description(), -1;
     return 0;
 }
 

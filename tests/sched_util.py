@@ -21,7 +21,8 @@ _IP = ctypes.POINTER(ctypes.c_int)
 def load(path: Path):
     lib = ctypes.CDLL(str(path))
     sig = {
-        "sd_create": (_P, [_I, _I, _I]), "sd_destroy": (None, [_P]), "sd_add": (None, [_P, _I, _IP, _I, _I]),
+        "sd_create": (_P, [_I, _I, _I]), "sd_create_policy": (_P, [_I, _I, _I, _I]), "sd_destroy": (None, [_P]),
+        "sd_add": (None, [_P, _I, _IP, _I, _I]),
         "sd_request": (_I, [_P, _I, _IP, _I]), "sd_engine_step": (_I, [_P, _IP, _I]), "sd_unfinished": (_I, [_P]),
         "sd_pool_create": (_P, [_I]), "sd_pool_destroy": (None, [_P]), "sd_alloc": (_I, [_P, _I, _IP]),
         "sd_free": (None, [_P, _IP, _I]), "sd_free_count": (_I, [_P]),
@@ -117,10 +118,13 @@ def parse_batch(v):
     return reqs
 
 
-def run_serving(lib, total_blocks: int, max_batch: int, chunk: int, arrivals, max_steps: int = 2000):
+def run_serving(lib, total_blocks: int, max_batch: int, chunk: int, arrivals, max_steps: int = 2000,
+                per_chunk: bool = False):
     """arrivals: {step: [(id, tokens, max_tokens), ...]}.  Emulated engine loop; returns the scheduled batches
-    (request id, context_len, generated count, block table) of every step."""
-    h = lib.sd_create(total_blocks, max_batch, chunk)
+    (request id, context_len, generated count, block table) of every step.  per_chunk selects
+    PrefillBlocks::PerChunk (this repository's build only); otherwise the reference's rule."""
+    h = lib.sd_create_policy(total_blocks, max_batch, chunk, 1 if per_chunk else 0)
+    assert h, "this build has no PerChunk policy"
     buf = (ctypes.c_int * (1 << 20))()
     trace = []
     try:

@@ -132,3 +132,73 @@ def test_graph_replayed_decode_steps_match_checker(shim, gpu):
                     r[1].append(int(free.pop()))
     finally:
         shim.dss_destroy(h)
+
+
+def test_graph_survives_workspace_growth(shim, gpu):
+    """A graph captured with the thread's cached decode workspace stays valid after a later eager call on the same
+    stream needs a larger one: the old buffer is retired, not freed, so the replay neither writes freed memory
+    nor disturbs a tensor allocated after the growth (firefly_amd/csrc/host/kernels.cpp)."""
+    import torch
+
+    Hq, Hkv, D, N, STRIDE = 32, 8, 128, 6000, 64
+    rng = np.random.default_rng(31)
+    kf = rng.standard_normal((N, 16, Hkv, D), dtype=np.float32) * np.float32(0.3)
+    vf = rng.standard_normal((N, 16, Hkv, D), dtype=np.float32)
+    pool_k, pool_v = cases.encode(kf, O.DTYPE_BF16), cases.encode(vf, O.DTYPE_BF16)
+    side = torch.cuda.Stream()
+    stream = side.cuda_stream
+    free = list(rng.permutation(N))
+    steps = {}
+    try:
+        for cap in (2, 64):  # the second step's workspace (more rows) outgrows the first's
+            ctx = [int(c) for c in rng.integers(100, 900, size=cap)]
+            blocks = [[int(free.pop()) for _ in range((c + 16) // 16)] for c in ctx]
+            h = shim.dss_create(cap, STRIDE)
+            assert h
+            shim.dss_pack(h, cap, _arr(ctx), _arr([len(b) for b in blocks]), _arr([x for b in blocks for x in b]))
+            assert shim.dss_upload(h, stream) == 0
+            table = np.ctypeslib.as_array(shim.dss_host_table(h), shape=(cap * STRIDE,)).reshape(cap, STRIDE).copy()
+            t = dict(h=h, cap=cap, table=table, ctx=np.array(ctx, np.int32),
+                     q=cases.encode(rng.standard_normal((cap, 1, Hq, D), dtype=np.float32), O.DTYPE_BF16),
+                     kn=cases.encode(rng.standard_normal((cap, 1, Hkv, D), dtype=np.float32), O.DTYPE_BF16),
+                     vn=cases.encode(rng.standard_normal((cap, 1, Hkv, D), dtype=np.float32), O.DTYPE_BF16),
+                     dk=gu.to_dev(pool_k, O.DTYPE_BF16, gpu), dv=gu.to_dev(pool_v, O.DTYPE_BF16, gpu))
+            t["dq"] = gu.to_dev(t["q"], O.DTYPE_BF16, gpu)
+            t["dkn"] = gu.to_dev(t["kn"], O.DTYPE_BF16, gpu)
+            t["dvn"] = gu.to_dev(t["vn"], O.DTYPE_BF16, gpu)
+            t["dout"] = torch.zeros((cap, 1, Hq * D), dtype=torch.bfloat16, device=gpu)
+            steps[cap] = t
+        torch.cuda.synchronize()
+
+        def args(t):
+            one = lambda x: (ctypes.c_void_p * 1)(x.data_ptr())  # noqa: E731
+            return (one(t["dq"]), one(t["dkn"]), one(t["dvn"]), one(t["dk"]), one(t["dv"]), one(t["dout"]), Hq,
+                    Hkv, D, N, O.DTYPE_BF16, stream)
+
+        small, big = steps[2], steps[64]
+        print("case workspace growth: eager + capture at B=2", flush=True)
+        assert shim.dss_step(small["h"], 1, 1, *args(small)) == 0, shim.dss_error(small["h"])
+        assert shim.dss_step(small["h"], 0, 1, *args(small)) == 0, shim.dss_error(small["h"])
+        print("case workspace growth: eager at B=64 on the same stream", flush=True)
+        assert shim.dss_step(big["h"], 1, 1, *args(big)) == 0, shim.dss_error(big["h"])
+        torch.cuda.synchronize()
+        canary = torch.full((64 << 20,), 7, dtype=torch.uint8, device=gpu)  # allocated after the growth
+        small["dk"].copy_(gu.to_dev(pool_k, O.DTYPE_BF16, gpu))
+        small["dv"].copy_(gu.to_dev(pool_v, O.DTYPE_BF16, gpu))
+        small["dout"].zero_()
+        torch.cuda.synchronize()
+        print("case workspace growth: replay the B=2 graph", flush=True)
+        assert shim.dss_launch(small["h"], stream) == 0, shim.dss_error(small["h"])
+        torch.cuda.synchronize()
+        assert bool((canary == 7).all()), "the replay wrote into memory allocated after the workspace grew"
+        for t in (small,):
+            hk, hv = pool_k.copy(), pool_v.copy()
+            O.append(t["kn"], t["vn"], O.DTYPE_BF16, hk, hv, O.DTYPE_BF16, t["table"], t["ctx"])
+            _, ref32 = O.paged_decode(t["q"], O.DTYPE_BF16, hk, hv, O.DTYPE_BF16, t["table"], t["ctx"])
+            got = t["dout"].float().cpu().numpy().reshape(ref32.shape)
+            m = np.maximum(np.abs(got), np.abs(ref32))
+            half = 2.0 ** (np.floor(np.log2(np.maximum(m, 2.0 ** -126))) - 8)
+            assert float((np.abs(got - ref32) - half).max()) <= 2e-3
+    finally:
+        for t in steps.values():
+            shim.dss_destroy(t["h"])

@@ -122,3 +122,67 @@ def test_prefix_matches_are_block_aligned(mine):
             assert len(blocks) == mt // 16
     finally:
         p.close()
+
+
+def _positions_covered(trace, prompts, chunk):
+    """For every scheduled entry, (KV positions its step writes, positions its block table covers)."""
+    rows = []
+    for batch in trace:
+        for rid, ctx, gen, blocks in batch:
+            if gen == 0:  # prefill: the next chunk of the prompt
+                end = ctx + min(len(prompts[rid]) - ctx, chunk)
+            else:         # decode: the newest token goes to position ctx
+                end = ctx + 1
+            rows.append((rid, gen, end, 16 * len(blocks)))
+    return rows
+
+
+def test_long_prompt_chunks_hold_their_blocks_per_chunk(mine):
+    """A 600-token prompt prefilled in chunks of 256: under PrefillBlocks::PerChunk every chunk's positions have
+    blocks before it runs.  Under the reference's rule the second chunk (positions 256..511) runs with 17 blocks,
+    as src/scheduler.cc:88-99 gives a running request one block per step; the reference build does the same."""
+    prompt = list(range(1, 601))
+    arrivals = {0: [(0, prompt, 4)]}
+    fixed = su.run_serving(mine, 200, 4, 256, arrivals, per_chunk=True)
+    rows = _positions_covered(fixed, {0: prompt}, 256)
+    assert [r[2] for r in rows if r[1] == 0] == [256, 512, 600]
+    assert all(end <= have for _, _, end, have in rows)
+    assert [have for _, gen, _, have in rows if gen == 0] == [256, 512, 608]
+
+    compat = su.run_serving(mine, 200, 4, 256, arrivals)
+    short = [(end, have) for _, gen, end, have in _positions_covered(compat, {0: prompt}, 256) if end > have]
+    assert short and short[0] == (512, 17 * 16)
+
+
+def test_long_prompt_reference_rule_matches_reference(mine, ref):
+    prompt = list(range(1, 601))
+    arrivals = {0: [(0, prompt, 4)], 1: [(1, prompt[:300] + [7] * 50, 3)]}
+    assert su.run_serving(mine, 200, 4, 256, arrivals) == su.run_serving(ref, 200, 4, 256, arrivals)
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_per_chunk_policy_equals_reference_when_prompts_fit_one_chunk(mine, seed):
+    """The policies differ only for requests that need more than one prefill chunk."""
+    rng = np.random.default_rng(300 + seed)
+    arrivals = su.shared_prefix_workload(400 + seed, 12, int(rng.integers(16, 120)), 1, 60, 1, 12,
+                                         n_prefixes=2)
+    args = (int(rng.integers(40, 200)), int(rng.integers(2, 8)), 256, arrivals)
+    assert su.run_serving(mine, *args, per_chunk=True) == su.run_serving(mine, *args)
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_per_chunk_policy_covers_every_step(mine, seed):
+    """Random serving workloads with long prompts and small chunks: with PerChunk every scheduled step has blocks
+    for every position it writes, and the allocator never hands out a block twice."""
+    rng = np.random.default_rng(500 + seed)
+    chunk = int(rng.choice([16, 32, 48, 64]))
+    arrivals = su.shared_prefix_workload(600 + seed, 10, int(rng.integers(40, 160)), 10, 200, 1, 10,
+                                         n_prefixes=2)
+    prompts = {rid: toks for reqs in arrivals.values() for rid, toks, _ in reqs}
+    trace = su.run_serving(mine, 2000, 6, chunk, arrivals, max_steps=3000, per_chunk=True)
+    rows = _positions_covered(trace, prompts, chunk)
+    assert rows and all(end <= have for _, _, end, have in rows)
+    for batch in trace:
+        # prefix blocks are shared between requests; a request's own blocks never repeat within its table
+        for _, _, _, blocks in batch:
+            assert len(set(blocks)) == len(blocks)
