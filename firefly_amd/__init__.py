@@ -28,6 +28,7 @@ ERR_WORKSPACE = -3
 ERR_HIP = -4
 
 BLOCK_SIZE = 16
+NOALLOC_SCRATCH_BYTES = 32 << 20  # FFKV_NOALLOC_SCRATCH_BYTES (include/ffkv.h)
 
 
 class FFKVError(RuntimeError):
@@ -57,6 +58,9 @@ def _load() -> ctypes.CDLL:
     lib.ffkv_paged_decode.restype = i32
     lib.ffkv_paged_decode.argtypes = [vp, vp, i32, vp, vp, i32, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32,
                                       i32, f32, vp, sz, vp]
+    lib.ffkv_paged_decode_noalloc.restype = i32
+    lib.ffkv_paged_decode_noalloc.argtypes = [vp, vp, i32, vp, vp, i32, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32,
+                                              i32, i32, f32, vp]
     lib.ffkv_decode_shared_prefix_workspace_bytes.restype = sz
     lib.ffkv_decode_shared_prefix_workspace_bytes.argtypes = [i32, i32, i32, i32, i32, i32, i32]
     lib.ffkv_paged_decode_shared_prefix.restype = i32
@@ -244,6 +248,22 @@ def append_paged_attention(k_new, v_new, q, k_cache, v_cache, block_table, conte
                                        _ptr(k_scale), _ptr(v_scale), _ptr(block_table), _ptr(context_lens), B, Hq,
                                        Hkv, D, BLOCK_SIZE, max_blocks, N, max_context_len, float(scale),
                                        _ptr(workspace), ws_bytes, _stream(stream)))
+    return out
+
+
+def paged_attention_noalloc(q, k_cache, v_cache, block_table, context_lens, out, k_scale=None, v_scale=None,
+                            max_context_len: int = 0, scale: float = 0.0, num_blocks: int | None = None, stream=None):
+    """PagedAttention decode that allocates no device memory (``ffkv_paged_decode_noalloc``): the split-K partials
+    use the library's static per-GPU scratch.  ``out`` ``[B, 1, Hq * D]`` is the caller's."""
+    B = q.shape[0]
+    Hq, D = q.shape[-2], q.shape[-1]
+    Hkv = k_cache.shape[2]
+    max_blocks = block_table.shape[-1]
+    N = k_cache.shape[0] if num_blocks is None else num_blocks
+    check(lib.ffkv_paged_decode_noalloc(_ptr(q), _ptr(out), torch_dtype_code(q), _ptr(k_cache), _ptr(v_cache),
+                                        torch_dtype_code(k_cache), _ptr(k_scale), _ptr(v_scale), _ptr(block_table),
+                                        _ptr(context_lens), B, Hq, Hkv, D, BLOCK_SIZE, max_blocks, N,
+                                        max_context_len, float(scale), _stream(stream)))
     return out
 
 

@@ -89,16 +89,16 @@ bool decode_use_mfma(int cache_dtype, int /*group*/)
 }
 
 // MFMA workspace layout: [row meta: batch x 2 int32 | (m, l): slots x num_heads x 2 fp32 | acc: slots x num_heads
-// x head_dim fp32], each region 256-byte aligned, slots = kMfmaMaxItems + batch.
+// x head_dim fp32], each region 256-byte aligned, slots = items + batch (slot = work item + row) plus, in
+// shared-prefix mode, prefix_chunks slots per row after those.  The public size query assumes kMfmaMaxItems items.
 struct MfmaLayout
 {
     int64_t meta, ml, acc, total;
 };
 
-MfmaLayout mfma_layout(int batch, int num_heads, int head_dim, int prefix_chunks = 0)
+MfmaLayout mfma_layout(int batch, int num_heads, int head_dim, int prefix_chunks = 0, int items = kMfmaMaxItems)
 {
-    // shared-prefix mode adds prefix_chunks slots per row after the decode kernel's
-    const int64_t slots = static_cast<int64_t>(kMfmaMaxItems) + batch + static_cast<int64_t>(prefix_chunks) * batch;
+    const int64_t slots = static_cast<int64_t>(items) + batch + static_cast<int64_t>(prefix_chunks) * batch;
     MfmaLayout    l{};
     l.meta = 0;
     l.ml = align256(static_cast<int64_t>(batch) * 2 * 4);
@@ -372,6 +372,39 @@ size_t ffkv_decode_workspace_bytes(int batch, int num_heads, int head_dim, int m
 namespace
 {
 
+// Split-K scratch of ffkv_paged_decode_noalloc: a file-scope device array, one copy on every GPU the library runs
+// on, held until the process ends.  Host code never passes `scratch` itself to a kernel (on the host it names a
+// stand-in, not device memory): scratch_for_device() resolves the current device's copy once with
+// hipGetSymbolAddress and every later use goes through that address.  Calls on one GPU share its copy; the
+// kernels write every partial before reading it, so nothing needs clearing between calls, but calls that overlap
+// in time on one GPU race.
+__device__ __align__(256) static unsigned char scratch[FFKV_NOALLOC_SCRATCH_BYTES];
+
+std::mutex         g_scratch_mu;
+std::map<int, void*> g_scratch;  // device -> address of its copy of `scratch`
+
+int scratch_for_device(void** ptr)
+{
+    int        dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    auto                        it = g_scratch.find(dev);
+    if (it == g_scratch.end())
+    {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || p == nullptr) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+        it = g_scratch.emplace(dev, p).first;
+    }
+    *ptr = it->second;
+    return FFKV_OK;
+}
+
+// workspace == kNoAlloc: the decode uses this library's static scratch (ffkv_paged_decode_noalloc) and allocates
+// nothing; sizes whose partials do not fit it are rejected.
+void* const kNoAlloc = reinterpret_cast<void*>(~uintptr_t{0});
+
 int decode_impl(const void* q, void* out, int qo_dtype, const void* k_cache, const void* v_cache, int cache_dtype,
                 const float* k_scale, const float* v_scale, const int32_t* block_table, const int32_t* context_lens,
                 int batch, int num_heads, int num_kv_heads, int head_dim, int block_size, int max_blocks,
@@ -418,12 +451,22 @@ int decode_impl(const void* q, void* out, int qo_dtype, const void* k_cache, con
     const int  chunk = ffkv::decode_chunk(batch, num_kv_heads, cap);
     const int  max_chunks = static_cast<int>(ceil_div(cap > 0 ? cap : 1, chunk));
 
+    ffkv::DecodeArgs a{};
+    a.qo_dtype = qo_dtype;
+    a.cache_dtype = cache_dtype;
+    a.batch = batch;
+    a.num_heads = num_heads;
+    a.num_kv_heads = num_kv_heads;
+    a.group = group;
+    a.head_dim = head_dim;
+    a.items = mfma ? ffkv::decode_mfma_launch_items(a) : 0;
+
     // workspace layout: MFMA kernel see mfma_layout, generic kernel [ml | acc] (none for single-chunk rows)
     ffkv::MfmaLayout lay{};
     int64_t          need = 0;
     if (mfma)
     {
-        lay = ffkv::mfma_layout(batch, num_heads, head_dim, pfx_chunks);
+        lay = ffkv::mfma_layout(batch, num_heads, head_dim, pfx_chunks, a.items);
         need = lay.total;
     }
     else if (max_chunks > 1)
@@ -437,6 +480,16 @@ int decode_impl(const void* q, void* out, int qo_dtype, const void* k_cache, con
     hipStream_t s = static_cast<hipStream_t>(stream);
     void*       ws = workspace;
     bool        owned = false;
+    if (ws == kNoAlloc)
+    {
+        if (need > static_cast<int64_t>(FFKV_NOALLOC_SCRATCH_BYTES))
+            return fail(FFKV_ERR_WORKSPACE,
+                        "ffkv_paged_decode_noalloc: these sizes need %lld bytes of split-K scratch, more than its "
+                        "maximum of %lld bytes (use ffkv_paged_decode with a workspace)",
+                        static_cast<long long>(need), static_cast<long long>(FFKV_NOALLOC_SCRATCH_BYTES));
+        if (const int rc = scratch_for_device(&ws)) return rc;
+        workspace_bytes = FFKV_NOALLOC_SCRATCH_BYTES;
+    }
     if (need > 0)
     {
         if (ws == nullptr)
@@ -457,8 +510,7 @@ int decode_impl(const void* q, void* out, int qo_dtype, const void* k_cache, con
     }
     char* wsb = static_cast<char*>(ws);
 
-    const float      sm_scale = scale > 0.0f ? scale : 1.0f / sqrtf(static_cast<float>(head_dim));
-    ffkv::DecodeArgs a{};
+    const float sm_scale = scale > 0.0f ? scale : 1.0f / sqrtf(static_cast<float>(head_dim));
     a.q = q;
     a.out = out;
     a.k_cache = k_cache;
@@ -470,13 +522,6 @@ int decode_impl(const void* q, void* out, int qo_dtype, const void* k_cache, con
     a.ws_meta = need > 0 && mfma ? reinterpret_cast<int32_t*>(wsb + lay.meta) : nullptr;
     a.ws_ml = need > 0 ? reinterpret_cast<float*>(wsb + lay.ml) : nullptr;
     a.ws_acc = need > 0 ? reinterpret_cast<float*>(wsb + lay.acc) : nullptr;
-    a.qo_dtype = qo_dtype;
-    a.cache_dtype = cache_dtype;
-    a.batch = batch;
-    a.num_heads = num_heads;
-    a.num_kv_heads = num_kv_heads;
-    a.group = group;
-    a.head_dim = head_dim;
     a.max_blocks = max_blocks;
     a.num_blocks = num_blocks;
     a.cap_tokens = cap;
@@ -488,7 +533,7 @@ int decode_impl(const void* q, void* out, int qo_dtype, const void* k_cache, con
     {
         a.skip_blocks = skip;
         a.pfx_chunks = pfx_chunks;
-        a.pfx_slot0 = ffkv::kMfmaMaxItems + batch;
+        a.pfx_slot0 = a.items + batch;
         ffkv::PrefillArgs p{};
         p.q = q;
         p.k_cache = k_cache;
@@ -555,6 +600,17 @@ int ffkv_paged_decode(const void* q, void* out, int qo_dtype, const void* k_cach
     return decode_impl(q, out, qo_dtype, k_cache, v_cache, cache_dtype, k_scale, v_scale, block_table, context_lens,
                        batch, num_heads, num_kv_heads, head_dim, block_size, max_blocks, num_blocks, max_context_len,
                        scale, 0, workspace, workspace_bytes, stream);
+}
+
+int ffkv_paged_decode_noalloc(const void* q, void* out, int qo_dtype, const void* k_cache, const void* v_cache,
+                              int cache_dtype, const float* k_scale, const float* v_scale, const int32_t* block_table,
+                              const int32_t* context_lens, int batch, int num_heads, int num_kv_heads, int head_dim,
+                              int block_size, int max_blocks, int num_blocks, int max_context_len, float scale,
+                              void* stream)
+{
+    return decode_impl(q, out, qo_dtype, k_cache, v_cache, cache_dtype, k_scale, v_scale, block_table, context_lens,
+                       batch, num_heads, num_kv_heads, head_dim, block_size, max_blocks, num_blocks, max_context_len,
+                       scale, 0, kNoAlloc, 0, stream);
 }
 
 int ffkv_append_paged_decode(const void* k_new, const void* v_new, int src_dtype, const void* q, void* out,

@@ -98,7 +98,7 @@ struct DecodeArgs
     const int32_t* block_table;
     const int32_t* context_lens;
     // Partial results.  Generic kernel: [batch, num_heads, max_chunks] entries.  MFMA kernel: slot = work item +
-    // row, [kMfmaMaxItems + batch, num_heads] entries.
+    // row, [items + batch, num_heads] entries.
     float*         ws_ml;   // [.., 2]: running max (log2 domain) and denominator
     float*         ws_acc;  // [.., head_dim]: unnormalised output
     int32_t*       ws_meta;  // MFMA kernel: [batch, 2] first and last work item covering each row
@@ -112,6 +112,7 @@ struct DecodeArgs
     int            max_blocks;
     int            num_blocks;
     int            cap_tokens;  // attended tokens per row are clamped to this
+    int            items;       // MFMA kernel: work items of the launch (decode_mfma_launch_items)
     int            chunk;       // tokens per split-K chunk (multiple of 16)
     int            max_chunks;  // ceil(cap_tokens / chunk)
     float          scale_log2;  // softmax scale * log2(e)
@@ -140,8 +141,10 @@ constexpr int kMfmaMaxItems = 2048;
 // Work items for one MFMA decode launch: as many workgroups as the device keeps resident at once (CUs times
 // occupancy of `kernel` at `threads` threads), divided over `grid_y` head groups, capped at kMfmaMaxItems.
 int decode_mfma_items(const void* kernel, int threads, int grid_y);
+// decode_mfma_items for the kernel instance launch_decode_mfma selects for `a` (its dtypes, head_dim and heads).
+int decode_mfma_launch_items(const DecodeArgs& a);
 bool decode_use_mfma(int cache_dtype, int group);
-size_t decode_mfma_workspace_bytes(int batch, int num_heads, int head_dim);
+size_t decode_mfma_workspace_bytes(int batch, int num_heads, int head_dim);  // upper bound (kMfmaMaxItems items)
 
 // Split-K geometry shared by the workspace query and the launcher.
 int    decode_cap_tokens(int max_blocks, int max_context_len);

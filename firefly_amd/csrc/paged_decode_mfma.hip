@@ -736,15 +736,35 @@ __global__ __launch_bounds__(64 * MW) void paged_decode_mfma_merge(DecodeArgs a)
 namespace
 {
 
-template <int CT, int QT, int D>
-hipError_t launch_m3(const DecodeArgs& a0, hipStream_t stream)
+// Waves per workgroup and workgroups per work item (grid y) of a launch: one wave per KV head and block of 16
+// query heads, up to FFKV_MFMA_MAX_WAVES per workgroup.
+struct MfmaShape
 {
-    DecodeArgs a = a0;
-    const int  vh = a.num_kv_heads * ((a.group + 15) / 16);  // one wave per KV head and block of 16 query heads
-    const int  nw = vh < FFKV_MFMA_MAX_WAVES ? vh : FFKV_MFMA_MAX_WAVES;
-    const int  gy = (vh + nw - 1) / nw;
-    const auto kern = paged_decode_mfma<CT, QT, D>;
-    const int  items = decode_mfma_items(reinterpret_cast<const void*>(kern), 64 * nw, gy);
+    int nw, gy;
+};
+
+MfmaShape mfma_shape(const DecodeArgs& a)
+{
+    const int vh = a.num_kv_heads * ((a.group + 15) / 16);
+    const int nw = vh < FFKV_MFMA_MAX_WAVES ? vh : FFKV_MFMA_MAX_WAVES;
+    return MfmaShape{nw, (vh + nw - 1) / nw};
+}
+
+template <int CT, int QT, int D>
+int items_m3(const DecodeArgs& a)
+{
+    const MfmaShape sh = mfma_shape(a);
+    return decode_mfma_items(reinterpret_cast<const void*>(paged_decode_mfma<CT, QT, D>), 64 * sh.nw, sh.gy);
+}
+
+template <int CT, int QT, int D>
+hipError_t launch_m3(const DecodeArgs& a, hipStream_t stream)
+{
+    const MfmaShape sh = mfma_shape(a);
+    const int       nw = sh.nw, gy = sh.gy;
+    const auto      kern = paged_decode_mfma<CT, QT, D>;
+    // the workspace holds items + batch partial slots
+    const int items = a.items > 0 ? a.items : items_m3<CT, QT, D>(a);
     hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(items), static_cast<unsigned>(gy)), dim3(64 * nw), 0, stream, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
@@ -754,6 +774,34 @@ hipError_t launch_m3(const DecodeArgs& a0, hipStream_t stream)
     else
         hipLaunchKernelGGL((paged_decode_mfma_merge<QT, D, 4>), mgrid, dim3(256), 0, stream, a);
     return hipGetLastError();
+}
+
+template <int CT, int QT>
+int items_m2(const DecodeArgs& a)
+{
+    switch (a.head_dim)
+    {
+        case 64:
+            return items_m3<CT, QT, 64>(a);
+        case 128:
+            return items_m3<CT, QT, 128>(a);
+        default:
+            return items_m3<CT, QT, 256>(a);
+    }
+}
+
+template <int CT>
+int items_m1(const DecodeArgs& a)
+{
+    switch (a.qo_dtype)
+    {
+        case F32:
+            return items_m2<CT, F32>(a);
+        case F16:
+            return items_m2<CT, F16>(a);
+        default:
+            return items_m2<CT, BF16>(a);
+    }
 }
 
 template <int CT, int QT>
@@ -785,6 +833,21 @@ hipError_t launch_m1(const DecodeArgs& a, hipStream_t stream)
 }
 
 }  // namespace
+
+int decode_mfma_launch_items(const DecodeArgs& a)
+{
+    switch (a.cache_dtype)
+    {
+        case BF16:
+            return items_m1<BF16>(a);
+        case F16:
+            return items_m1<F16>(a);
+        case I8:
+            return items_m1<I8>(a);
+        default:
+            return items_m1<FP8>(a);
+    }
+}
 
 hipError_t launch_decode_mfma(const DecodeArgs& a, hipStream_t stream)
 {

