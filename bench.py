@@ -14,8 +14,11 @@ Printed JSON line (rank 0, N = 1):
   roofline       the decode call (split-K pass + merge pass) timed with HIP events on the launch stream;
                  achieved = algorithmic decode bytes / mean call duration, peak 8 TB/s
   cpu_baseline   the C restatement under oracle/ (the checker) timed on the host cores on the same layer-0
-                 inputs, same algorithmic-bytes formula
+                 inputs, same algorithmic-bytes formula, threaded over every core this process may run on
   parity         max-abs error of the layer-0 GPU output against that CPU result (fp32, before rounding)
+  device_copy    a 1 GiB torch device copy timed the same way: the streaming rate a plain kernel reaches here
+  other_configs  C3, C4 and C5 (int8 and fp8 pools filled by the quantizing append, whose bulk throughput is
+                 reported as quantized_append), the fused rope + append, and the decode step's host upload
 
 Algorithmic bytes per decode call (L'_b = context_lens[b] + 1):
   sum_b L'_b*Hkv*D*2*2 (K and V) + B*Hq*D*2*2 (q in, out) + sum_b ceil(L'_b/16)*4 (block table) + 4*B
@@ -72,14 +75,26 @@ def append_bytes(T: int, batch: int) -> int:
 
 
 def measured_traffic():
-    """HBM bytes per decode call from the rocprofv3 counter passes recorded in profiles/ (FETCH_SIZE and
-    WRITE_SIZE of the decode and merge kernels, scaled by the same counters' reading for a copy of known size);
-    None when that record is absent."""
+    """(HBM bytes per decode call, commit it was measured at) from the rocprofv3 counter passes recorded in
+    profiles/decode_c2_traffic.json (FETCH_SIZE and WRITE_SIZE of the decode and merge kernels, scaled by the same
+    counters' reading for a copy of known size); (None, None) when that record is absent."""
     path = ROOT / "profiles" / "decode_c2_traffic.json"
     if not path.exists():
-        return None
+        return None, None
     rec = json.loads(path.read_text())
-    return rec.get("bytes_per_call")
+    return rec.get("bytes_per_call"), rec.get("measured_at_commit")
+
+
+def device_copy_rate(torch, dev, stream, nbytes: int = 1 << 30) -> dict:
+    """A 1 GiB device-to-device copy (torch), timed with HIP events: the streaming rate a plain kernel reaches on
+    this GPU, reported beside the roofline's 8 TB/s peak (read + write bytes over time)."""
+    src = torch.ones(nbytes, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    us = _events_us(lambda i: dst.copy_(src), 20, stream)
+    del src, dst
+    torch.cuda.empty_cache()
+    return {"bytes_moved": 2 * nbytes, "us_per_copy": us, "TB_per_s": 2 * nbytes / (us * 1e-6) / 1e12,
+            "pct_of_peak": 2 * nbytes / (us * 1e-6) / 1e12 / HBM_PEAK_TBS * 100}
 
 
 BF16_MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense bf16
@@ -121,32 +136,60 @@ def _tables(rng, need, shared_blocks=0):
 
 
 def _pools(torch, gen, dev, N, Hkv, D, kv, layers):
+    """Random bf16 pools (kv must be "bf16"; quantized pools come from _appended_pools)."""
+    assert kv == "bf16"
     shape = (N, BLOCK, Hkv, D)
-    out = []
-    for _ in range(layers):
-        if kv == "bf16":
-            kp = torch.randn(shape, generator=gen, device=dev, dtype=torch.bfloat16)
-            vp = torch.randn(shape, generator=gen, device=dev, dtype=torch.bfloat16)
-            ks = vs = None
-        elif kv == "i8":
-            kp = torch.randint(-127, 128, shape, generator=gen, device=dev, dtype=torch.int8)
-            vp = torch.randint(-127, 128, shape, generator=gen, device=dev, dtype=torch.int8)
-            ks = torch.rand((N, BLOCK, Hkv), generator=gen, device=dev) * 0.05
-            vs = torch.rand((N, BLOCK, Hkv), generator=gen, device=dev) * 0.05
-        else:  # fp8 e4m3 codes of magnitude <= 448 (no NaN codes)
-            kp = torch.randint(0, 126, shape, generator=gen, device=dev, dtype=torch.uint8)
-            kp |= torch.randint(0, 2, shape, generator=gen, device=dev, dtype=torch.uint8) << 7
-            vp = torch.randint(0, 126, shape, generator=gen, device=dev, dtype=torch.uint8)
-            vp |= torch.randint(0, 2, shape, generator=gen, device=dev, dtype=torch.uint8) << 7
-            ks = torch.full((Hkv,), 0.01, device=dev)
-            vs = torch.full((Hkv,), 0.01, device=dev)
-        out.append((kp, vp, ks, vs))
-    return out
+    return [(torch.randn(shape, generator=gen, device=dev, dtype=torch.bfloat16),
+             torch.randn(shape, generator=gen, device=dev, dtype=torch.bfloat16), None, None) for _ in range(layers)]
+
+
+def _appended_pools(ff, torch, gen, dev, stream, N, Hkv, D, kv, layers, table, ctx, chunk=1024):
+    """Quantized pools filled the way an engine fills them: bf16 K/V ~ N(0,1) with 1% of the elements x8 go
+    through the quantizing append (int8: per-token absmax/127 scales written by the append; fp8: per-head scales
+    absmax/448 read by it) in chunks of `chunk` tokens per row at positions 0, chunk, 2*chunk, ... (one chunk of
+    source data, appended at every offset).  Returns (pools, quantized-append figure of the first chunk)."""
+    import numpy as np
+
+    B = table.shape[0]
+
+    def src():
+        x = torch.randn((B, chunk, Hkv, D), generator=gen, device=dev, dtype=torch.float32)
+        x = torch.where(torch.rand(x.shape, generator=gen, device=dev) < 0.01, x * 8.0, x)
+        return x.to(torch.bfloat16)
+
+    ks_src, vs_src = src(), src()
+    offsets = range(0, int(max(ctx)) + 1, chunk)
+    cx = [torch.full((B,), o, dtype=torch.int32, device=dev) for o in offsets]
+    pools, fig = [], None
+    for layer in range(layers):
+        store = torch.int8 if kv == "i8" else torch.uint8
+        kp = torch.empty((N, BLOCK, Hkv, D), dtype=store, device=dev)
+        vp = torch.empty_like(kp)
+        if kv == "i8":
+            ks = torch.empty((N, BLOCK, Hkv), device=dev)
+            vs = torch.empty_like(ks)
+        else:
+            ks = (ks_src.float().abs().amax(dim=(0, 1, 3)) / 448.0).contiguous()
+            vs = (vs_src.float().abs().amax(dim=(0, 1, 3)) / 448.0).contiguous()
+        if layer == 0:  # time the first chunk's append: every row has >= 1024 cached tokens (C5 contexts)
+            us = _events_us(lambda i: ff.append_kv_cache(ks_src, vs_src, kp, vp, table, cx[0], ks, vs, stream=stream),
+                            10, stream)
+            T = B * chunk
+            nbytes = T * Hkv * D * (2 + 1) * 2 + (T * Hkv * 4 * 2 if kv == "i8" else Hkv * 4 * 2) + 4 * B + 4 * T
+            fig = {"kv": kv, "tokens": T, "bytes": nbytes, "us_per_call": us, "GB_per_s": nbytes / (us * 1e-6) / 1e9,
+                   "pct_of_peak": nbytes / (us * 1e-6) / 1e12 / HBM_PEAK_TBS * 100}
+        for c in cx:
+            ff.append_kv_cache(ks_src, vs_src, kp, vp, table, c, ks, vs, stream=stream)
+        pools.append((kp, vp, ks, vs))
+    torch.cuda.synchronize()
+    del ks_src, vs_src
+    return pools, fig
 
 
 def decode_config(ff, torch, dev, stream, name, B, Hq, Hkv, D, ctx, kv="bf16", layers=2, shared_blocks=0,
                   calls=50, seed=0):
-    """Decode attention alone on one configuration (layers rotated to defeat the 256 MB Infinity Cache)."""
+    """Decode attention alone on one configuration (layers rotated to defeat the 256 MB Infinity Cache).  bf16
+    pools are random; int8 / fp8 pools are filled by the quantizing append (whose throughput is reported)."""
     import numpy as np
 
     rng = np.random.default_rng(seed)
@@ -155,10 +198,14 @@ def decode_config(ff, torch, dev, stream, name, B, Hq, Hkv, D, ctx, kv="bf16", l
     Lp = [int(c) + 1 for c in ctx]
     need = [math.ceil(x / BLOCK) for x in Lp]
     table_np, N = _tables(rng, need, shared_blocks)
-    pools = _pools(torch, gen, dev, N, Hkv, D, kv, layers)
+    bt = torch.from_numpy(table_np).to(dev)
+    append_fig = None
+    if kv == "bf16":
+        pools = _pools(torch, gen, dev, N, Hkv, D, kv, layers)
+    else:
+        pools, append_fig = _appended_pools(ff, torch, gen, dev, stream, N, Hkv, D, kv, layers, bt, Lp)
     q = torch.randn((B, 1, Hq, D), generator=gen, device=dev, dtype=torch.bfloat16)
     out = torch.empty((B, 1, Hq * D), device=dev, dtype=torch.bfloat16)
-    bt = torch.from_numpy(table_np).to(dev)
     cx = torch.from_numpy(np.asarray(ctx, np.int32)).to(dev)
     ws = ff.decode_workspace(B, Hq, D, table_np.shape[1], max(Lp), device=dev)
 
@@ -177,6 +224,8 @@ def decode_config(ff, torch, dev, stream, name, B, Hq, Hkv, D, ctx, kv="bf16", l
            "context_tokens": tok, "us_per_call": us, "algorithmic_bytes": logical,
            "TB_per_s": logical / (us * 1e-6) / 1e12, "pct_of_peak": logical / (us * 1e-6) / 1e12 / HBM_PEAK_TBS * 100,
            "tokens_per_s": B / (us * 1e-6)}
+    if append_fig is not None:
+        rec["quantized_append"] = append_fig
     if shared_blocks:
         ushared = shared_blocks * BLOCK
         utok = ushared + sum(x - min(ushared, x) for x in Lp)
@@ -368,7 +417,7 @@ def cpu_baseline(ctx, table, N, k_pool, v_pool, q, gpu_out, seconds: float = 10.
 
     import oracle as O
 
-    threads = min(16, os.cpu_count() or 1)
+    threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
     kp = k_pool.view(torch.int16).cpu().numpy().view(np.uint16)
     vp = v_pool.view(torch.int16).cpu().numpy().view(np.uint16)
     qn = q.view(torch.int16).cpu().numpy().view(np.uint16)
@@ -554,6 +603,8 @@ def main(argv=None) -> int:
             return 2
         configs = {name: makers[name]() for name in want}
 
+    copy_rate = device_copy_rate(torch, dev, stream)
+
     # Layer-0 output for the parity figure and the CPU baseline on the same inputs.
     kp0, vp0 = pools[0]
     ff.paged_attention(q, kp0, vp0, table, ctx, out=out, max_context_len=max_ctx, workspace=ws, stream=stream)
@@ -563,6 +614,7 @@ def main(argv=None) -> int:
     if args.cpu_seconds > 0:
         cpu, err = cpu_baseline(ctx_np, table_np, N, kp0, vp0, q, out, args.cpu_seconds)
 
+    traffic, traffic_commit = measured_traffic()
     line = {
         "metric": "paged decode-attn HBM TB/s (% of peak) + tokens/s; KV-append GB/s, 1 GPU",
         "value": (dbytes + abytes) / (ms_per_step * 1e-3) / 1e12,
@@ -588,8 +640,9 @@ def main(argv=None) -> int:
         "append_bulk": bulk,
         "roofline": {"kernel": "ffkv_paged_decode (paged_decode_mfma + paged_decode_mfma_merge)", "bound": "hbm",
                      "achieved": achieved * 1e3, "peak": HBM_PEAK_TBS * 1e3, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_TBS, "traffic": measured_traffic(),
+                     "frac": achieved / HBM_PEAK_TBS, "traffic": traffic, "traffic_measured_at_commit": traffic_commit,
                      "algorithmic_bytes": dbytes},
+        "device_copy": copy_rate,
         "other_configs": configs,
         "cpu_baseline": cpu,
         "parity_max_abs_err_vs_cpu": err,

@@ -89,6 +89,105 @@ __device__ __forceinline__ int32_t quant_i8(float x, float s)
     return static_cast<int32_t>(r);
 }
 
+// The quantizers below give exactly the codes of quant_i8(x, s) and f32_to_e4m3(x / s) without a divide per
+// element.  A code depends on the quotient fl(x / s) only through where it falls between the target format's
+// rounding boundaries (int8: half-integers; e4m3: the midpoints between neighbouring codes).  y = x * rcp(s) is
+// within a few ulps of x / s (v_rcp_f32 is accurate to 1 ulp and the product rounds once), and fl(x / s) within
+// half an ulp, so when y lies more than 64 of its ulps from every boundary both round to the same code.  Only
+// when it does not (a fraction of about 1e-4 of random inputs), or for non-finite values, is the IEEE divide
+// evaluated.
+
+// 1/s for the quantizers: NaN unless s is positive, normal and finite, which sends every element to the divide.
+__device__ __forceinline__ float quant_rcp(float s)
+{
+    return s >= 0x1p-126f && s < __builtin_huge_valf() ? __builtin_amdgcn_rcpf(s) : __builtin_nanf("");
+}
+
+#ifndef FFKV_FP8_HW_CVT
+#define FFKV_FP8_HW_CVT 1  // fp8 codes of safe values from v_cvt_pk_fp8_f32 (0: the integer conversion)
+#endif
+
+// int8: y = x * rs is safe when it is more than 64 ulps from the half-integers, i.e. |y - rint(y)| < 0.5 - 64 ulp.
+// NaN and infinite y fail the test.
+__device__ __forceinline__ bool quant_i8_safe(float y, float r)
+{
+    return __builtin_fabsf(y - r) < __builtin_fmaf(-__builtin_fabsf(y), 0x1p-17f, 0.5f - 0x1p-40f);
+}
+
+// e4m3: y is safe when 2^-6 <= |y| < inf (e4m3 normal range, saturating above 448) and the 20 mantissa bits below
+// the 3 kept ones are more than 64 from the midpoint pattern 0x80000.  Subnormal-range y take the divide.
+__device__ __forceinline__ bool quant_e4m3_safe(float y)
+{
+    const uint32_t u = f2u(y);
+    const uint32_t a = u & 0x7fffffffu;
+    return a - 0x3c800000u < 0x7f800000u - 0x3c800000u && (u & 0xfffffu) + (64u - 0x80000u) > 128u;
+}
+
+// Quantize 8 values to packed codes (element i in byte i % 4 of w[i / 4]) with the fast forms; only in a wave
+// where some lane has an unsafe value are those values redone with the divide.  int8: s = the row's scale (> 0);
+// fp8: s = the head's scale.  fp8 codes of safe values come from the gfx950 conversion v_cvt_pk_fp8_f32 (OCP
+// e4m3, round to nearest even) of y clamped to +-448, which equals f32_to_e4m3(y) there: normal-range outputs,
+// and y is no tie.
+template <bool INT8>
+__device__ __forceinline__ void quant8(const float* x, float s, uint32_t* w)
+{
+    const float rs = quant_rcp(s);
+    bool        safe = true;
+    if constexpr (INT8)
+    {
+        uint32_t c[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+        {
+            const float y = x[i] * rs;
+            const float r = __builtin_rintf(y);
+            safe = safe && quant_i8_safe(y, r);
+            c[i] = static_cast<uint32_t>(static_cast<int32_t>(__builtin_fminf(__builtin_fmaxf(r, -127.0f), 127.0f)));
+        }
+        w[0] = (c[0] & 0xffu) | ((c[1] & 0xffu) << 8) | ((c[2] & 0xffu) << 16) | (c[3] << 24);
+        w[1] = (c[4] & 0xffu) | ((c[5] & 0xffu) << 8) | ((c[6] & 0xffu) << 16) | (c[7] << 24);
+    }
+    else
+    {
+        float y[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+        {
+            y[i] = x[i] * rs;
+            safe = safe && quant_e4m3_safe(y[i]);
+            y[i] = __builtin_fminf(__builtin_fmaxf(y[i], -448.0f), 448.0f);
+        }
+#if FFKV_FP8_HW_CVT
+#pragma unroll
+        for (int k = 0; k < 2; ++k)
+        {
+            const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(y[4 * k], y[4 * k + 1], 0, false);
+            w[k] = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(y[4 * k + 2], y[4 * k + 3], lo, true));
+        }
+#else
+#pragma unroll
+        for (int k = 0; k < 2; ++k)
+            w[k] = f32_to_e4m3(y[4 * k]) | (f32_to_e4m3(y[4 * k + 1]) << 8) | (f32_to_e4m3(y[4 * k + 2]) << 16) |
+                   (f32_to_e4m3(y[4 * k + 3]) << 24);
+#endif
+    }
+    if (__builtin_expect(!__all(safe), 0))
+    {
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+        {
+            const float y = x[i] * rs;
+            const bool  ok = INT8 ? quant_i8_safe(y, __builtin_rintf(y)) : quant_e4m3_safe(y);
+            if (!ok)
+            {
+                const uint32_t q = INT8 ? static_cast<uint32_t>(quant_i8(x[i], s)) & 0xffu : f32_to_e4m3(x[i] / s);
+                const int      sh = 8 * (i & 3);
+                w[i / 4] = (w[i / 4] & ~(0xffu << sh)) | (q << sh);
+            }
+        }
+    }
+}
+
 // ---------------------------------------------------------------------------------------------------------
 // 8-element vector access.  `p` points at element index `i` (a multiple of 8) of an array of type T.
 // ---------------------------------------------------------------------------------------------------------

@@ -53,19 +53,12 @@ __device__ __forceinline__ void store_cache8(void* cache, size_t dst, const floa
     Raw8 out;
     if constexpr (CACHE == I8)
     {
-        uint32_t q[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) q[i] = sc == 0.0f ? 0u : (quant_i8(x[i], sc) & 0xffu);
-        out.w[0] = q[0] | (q[1] << 8) | (q[2] << 16) | (q[3] << 24);
-        out.w[1] = q[4] | (q[5] << 8) | (q[6] << 16) | (q[7] << 24);
+        quant8<true>(x, sc == 0.0f ? 1.0f : sc, out.w);
+        if (sc == 0.0f) out.w[0] = out.w[1] = 0u;  // an all-zero row
     }
     else if constexpr (CACHE == FP8)
     {
-        uint32_t q[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) q[i] = f32_to_e4m3(x[i] / sc);
-        out.w[0] = q[0] | (q[1] << 8) | (q[2] << 16) | (q[3] << 24);
-        out.w[1] = q[4] | (q[5] << 8) | (q[6] << 16) | (q[7] << 24);
+        quant8<false>(x, sc, out.w);
     }
     else
     {
