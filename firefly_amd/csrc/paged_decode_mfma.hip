@@ -33,6 +33,10 @@
 //     page of a row has been scored, so a wave never waits on a dependent scalar load between pages.
 #include "mfma_common.h"
 
+#ifndef FFKV_MERGE_ROWS_MIN_BATCH
+#define FFKV_MERGE_ROWS_MIN_BATCH 16  // batches above this merge with paged_decode_mfma_merge_rows
+#endif
+
 #ifndef FFKV_MFMA_MAX_WAVES
 #define FFKV_MFMA_MAX_WAVES 4  // waves (KV heads, or blocks of 16 query heads of one) per workgroup
 #endif
@@ -733,6 +737,65 @@ __global__ __launch_bounds__(64 * MW) void paged_decode_mfma_merge(DecodeArgs a)
     }
 }
 
+// Combine the partials of split rows when each row has few pieces (more than 16 rows): thread k of the row's
+// workgroups owns output dims 4(k % (D/4)) .. +3 of head k / (D/4), folds that chunk of every piece of the row
+// (loads of up to MF = 16 pieces in flight together) and writes it; no cross-thread combine.  Rows written whole by
+// the decode kernel (one piece, no shared-prefix partials) or without tokens are left alone.
+template <int QT, int D>
+__global__ __launch_bounds__(256) void paged_decode_mfma_merge_rows(DecodeArgs a)
+{
+    constexpr int MF = 16;
+    const int     b = blockIdx.x;
+    const int     k = static_cast<int>(blockIdx.y) * 256 + static_cast<int>(threadIdx.x);
+    const int     i_lo = a.ws_meta[2 * b];
+    const int     i_hi = a.ws_meta[2 * b + 1];
+    if ((i_lo == i_hi && a.pfx_chunks == 0) || k >= a.num_heads * (D / 4)) return;
+    const int     h = k / (D / 4);
+    const int     d4 = (k - h * (D / 4)) * 4;
+    const int     pieces = a.pfx_chunks + (i_lo >= 0 ? i_hi - i_lo + 1 : 0);
+    float         m = kNegInf, l = 0.0f;
+    f32x4         o = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int i0 = 0; i0 < pieces; i0 += MF)
+    {
+        float ms[MF], ls[MF];
+        f32x4 xs[MF];
+#pragma unroll
+        for (int f = 0; f < MF; ++f)
+        {
+            ms[f] = kNegInf;
+            ls[f] = 0.0f;
+            xs[f] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            const int i = i0 + f;
+            if (i < pieces)
+            {
+                // the shared-prefix partials (slots pfx_slot0 + j * batch + b), then work items i_lo .. i_hi (slots
+                // item + b)
+                const int64_t slot = i < a.pfx_chunks
+                                         ? static_cast<int64_t>(a.pfx_slot0) + static_cast<int64_t>(i) * a.batch + b
+                                         : static_cast<int64_t>(i_lo + i - a.pfx_chunks) + b;
+                const int64_t e = slot * a.num_heads + h;
+                const float2  ml = *reinterpret_cast<const float2*>(a.ws_ml + e * 2);
+                ms[f] = ml.x;
+                ls[f] = ml.y;
+                xs[f] = *reinterpret_cast<const f32x4*>(a.ws_acc + e * D + d4);
+            }
+        }
+#pragma unroll
+        for (int f = 0; f < MF; ++f)
+        {
+            if (ms[f] == kNegInf) continue;  // a piece without a valid page (or past the row's pieces)
+            const float mn = fmaxf(m, ms[f]);
+            const float wa = __builtin_amdgcn_exp2f(m - mn);
+            const float wb = __builtin_amdgcn_exp2f(ms[f] - mn);
+            l = l * wa + ls[f] * wb;
+            o = o * wa + xs[f] * wb;
+            m = mn;
+        }
+    }
+    store_out4<QT>(a.out, (static_cast<size_t>(b) * a.num_heads + h) * D + d4,
+                   l > 0.0f ? o * (1.0f / l) : f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+}
+
 namespace
 {
 
@@ -768,11 +831,16 @@ hipError_t launch_m3(const DecodeArgs& a, hipStream_t stream)
     hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(items), static_cast<unsigned>(gy)), dim3(64 * nw), 0, stream, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    const dim3 mgrid(static_cast<unsigned>(a.batch), static_cast<unsigned>(a.num_heads));
-    if (a.batch <= 16)  // few rows over the same items: tens of pieces per row
+    if (a.batch <= FFKV_MERGE_ROWS_MIN_BATCH)  // few rows over the same items: tens of pieces per row
+    {
+        const dim3 mgrid(static_cast<unsigned>(a.batch), static_cast<unsigned>(a.num_heads));
         hipLaunchKernelGGL((paged_decode_mfma_merge<QT, D, 16>), mgrid, dim3(1024), 0, stream, a);
+    }
     else
-        hipLaunchKernelGGL((paged_decode_mfma_merge<QT, D, 4>), mgrid, dim3(256), 0, stream, a);
+    {
+        const dim3 mgrid(static_cast<unsigned>(a.batch), static_cast<unsigned>((a.num_heads * (D / 4) + 255) / 256));
+        hipLaunchKernelGGL((paged_decode_mfma_merge_rows<QT, D>), mgrid, dim3(256), 0, stream, a);
+    }
     return hipGetLastError();
 }
 
