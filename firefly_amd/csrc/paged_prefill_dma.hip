@@ -584,9 +584,14 @@ void paged_prefill_dma(PrefillArgs a)
     // denominator share the reference, so the result is the same softmax.
     float c_log2 = a.scale_log2;
     float v_head_scale = 1.0f;
+    float k_sign = 1.0f;  // fp8: the sign of the head's K scale, applied to the raw scores
     if constexpr (CT == FP8)  // per-head scales: K's into the score scale, V's onto the output
     {
-        c_log2 *= a.k_scale[kvh];
+        const float ks = a.k_scale[kvh];
+        k_sign = ks < 0.0f ? -1.0f : 1.0f;
+        // a zero scale (every score 0: uniform weights, as in decode) keeps a tiny positive factor, so the raw
+        // reference maximum, its threshold and masked keys' -inf scores stay well defined
+        c_log2 = fmaxf(c_log2 * __builtin_fabsf(ks), 1e-30f);
         v_head_scale = a.v_scale[kvh];
     }
     const float thr_raw = 8.0f / c_log2;
@@ -703,7 +708,7 @@ void paged_prefill_dma(PrefillArgs a)
 #pragma unroll
                     for (int i = 0; i < 4; ++i)
                     {
-                        sc[4 * u + i] = s[gi][u][i];
+                        sc[4 * u + i] = CT == FP8 ? s[gi][u][i] * k_sign : s[gi][u][i];
                         mt = fmaxf(mt, sc[4 * u + i]);
                     }
             }
@@ -716,7 +721,7 @@ void paged_prefill_dma(PrefillArgs a)
                     for (int i = 0; i < 4; ++i)
                     {
                         const bool vis = ((okm >> u) & 1) && u * kBlockSize + i < kr;
-                        sc[4 * u + i] = vis ? s[gi][u][i] : kNegInf;
+                        sc[4 * u + i] = vis ? (CT == FP8 ? s[gi][u][i] * k_sign : s[gi][u][i]) : kNegInf;
                         mt = fmaxf(mt, sc[4 * u + i]);
                     }
             }

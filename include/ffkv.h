@@ -185,7 +185,9 @@ FFKV_API int ffkv_paged_decode_shared_prefix(const void* q, void* out, int qo_dt
  * zeros.  With block_table == NULL, k_cache / v_cache are the chunk's contiguous [batch, seq_len, num_kv_heads,
  * head_dim] tensors and positions start at 0: the reference's causal prefill.  seq_len = 1 is decode attention.
  * cache_dtype F16, BF16, I8 or FP8_E4M3 (scales as for ffkv_paged_decode); any GQA group; scale <= 0 selects
- * 1/sqrt(head_dim).  No workspace; pointers 16-byte aligned.
+ * 1/sqrt(head_dim).  No workspace; pointers 16-byte aligned.  fp8 per-head K scales may be any finite value (0
+ * weighs the keys uniformly, a negative one negates the scores, as in decode).  Range limit of int8 caches: the
+ * attention weights meet their V scales in f16, so per-token V scales must stay below 256 (|V| below 32,512).
  */
 FFKV_API int ffkv_paged_prefill(const void* q, void* out, int qo_dtype, const void* k_cache, const void* v_cache,
                                 int cache_dtype, const float* k_scale, const float* v_scale, const int32_t* block_table,

@@ -178,3 +178,42 @@ def test_prefill_single_token_agrees_with_decode(ff, gpu):
     d = dec.float().cpu().numpy().reshape(got.shape)
     _check(got, ref, c.act, 2e-3)
     assert np.abs(d - got).max() <= 2 * 2e-3
+
+
+@pytest.mark.parametrize("k_scale_kind", ["zero", "negative"])
+def test_fp8_degenerate_k_scales(ff, gpu, k_scale_kind):
+    """fp8 per-head K scales of 0 (every score 0: uniform weights) and below 0 (the softmax of the negated scores)
+    give the checker's result in the prefill, the shared-prefix decode (whose prefix partials run the prefill
+    kernel) and the plain decode alike, instead of NaN."""
+    import torch
+
+    c, qn = _case(61, 3, 8, 2, 128, [40, 300, 17], 37, kv="fp8")
+    c.k_scale = c.k_scale.copy()
+    if k_scale_kind == "zero":
+        c.k_scale[:] = 0.0
+    else:
+        c.k_scale[0] = -c.k_scale[0]
+    # a scale of 0 stores zero codes on append; keep the pool's codes for the negative-scale case only
+    got, ref = _run(ff, gpu, c, qn)
+    assert np.isfinite(got).all()
+    _check(got, ref, c.act, 2e-2)
+
+    # decode over a 1-page shared prefix and the plain decode on the same pools
+    d = cases.make_case(62, 4, 8, 2, 128, [40, 90, 33, 70], act="bf16", kv="fp8", shared_prefix_blocks=1)
+    d.k_scale = d.k_scale.copy()
+    if k_scale_kind == "zero":
+        d.k_scale[:] = 0.0
+    else:
+        d.k_scale[1] = -d.k_scale[1]
+    kp, vp, ks, vs, _, out32 = cases.oracle_step(d)
+    dev = gpu
+    args = (gu.to_dev(d.q, d.act, dev), gu.to_dev(kp, d.kv, dev), gu.to_dev(vp, d.kv, dev),
+            torch.from_numpy(d.block_table).to(dev), torch.from_numpy(d.ctx).to(dev))
+    for shared in (0, 1):
+        out = (ff.paged_attention_shared_prefix(*args, shared, k_scale=torch.from_numpy(ks).to(dev),
+                                                v_scale=torch.from_numpy(vs).to(dev)) if shared else
+               ff.paged_attention(*args, k_scale=torch.from_numpy(ks).to(dev), v_scale=torch.from_numpy(vs).to(dev)))
+        torch.cuda.synchronize()
+        g = out.float().cpu().numpy().reshape(out32.shape)
+        assert np.isfinite(g).all(), f"shared={shared}"
+        _check(g, out32.astype(np.float64), d.act, 2e-2)
