@@ -460,6 +460,9 @@ def main(argv=None) -> int:
                     help="skip the other BASELINE configurations (C3, C4, C5 int8/fp8) and the rope+append figures")
     ap.add_argument("--configs", default="all",
                     help="comma-separated subset of C3,C5_int8,C5_fp8,C4,rope_append,C2_decode_step_host (default all)")
+    ap.add_argument("--skip-c2", action="store_true",
+                    help="skip the C2 steps, the device copy and the CPU baseline (profiling other configurations "
+                         "alone); the headline fields are then null")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run one 1 GiB device-to-device copy (a kernel of known read/write bytes, used to "
                          "scale rocprofv3 FETCH_SIZE/WRITE_SIZE counters)")
@@ -513,45 +516,47 @@ def main(argv=None) -> int:
         torch.cuda.synchronize()
         del src, dst
 
-    for i in range(args.warmup):
-        step(i)
-    torch.cuda.synchronize()
-
-    # Timed region: K steps, wall clock, synchronized on both sides.
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        step(i)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    ms_per_step = wall / args.steps * 1e3
-
-    # The same steps as two calls (ffkv_append, then ffkv_paged_decode), as the reference's model issues them.
-    for i in range(args.warmup):
-        step_separate(i)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        step_separate(i)
-    torch.cuda.synchronize()
-    ms_per_step_separate = (time.perf_counter() - t0) / args.steps * 1e3
-
-    # Per-call durations with HIP events on the launch stream (same loop, events around each call).
-    n_ev = args.steps
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(n_ev)]
-    for i in range(n_ev):
-        kp, vp = pools[i % args.layers]
-        ev[i][0].record(stream)
-        ff.append_kv_cache(k_new, v_new, kp, vp, table, ctx, stream=stream)
-        ev[i][1].record(stream)
-        ff.paged_attention(q, kp, vp, table, ctx, out=out, max_context_len=max_ctx, workspace=ws, stream=stream)
-        ev[i][2].record(stream)
-    torch.cuda.synchronize()
-    app_ms = float(np.mean([e[0].elapsed_time(e[1]) for e in ev]))
-    dec_ms = float(np.mean([e[1].elapsed_time(e[2]) for e in ev]))
-
+    ms_per_step = ms_per_step_separate = app_ms = dec_ms = achieved = None
     dbytes = decode_bytes(ctx_np)
     abytes = append_bytes(B, B)
-    achieved = dbytes / (dec_ms * 1e-3) / 1e12
+    if not args.skip_c2:
+        for i in range(args.warmup):
+            step(i)
+        torch.cuda.synchronize()
+
+        # Timed region: K steps, wall clock, synchronized on both sides.
+        t0 = time.perf_counter()
+        for i in range(args.steps):
+            step(i)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        ms_per_step = wall / args.steps * 1e3
+
+        # The same steps as two calls (ffkv_append, then ffkv_paged_decode), as the reference's model issues them.
+        for i in range(args.warmup):
+            step_separate(i)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(args.steps):
+            step_separate(i)
+        torch.cuda.synchronize()
+        ms_per_step_separate = (time.perf_counter() - t0) / args.steps * 1e3
+
+        # Per-call durations with HIP events on the launch stream (same loop, events around each call).
+        n_ev = args.steps
+        ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(n_ev)]
+        for i in range(n_ev):
+            kp, vp = pools[i % args.layers]
+            ev[i][0].record(stream)
+            ff.append_kv_cache(k_new, v_new, kp, vp, table, ctx, stream=stream)
+            ev[i][1].record(stream)
+            ff.paged_attention(q, kp, vp, table, ctx, out=out, max_context_len=max_ctx, workspace=ws, stream=stream)
+            ev[i][2].record(stream)
+        torch.cuda.synchronize()
+        app_ms = float(np.mean([e[0].elapsed_time(e[1]) for e in ev]))
+        dec_ms = float(np.mean([e[1].elapsed_time(e[2]) for e in ev]))
+
+        achieved = dbytes / (dec_ms * 1e-3) / 1e12
 
     # Bulk append: 64 sequences x 2048 new tokens into fresh pages (the KV-append GB/s figure).
     bulk = None
@@ -603,7 +608,7 @@ def main(argv=None) -> int:
             return 2
         configs = {name: makers[name]() for name in want}
 
-    copy_rate = device_copy_rate(torch, dev, stream)
+    copy_rate = None if args.skip_c2 else device_copy_rate(torch, dev, stream)
 
     # Layer-0 output for the parity figure and the CPU baseline on the same inputs.
     kp0, vp0 = pools[0]
@@ -611,13 +616,17 @@ def main(argv=None) -> int:
     torch.cuda.synchronize()
     cpu = None
     err = None
-    if args.cpu_seconds > 0:
+    if args.cpu_seconds > 0 and not args.skip_c2:
         cpu, err = cpu_baseline(ctx_np, table_np, N, kp0, vp0, q, out, args.cpu_seconds)
 
     traffic, traffic_commit = measured_traffic()
+
+    def per_s(amount, ms, unit):  # amount per second of a duration in ms, in `unit`s (None without the duration)
+        return None if ms is None else amount / (ms * 1e-3) / unit
+
     line = {
         "metric": "paged decode-attn HBM TB/s (% of peak) + tokens/s; KV-append GB/s, 1 GPU",
-        "value": (dbytes + abytes) / (ms_per_step * 1e-3) / 1e12,
+        "value": per_s(dbytes + abytes, ms_per_step, 1e12),
         "unit": "TB/s",
         "n_gpus": 1,
         "steps": args.steps,
@@ -631,16 +640,17 @@ def main(argv=None) -> int:
         "config": {"workload": "C2 Qwen3-8B layer: Hq32/Hkv8/D128 bf16, B=64, ctx U[512,4096], block 16, "
                                "append 1 token + decode per step",
                    "batch": B, "context_tokens": int(ctx_np.sum()) + B, "pool_blocks": N, "layers": args.layers},
-        "pct_of_peak": (dbytes + abytes) / (ms_per_step * 1e-3) / 1e12 / HBM_PEAK_TBS * 100,
-        "decode_tokens_per_s": B / (ms_per_step * 1e-3),
-        "decode_tokens_per_s_qwen3_8b_36_layers": B / (ms_per_step * 1e-3 * 36),
+        "pct_of_peak": per_s(dbytes + abytes, ms_per_step, HBM_PEAK_TBS * 1e10),
+        "decode_tokens_per_s": per_s(B, ms_per_step, 1),
+        "decode_tokens_per_s_qwen3_8b_36_layers": per_s(B, ms_per_step, 36),
         "decode_call_ms": dec_ms,
         "step_ms_two_calls": ms_per_step_separate,
-        "append_call_us": app_ms * 1e3,
+        "append_call_us": None if app_ms is None else app_ms * 1e3,
         "append_bulk": bulk,
         "roofline": {"kernel": "ffkv_paged_decode (paged_decode_mfma + paged_decode_mfma_merge)", "bound": "hbm",
-                     "achieved": achieved * 1e3, "peak": HBM_PEAK_TBS * 1e3, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_TBS, "traffic": traffic, "traffic_measured_at_commit": traffic_commit,
+                     "achieved": None if achieved is None else achieved * 1e3, "peak": HBM_PEAK_TBS * 1e3,
+                     "unit": "GB/s", "frac": None if achieved is None else achieved / HBM_PEAK_TBS,
+                     "traffic": traffic, "traffic_measured_at_commit": traffic_commit,
                      "algorithmic_bytes": dbytes},
         "device_copy": copy_rate,
         "other_configs": configs,
