@@ -18,7 +18,8 @@ Printed JSON line (rank 0, N = 1):
   parity         max-abs error of the layer-0 GPU output against that CPU result (fp32, before rounding)
   device_copy    a 1 GiB torch device copy timed the same way: the streaming rate a plain kernel reaches here
   other_configs  C3, C4 and C5 (int8 and fp8 pools filled by the quantizing append, whose bulk throughput is
-                 reported as quantized_append), the fused rope + append, and the decode step's host upload
+                 reported as quantized_append), the C4 prefill on every cache type and head_dim, a head_dim 256
+                 decode, the fused rope + append, and the decode step's host upload
 
 Algorithmic bytes per decode call (L'_b = context_lens[b] + 1):
   sum_b L'_b*Hkv*D*2*2 (K and V) + B*Hq*D*2*2 (q in, out) + sum_b ceil(L'_b/16)*4 (block table) + 4*B
@@ -332,6 +333,52 @@ def c4_config(ff, torch, dev, stream, layers=2, calls=30, seed=4):
     }
 
 
+def prefill_variants_config(ff, torch, dev, stream, layers=2, calls=30, seed=7):
+    """The C4 chunked prefill (8 rows x 512 new tokens over 2048 + U[64, 1024] cached tokens) on every cache type
+    and head_dim the prefill serves: bf16 / f16 / fp8 / int8 caches at head_dim 128 (Hq32/Hkv8; q in the cache's
+    16-bit type, bf16 for the 8-bit caches), and bf16 at head_dim 64 (Hq32/Hkv8) and 256 (Hq16/Hkv4).  16-bit pools
+    are random; 8-bit pools are filled by the quantizing append."""
+    import numpy as np
+
+    Bc, CH, PRE = 8, 512, 2048
+    out = {}
+    for name, kv, D, Hq, Hkv in (("bf16_d128", "bf16", 128, 32, 8), ("f16_d128", "f16", 128, 32, 8),
+                                 ("fp8_d128", "fp8", 128, 32, 8), ("i8_d128", "i8", 128, 32, 8),
+                                 ("bf16_d64", "bf16", 64, 32, 8), ("bf16_d256", "bf16", 256, 16, 4)):
+        rng = np.random.default_rng(seed)
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(seed)
+        ctx = (PRE + rng.integers(64, 1025, size=Bc)).astype(np.int32)
+        need = [math.ceil((int(c) + CH) / BLOCK) for c in ctx]
+        table_np, N = _tables(rng, need)
+        bt = torch.from_numpy(table_np).to(dev)
+        cx = torch.from_numpy(ctx).to(dev)
+        qt = torch.float16 if kv == "f16" else torch.bfloat16
+        if kv in ("bf16", "f16"):
+            shape = (N, BLOCK, Hkv, D)
+            pools = [(torch.randn(shape, generator=gen, device=dev).to(qt),
+                      torch.randn(shape, generator=gen, device=dev).to(qt), None, None) for _ in range(layers)]
+        else:
+            pools, _ = _appended_pools(ff, torch, gen, dev, stream, N, Hkv, D, kv, layers, bt,
+                                       [int(c) + CH for c in ctx])
+        q = torch.randn((Bc, CH, Hq, D), generator=gen, device=dev).to(qt)
+        o = torch.empty((Bc, CH, Hq * D), device=dev, dtype=qt)
+
+        def pre(i):
+            kp, vp, ks, vs = pools[i % layers]
+            ff.paged_prefill(q, kp, vp, bt, cx, out=o, k_scale=ks, v_scale=vs, stream=stream)
+
+        us = _events_us(pre, calls, stream)
+        flops = sum((int(c) + t + 1) * Hq * D * 4 for c in ctx for t in range(CH))
+        out[name] = {"kv": kv, "q": "f16" if kv == "f16" else "bf16", "heads": f"{Hq}/{Hkv}", "head_dim": D,
+                     "us_per_call": us, "causal_flops": flops, "TFLOP_per_s": flops / (us * 1e-6) / 1e12,
+                     "pct_of_16bit_mfma_peak": flops / (us * 1e-6) / 1e12 / BF16_MFMA_PEAK_TFLOPS * 100}
+        del pools, q, o
+        torch.cuda.empty_cache()
+    return {"workload": "chunked prefill, 8 rows x 512 tokens over 2048 + U[64,1024] cached tokens, per cache "
+                        "type and head_dim", **out}
+
+
 def rope_append_config(ff, torch, dev, stream, calls=50, seed=5):
     """Fused rotary embedding + KV append: the C2 decode-step shape (64 tokens) and a bulk 64 x 2048 prefill."""
     import numpy as np
@@ -459,7 +506,8 @@ def main(argv=None) -> int:
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the other BASELINE configurations (C3, C4, C5 int8/fp8) and the rope+append figures")
     ap.add_argument("--configs", default="all",
-                    help="comma-separated subset of C3,C5_int8,C5_fp8,C4,rope_append,C2_decode_step_host (default all)")
+                    help="comma-separated subset of C3,C5_int8,C5_fp8,C4,prefill_variants,decode_d256,rope_append,"
+                         "C2_decode_step_host (default all)")
     ap.add_argument("--skip-c2", action="store_true",
                     help="skip the C2 steps, the device copy and the CPU baseline (profiling other configurations "
                          "alone); the headline fields are then null")
@@ -596,11 +644,15 @@ def main(argv=None) -> int:
             "C5_fp8": lambda: decode_config(ff, torch, dev, stream, "C5 fp8 e4m3 KV (per-head scales): Hq32/Hkv8/D128, "
                                             "B=256, ctx U[1024,8192]", 256, 32, 8, 128, c5_ctx[1], kv="fp8", seed=6),
             "C4": lambda: c4_config(ff, torch, dev, stream),
+            "prefill_variants": lambda: prefill_variants_config(ff, torch, dev, stream),
+            "decode_d256": lambda: decode_config(ff, torch, dev, stream, "head_dim 256 decode: Hq16/Hkv4/D256 bf16, "
+                                                 "B=64, ctx U[512,4096]", 64, 16, 4, 256, d256_ctx, seed=8),
             "rope_append": lambda: rope_append_config(ff, torch, dev, stream),
             "C2_decode_step_host": lambda: decode_step_config(ff, torch, dev, stream, ctx_np, table_np, N, pools, q,
                                                               k_new, v_new, out, ws, max_ctx),
         }
         c5_ctx = [rng.integers(1024, 8193, size=256), rng.integers(1024, 8193, size=256)]
+        d256_ctx = rng.integers(512, 4097, size=64)
         want = list(makers) if args.configs == "all" else [x for x in args.configs.split(",") if x]
         unknown = [x for x in want if x not in makers]
         if unknown:

@@ -186,9 +186,9 @@ def test_generic_and_mfma_kernels_agree(ff, gpu):
 
 
 def test_workspace_reused_across_calls(ff, gpu):
-    """One workspace, filled with garbage first, serves consecutive calls of different shapes, in-kernel merge
-    (B=64) and merge-kernel (B=5) calls alternating, so each call finds the other layout's data where its
-    arrival counters live."""
+    """One workspace, filled with garbage first, serves consecutive calls of different shapes: B=64 (split-K
+    partials folded by the per-row merge) and B=5 (folded by the per-(row, head) merge) alternating, so each call
+    finds the other layout's partials and metadata in its slots and must overwrite every entry it reads."""
     import torch
 
     import gpu_util as gu
