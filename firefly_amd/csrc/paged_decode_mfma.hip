@@ -18,7 +18,8 @@
 //     layout (k = token = 4g + i), V^T comes from an LDS copy of the page's V rows whose 16-byte chunks are
 //     XOR-swizzled per token, so both the 16-byte row writes and the transposing column reads are free of bank
 //     conflicts while every row stays 16-byte aligned.
-//     P is split into hi + lo parts of the MFMA input type, so the products carry ~16 significant bits.
+//     bf16 P is split into hi + lo parts, so the products carry ~16 significant bits; f16 P (f16 caches, and the
+//     f16 PV products of 8-bit caches) is one product of 11 bits.
 //   * quantized caches: int8 and fp8 e4m3 codes convert exactly to the MFMA input type when a page is staged
 //     (fp8 with the gfx950 conversion instructions, int8 with byte permutes and packed f16 ops); int8 per-token
 //     K scales multiply the scores and V scales multiply P, fp8 per-head scales fold into the score scale and
@@ -71,6 +72,10 @@ struct PageRegs
 #ifndef FFKV_MFMA_DEPTH16
 #define FFKV_MFMA_DEPTH16 2  // pages in flight per wave: 16-bit caches
 #endif
+#ifndef FFKV_DECODE_V16
+#define FFKV_DECODE_V16 1  // 8-bit caches: PV products in f16 (P in one product)
+#endif
+
 #ifndef FFKV_MFMA_DEPTH_FP8
 #define FFKV_MFMA_DEPTH_FP8 2  // fp8 caches
 #endif
@@ -123,12 +128,19 @@ template <int CT, int QT, int D>
 __global__ __launch_bounds__(64 * FFKV_MFMA_MAX_WAVES) __attribute__((amdgpu_waves_per_eu(kMfmaWaves<CT, QT, D>, 8)))
 void paged_decode_mfma(DecodeArgs a)
 {
+    // Score products in M (BF: bf16, else f16); PV products in MV.  8-bit codes are exact in both types, so their
+    // PV products take f16, where P fits one product (11 bits) instead of a bf16 hi + lo pair; bf16 caches keep
+    // bf16 P as hi + lo.  (int8 scores stay f16 with q split in two: bf16 scores, q whole, measured 20 % slower
+    // on C5 from the extra conversion registers.)
     constexpr bool BF = kBF<CT, QT>;
+    constexpr bool VBF = CT == BF16 || (kElemBytes<CT> == 1 && BF && !FFKV_DECODE_V16);
     using M = MType<BF>;
+    using MV = MType<VBF>;
     using X8 = typename M::x8;
     constexpr int  KSTEPS = D / 32;
     constexpr int  NT = D / 16;  // output tiles of 16 dims
     constexpr bool NEED_LO = !((QT == BF16 && BF) || (QT == F16 && !BF));
+    constexpr bool P_LO = VBF;  // bf16 P: hi + lo parts
     constexpr int  DEPTH = kMfmaDepth<CT, D>;
     constexpr int  NW = kElemBytes<CT> == 2 ? KSTEPS : KSTEPS / 2;
 
@@ -410,12 +422,14 @@ void paged_decode_mfma(DecodeArgs a)
     f32x4 acc[NT];
 
     // K or V words of k-step j in the MFMA input type.
-    auto mword = [&](const u32x4* w, int j) -> u32x4
+    // k-step j's 8 values as MFMA words: of type bf16 (TBF) or f16 for 8-bit codes
+    auto mword = [&]<bool TBF>(const u32x4* w, int j) -> u32x4
     {
         if constexpr (kElemBytes<CT> == 2)
             return w[j];
         else
-            return (j & 1) ? codes_to_m<CT, BF>(w[j / 2][2], w[j / 2][3]) : codes_to_m<CT, BF>(w[j / 2][0], w[j / 2][1]);
+            return (j & 1) ? codes_to_m<CT, TBF>(w[j / 2][2], w[j / 2][3])
+                           : codes_to_m<CT, TBF>(w[j / 2][0], w[j / 2][1]);
     };
 
     // Stage a loaded page: V rows into the wave's LDS tile, scores S^T = K Q^T into s.  Consumes r.k and r.v,
@@ -441,7 +455,7 @@ void paged_decode_mfma(DecodeArgs a)
 #pragma unroll
         for (int j = 0; j < KSTEPS; ++j)
         {
-            const u32x4 w = tok_ok ? mword(r.v, j) : u32x4{0u, 0u, 0u, 0u};
+            const u32x4 w = tok_ok ? mword.template operator()<VBF>(r.v, j) : u32x4{0u, 0u, 0u, 0u};
 #if FFKV_DECODE_TRV
             *reinterpret_cast<u32x4*>(sv + vt_pos<D>(c, dim_of<CT>(j, g))) = w;
 #else
@@ -452,7 +466,7 @@ void paged_decode_mfma(DecodeArgs a)
 #pragma unroll
         for (int j = 0; j < KSTEPS; ++j)
         {
-            const X8 kj = __builtin_bit_cast(X8, mword(r.k, j));
+            const X8 kj = __builtin_bit_cast(X8, mword.template operator()<BF>(r.k, j));
             s = M::mma32(kj, qhi[j], s);
             if constexpr (NEED_LO) s = M::mma32(kj, qlo[j], s);
         }
@@ -506,18 +520,18 @@ void paged_decode_mfma(DecodeArgs a)
         }
         m_run = m_new;
 
-        // P^T as MFMA B operands (k = token 4g + i, column c = head), hi + lo parts
+        // P^T as MFMA B operands (k = token 4g + i, column c = head); bf16 P as hi + lo parts
         uint32_t ph[4], pl[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i)
         {
-            ph[i] = M::bits(pv[i]);
-            pl[i] = M::bits(pv[i] - M::value(ph[i]));
+            ph[i] = MV::bits(pv[i]);
+            pl[i] = P_LO ? MV::bits(pv[i] - MV::value(ph[i])) : 0u;
         }
-        const typename M::x4 phi =
-            __builtin_bit_cast(typename M::x4, u32x2{ph[0] | (ph[1] << 16), ph[2] | (ph[3] << 16)});
-        const typename M::x4 plo =
-            __builtin_bit_cast(typename M::x4, u32x2{pl[0] | (pl[1] << 16), pl[2] | (pl[3] << 16)});
+        const typename MV::x4 phi =
+            __builtin_bit_cast(typename MV::x4, u32x2{ph[0] | (ph[1] << 16), ph[2] | (ph[3] << 16)});
+        const typename MV::x4 plo =
+            __builtin_bit_cast(typename MV::x4, u32x2{pl[0] | (pl[1] << 16), pl[2] | (pl[3] << 16)});
 
         // LDS writes of this wave are complete before its reads below (in-order LDS queue of one wave);
         // the fence keeps the compiler from moving the reads above the writes.
@@ -534,16 +548,16 @@ void paged_decode_mfma(DecodeArgs a)
             // receives dim 16n + c of tokens 4g .. 4g + 3
             const auto raw = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
                 (__attribute__((address_space(3))) bf16x4*)(sv + vt_pos<D>(4 * g + (c >> 2), 16 * n + 4 * (c & 3))));
-            const typename M::x4 vt = __builtin_bit_cast(typename M::x4, raw);
+            const typename MV::x4 vt = __builtin_bit_cast(typename MV::x4, raw);
 #else
             const uint32_t v0 = sv[lds_pos<D>(4 * g + 0, 16 * n + c)];
             const uint32_t v1 = sv[lds_pos<D>(4 * g + 1, 16 * n + c)];
             const uint32_t v2 = sv[lds_pos<D>(4 * g + 2, 16 * n + c)];
             const uint32_t v3 = sv[lds_pos<D>(4 * g + 3, 16 * n + c)];
-            const typename M::x4 vt = __builtin_bit_cast(typename M::x4, u32x2{v0 | (v1 << 16), v2 | (v3 << 16)});
+            const typename MV::x4 vt = __builtin_bit_cast(typename MV::x4, u32x2{v0 | (v1 << 16), v2 | (v3 << 16)});
 #endif
-            acc[n] = M::mma16(vt, phi, acc[n]);
-            acc[n] = M::mma16(vt, plo, acc[n]);
+            acc[n] = MV::mma16(vt, phi, acc[n]);
+            if constexpr (P_LO) acc[n] = MV::mma16(vt, plo, acc[n]);
         }
         // the next page's LDS writes must not overtake these reads
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");

@@ -38,8 +38,10 @@
 // the K operand is an 8-byte read of 8 codes, the V^T operand one ds_read_b64_tr_b8 (within each 16-lane group,
 // lanes 2r and 2r + 1 supply the two halves of key row r's 16 dims, and lane j receives dim j of rows 0..7,
 // which are the 8 keys of one k-slot group), both turned into 8 MFMA-type values by the gfx950 conversions.
-// int8 per-token scales (fp32 [N, 16, Hkv]) travel with their page into the stage by 4-byte loads; fp8 per-head
-// scales fold into the score scale and the output.
+// Under a bf16 q the score products are bf16 (q whole), and the PV products f16: the codes are exact in both
+// types, and f16's 11 bits hold P in one product where bf16 P needs a hi + lo pair (C4-shaped prefill: fp8 300 ->
+// 240 us, int8 356 -> 333 us).  int8 per-token scales (fp32 [N, 16, Hkv]) travel with their page into the stage
+// by 4-byte loads; fp8 per-head scales fold into the score scale and the output.
 //
 // Keys past the row's end and keys on invalid pages are fetched from a zero block instead, so masked keys meet
 // zero V rows (their probabilities are exactly zero) and no lane reads outside the cache.
@@ -73,7 +75,7 @@ constexpr int kXcds = 8;  // MI355X: workgroups are dealt to 8 XCDs (separate L2
 #endif
 
 #ifndef FFKV_PREFILL_I8_BF
-#define FFKV_PREFILL_I8_BF 0  // int8 with bf16 q: f16 MFMAs with q split (measured faster than bf16 MFMAs with P split)
+#define FFKV_PREFILL_I8_BF 1  // int8 with bf16 q: bf16 score products (q whole) and f16 PV products (P whole)
 #endif
 
 #ifndef FFKV_PREFILL_RG
@@ -90,6 +92,10 @@ constexpr int kXcds = 8;  // MI355X: workgroups are dealt to 8 XCDs (separate L2
 
 #ifndef FFKV_PREFILL_DMA_KP256
 #define FFKV_PREFILL_DMA_KP256 4  // pages per step at head_dim 256 (the shared-prefix partials take 2)
+#endif
+
+#ifndef FFKV_PREFILL_V16
+#define FFKV_PREFILL_V16 1  // PV products in f16 for 8-bit caches whose score products are bf16
 #endif
 
 #define FFKV_LDS __attribute__((address_space(3)))
@@ -234,7 +240,7 @@ void paged_prefill_dma(PrefillArgs a)
     constexpr int  W = 8 / RG;  // waves per workgroup
     constexpr int  EB = kElemBytes<CT>;
     constexpr bool Q8 = EB == 1;
-    // int8 codes take bf16 MFMAs beside a bf16 q (exact: 8 significant bits), so q needs no hi / lo split
+    // int8 codes take bf16 score products beside a bf16 q (exact: 8 significant bits), so q needs no hi / lo split
     constexpr bool BF = CT == I8 ? (FFKV_PREFILL_I8_BF && QT != F16) : kBF<CT, QT>;
     using C = DmaCfg<D, EB, CT == I8, W, PFX>;  // the scale bytes (and their loads, counted in the waits) only for int8
     using M = MType<BF>;
@@ -248,6 +254,9 @@ void paged_prefill_dma(PrefillArgs a)
     // prefill it is 2-6 % faster for f16 / f32 queries, int8 caches and head_dim 64 / 256, and 2-3 % slower for
     // bf16 queries over bf16 / fp8 caches at head_dim 128, where the per-run form stays.
     constexpr bool PAGE_ISSUE = !PFX && !(QT == BF16 && D == 128 && CT != I8);
+    // 8-bit codes are exact in f16 as in bf16: with bf16 score products (BF), their PV products still take f16
+    // V^T and P^T, so P needs one product instead of a bf16 hi + lo pair.
+    constexpr bool V16 = FFKV_PREFILL_V16 && Q8 && BF;
 
     // NS stages (three by default), each [K tile | V tile | int8 scales] of KP pages, key-major, swizzled chunks
     __shared__ __align__(16) uint8_t s_st0[2 * C::TILEB + C::SCB];
@@ -597,14 +606,6 @@ void paged_prefill_dma(PrefillArgs a)
     const float thr_raw = 8.0f / c_log2;
     float       m_run[RG], l_run[RG];
     f32x4       acc[RG][NT];
-#pragma unroll
-    for (int gi = 0; gi < RG; ++gi)
-    {
-        m_run[gi] = kNegInf;
-        l_run[gi] = 0.0f;
-#pragma unroll
-        for (int n = 0; n < NT; ++n) acc[gi][n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    }
 
     // Smallest causal limit over the wave's active columns: steps wholly below it need no mask.
     int kmin = INT32_MAX;
@@ -689,13 +690,12 @@ void paged_prefill_dma(PrefillArgs a)
         }
     };
 
-    // Online softmax of a step's scores and O^T += V^T P^T from its stage.
-    auto softmax_pv = [&](int si, const uint8_t* stage, int okm, const f32x4 (&s)[RG][KP])
+    // Online softmax of a step's scores: the probabilities pv (int8: times the keys' V scales).
+    auto softmax = [&](int si, const uint8_t* stage, int okm, const f32x4 (&s)[RG][KP], float (&pv)[RG][KP * 4])
     {
         const int pg0 = pg_lo + si * KP;
         // uniform: every key of the step is visible to every column of the wave
         const bool unmasked = okm == (1 << KP) - 1 && (pg0 + KP) * kBlockSize <= kmin;
-        float      pv[RG][KP * 4];
 #pragma unroll
         for (int gi = 0; gi < RG; ++gi)
         {
@@ -756,15 +756,23 @@ void paged_prefill_dma(PrefillArgs a)
                     for (int i = 0; i < 4; ++i) pv[gi][4 * u + i] *= vsc[i];
             }
         }
+    };
 
-        auto vread = [&](int n, int u0) -> X8  // V^T operand of output tile n over pages u0, u0 + 1
+    // O^T += V^T P^T from the stage.  V16: the products take f16 V^T (codes converted to f16) and P^T, with P in
+    // one product (11 bits); otherwise bf16 P is a hi + lo pair, which keeps 16 significant bits in two products.
+    auto pv_mma = [&]<bool V16>(const uint8_t* stage, const float (&pv)[RG][KP * 4])
+    {
+        constexpr bool PBF = BF && !V16;  // P^T and V^T operand type
+        using MP = MType<PBF>;
+        using XP = typename MP::x8;
+        auto vread = [&](int n, int u0) -> XP  // V^T operand of output tile n over pages u0, u0 + 1
         {
             if constexpr (Q8)
             {
                 const auto raw = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
                     (FFKV_LDS i32x2*)(stage + u0 * kBlockSize * C::RB + v8base + ((n ^ v8sw) << 4)));
                 const u32x2 w = __builtin_bit_cast(u32x2, raw);
-                return __builtin_bit_cast(X8, codes_to_m<CT, BF>(w[0], w[1]));
+                return __builtin_bit_cast(XP, codes_to_m<CT, PBF>(w[0], w[1]));
             }
             else
             {
@@ -775,15 +783,15 @@ void paged_prefill_dma(PrefillArgs a)
                     (FFKV_LDS bf16x4*)(stage + (u0 + 1) * kBlockSize * C::RB + off));
                 const u32x2 w0 = __builtin_bit_cast(u32x2, a0);
                 const u32x2 w1 = __builtin_bit_cast(u32x2, a1);
-                return __builtin_bit_cast(X8, u32x4{w0[0], w0[1], w1[0], w1[1]});
+                return __builtin_bit_cast(XP, u32x4{w0[0], w0[1], w1[0], w1[1]});
             }
         };
 #pragma unroll
         for (int u0 = 0; u0 < KP; u0 += 2)
         {
             // P^T operands: pairs of p rounded to the MFMA type (packed conversions); for bf16 also the residual
-            // p - hi, which keeps 16 significant bits in two products (f16's 11 bits suffice in one).
-            X8 phi[RG], plo[RG];
+            // p - hi.
+            XP phi[RG], plo[RG];
 #pragma unroll
             for (int gi = 0; gi < RG; ++gi)
             {
@@ -792,7 +800,7 @@ void paged_prefill_dma(PrefillArgs a)
                 for (int e = 0; e < 4; ++e)
                 {
                     const f32x2 v = f32x2{pv[gi][4 * u0 + 2 * e], pv[gi][4 * u0 + 2 * e + 1]};
-                    if constexpr (BF)
+                    if constexpr (PBF)
                     {
                         ph[e] = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
                         const f32x2 r = f32x2{v[0] - __builtin_bit_cast(float, ph[e] << 16),
@@ -805,22 +813,22 @@ void paged_prefill_dma(PrefillArgs a)
                         pl[e] = 0u;
                     }
                 }
-                phi[gi] = __builtin_bit_cast(X8, u32x4{ph[0], ph[1], ph[2], ph[3]});
-                plo[gi] = __builtin_bit_cast(X8, u32x4{pl[0], pl[1], pl[2], pl[3]});
+                phi[gi] = __builtin_bit_cast(XP, u32x4{ph[0], ph[1], ph[2], ph[3]});
+                plo[gi] = __builtin_bit_cast(XP, u32x4{pl[0], pl[1], pl[2], pl[3]});
             }
             // every V^T operand read from LDS feeds the products of all RG row groups
             mfma_priority<Q8>(1);
-            X8 vcur = vread(0, u0);
+            XP vcur = vread(0, u0);
 #pragma unroll
             for (int n = 0; n < NT; ++n)
             {
-                X8 vnxt{};
+                XP vnxt{};
                 if (n + 1 < NT) vnxt = vread(n + 1, u0);  // next tile's reads in flight behind this tile's products
 #pragma unroll
                 for (int gi = 0; gi < RG; ++gi)
                 {
-                    acc[gi][n] = M::mma32(vcur, phi[gi], acc[gi][n]);
-                    if constexpr (BF) acc[gi][n] = M::mma32(vcur, plo[gi], acc[gi][n]);
+                    acc[gi][n] = MP::mma32(vcur, phi[gi], acc[gi][n]);
+                    if constexpr (PBF) acc[gi][n] = MP::mma32(vcur, plo[gi], acc[gi][n]);
                 }
                 vcur = vnxt;
             }
@@ -833,6 +841,14 @@ void paged_prefill_dma(PrefillArgs a)
     // reads), so "step si has landed" is always vmcnt <= the loads of steps si + 1 .. si + NS - 2.
     constexpr int NS = kDmaStages<D>;
     constexpr int LPS = C::RPW + C::SCB / 256;  // loads per wave and step
+#pragma unroll
+    for (int gi = 0; gi < RG; ++gi)
+    {
+        m_run[gi] = kNegInf;
+        l_run[gi] = 0.0f;
+#pragma unroll
+        for (int n = 0; n < NT; ++n) acc[gi][n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
     // The scores' products are issued before the next loads' scalar address work, which then runs while they
     // execute.
     auto body = [&](int si, uint8_t* cur, int okm_cur, uint8_t* nxt, int& okm_nxt)
@@ -842,7 +858,12 @@ void paged_prefill_dma(PrefillArgs a)
         f32x4 sx[RG][KP];
         if (wave_active) qk(cur, sx);
         okm_nxt = issue(si + NS - 1, nxt);
-        if (wave_active) softmax_pv(si, cur, okm_cur, sx);
+        if (wave_active)
+        {
+            float pv[RG][KP * 4];
+            softmax(si, cur, okm_cur, sx, pv);
+            pv_mma.template operator()<V16>(cur, pv);
+        }
     };
 
     int okm0 = issue(0, s_st0);

@@ -217,3 +217,34 @@ def test_fp8_degenerate_k_scales(ff, gpu, k_scale_kind):
         g = out.float().cpu().numpy().reshape(out32.shape)
         assert np.isfinite(g).all(), f"shared={shared}"
         _check(g, out32.astype(np.float64), d.act, 2e-2)
+
+
+@pytest.mark.parametrize("big", [7.0e4, 3.0e5, float("inf")])
+def test_prefill_bf16_large_v(ff, gpu, big):
+    """V values far beyond the N(0,1) data (and beyond f16's range, so no product may pass through f16): row 1,
+    kv head 3 gets them in its cached pages and in its chunk.  Its outputs must match the float64 closed form
+    relative to the row's largest |v| (infinite V: the same non-finite outputs as the closed form), and rows 0
+    and 2 keep the ordinary bar."""
+    c, qn = _case(150, 3, 32, 8, 128, [17, 300, 5], 37)
+    rng = np.random.default_rng(151)
+    vals = np.array([big, -big, big / 3], np.float32)
+    enc = cases.encode(vals, O.DTYPE_BF16)
+    # cached tokens of row 1 (pages of its block table), kv head 3
+    for t in rng.choice(300, size=6, replace=False):
+        page, slot = c.block_table[1, t // 16], t % 16
+        c.v_pool[page, slot, 3, rng.integers(0, 128)] = enc[rng.integers(0, 3)]
+    c.v_new[1, 5, 3, 7] = enc[0]
+    got, ref = _run(ff, gpu, c, qn)
+    for b in (0, 2):
+        _check(got[b:b + 1], ref[b:b + 1], c.act, 2e-3)
+    g1, r1 = got[1].astype(np.float64), ref[1]
+    fin = np.isfinite(r1)
+    assert np.array_equal(np.isfinite(g1), fin), "non-finite outputs differ from the closed form"
+    if np.isfinite(big):
+        scale = max(1.0, big)
+        err = float(np.abs(g1 - r1).max())
+        print(f"  row 1 max-abs err {err:.3e} against |v| up to {scale:.1e}", flush=True)
+        assert err <= 2e-3 * scale
+    else:
+        # kv head 3's heads (12..15) hold the infinities; the other heads keep the ordinary bar
+        _check(got[1][:, :12], ref[1][:, :12], c.act, 2e-3)
