@@ -45,7 +45,11 @@ int ok()
 bool is_act(int dt) { return dt == FFKV_DTYPE_F32 || dt == FFKV_DTYPE_F16 || dt == FFKV_DTYPE_BF16; }
 bool is_cache(int dt) { return is_act(dt) || dt == FFKV_DTYPE_I8 || dt == FFKV_DTYPE_FP8_E4M3; }
 bool quantized(int dt) { return dt == FFKV_DTYPE_I8 || dt == FFKV_DTYPE_FP8_E4M3; }
-bool head_dim_ok(int d) { return d == 64 || d == 128 || d == 256; }
+// Append and decode take any head_dim that is a multiple of 8 up to 128 (as the reference's decode, one 8-element
+// vector per lane of a 16-lane group: src/kernels/attention.cu:307-316), and 256; prefill and rope+append take 64,
+// 128 and 256 (the reference's prefill and rope take 128, and 64 / 128).
+bool head_dim_ok(int d) { return d == 256 || (d >= 8 && d <= 128 && d % 8 == 0); }
+bool head_dim_mfma(int d) { return d == 64 || d == 128 || d == 256; }
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
@@ -83,9 +87,9 @@ int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
 namespace ffkv
 {
 
-bool decode_use_mfma(int cache_dtype, int /*group*/)
+bool decode_use_mfma(int cache_dtype, int /*group*/, int head_dim)
 {
-    return !env_force_generic() && cache_dtype != FFKV_DTYPE_F32;
+    return !env_force_generic() && cache_dtype != FFKV_DTYPE_F32 && head_dim_mfma(head_dim);
 }
 
 // MFMA workspace layout: [row meta: batch x 2 int32 | (m, l): slots x num_heads x 2 fp32 | acc: slots x num_heads
@@ -216,7 +220,8 @@ int ffkv_append(const void* k_src, const void* v_src, int src_dtype, void* k_cac
     if (block_size != FFKV_BLOCK_SIZE) return fail(FFKV_ERR_UNSUPPORTED, "block_size must be 16, got %d", block_size);
     if (!is_act(src_dtype)) return fail(FFKV_ERR_UNSUPPORTED, "unsupported source dtype %d", src_dtype);
     if (!is_cache(cache_dtype)) return fail(FFKV_ERR_UNSUPPORTED, "unsupported cache dtype %d", cache_dtype);
-    if (!head_dim_ok(head_dim)) return fail(FFKV_ERR_UNSUPPORTED, "head_dim must be 64, 128 or 256, got %d", head_dim);
+    if (!head_dim_ok(head_dim))
+        return fail(FFKV_ERR_UNSUPPORTED, "head_dim must be a multiple of 8 up to 128, or 256, got %d", head_dim);
     if (batch < 0 || seq_len < 0 || num_kv_heads <= 0 || max_blocks < 0 || num_blocks < 0)
         return fail(FFKV_ERR_INVALID_ARGUMENT, "negative size (batch %d seq_len %d kv_heads %d max_blocks %d "
                     "num_blocks %d)", batch, seq_len, num_kv_heads, max_blocks, num_blocks);
@@ -248,7 +253,7 @@ int ffkv_paged_prefill(const void* q, void* out, int qo_dtype, const void* k_cac
     if (!is_cache(cache_dtype) || cache_dtype == FFKV_DTYPE_F32)
         return fail(FFKV_ERR_UNSUPPORTED, "prefill supports F16, BF16, I8 and FP8_E4M3 caches, got dtype %d",
                     cache_dtype);
-    if (!head_dim_ok(head_dim)) return fail(FFKV_ERR_UNSUPPORTED, "head_dim must be 64, 128 or 256, got %d", head_dim);
+    if (!head_dim_mfma(head_dim)) return fail(FFKV_ERR_UNSUPPORTED, "head_dim must be 64, 128 or 256, got %d", head_dim);
     if (batch < 0 || seq_len < 0 || num_heads <= 0 || num_kv_heads <= 0 || (paged && (max_blocks < 0 || num_blocks < 0)))
         return fail(FFKV_ERR_INVALID_ARGUMENT, "bad size (batch %d seq_len %d heads %d kv_heads %d max_blocks %d "
                     "num_blocks %d)", batch, seq_len, num_heads, num_kv_heads, max_blocks, num_blocks);
@@ -317,7 +322,7 @@ int ffkv_rope_append(void* q, void* k, const void* v, int src_dtype, void* k_cac
     if (block_size != FFKV_BLOCK_SIZE) return fail(FFKV_ERR_UNSUPPORTED, "block_size must be 16, got %d", block_size);
     if (!is_act(src_dtype)) return fail(FFKV_ERR_UNSUPPORTED, "unsupported q/k/v dtype %d", src_dtype);
     if (append && !is_cache(cache_dtype)) return fail(FFKV_ERR_UNSUPPORTED, "unsupported cache dtype %d", cache_dtype);
-    if (!head_dim_ok(head_dim)) return fail(FFKV_ERR_UNSUPPORTED, "head_dim must be 64, 128 or 256, got %d", head_dim);
+    if (!head_dim_mfma(head_dim)) return fail(FFKV_ERR_UNSUPPORTED, "head_dim must be 64, 128 or 256, got %d", head_dim);
     if (q == nullptr) num_heads = 0;
     if (batch < 0 || seq_len < 0 || num_heads < 0 || num_kv_heads <= 0 || max_blocks < 0 || num_blocks < 0)
         return fail(FFKV_ERR_INVALID_ARGUMENT, "negative size (batch %d seq_len %d heads %d kv_heads %d max_blocks %d "
@@ -414,7 +419,8 @@ int decode_impl(const void* q, void* out, int qo_dtype, const void* k_cache, con
     if (block_size != FFKV_BLOCK_SIZE) return fail(FFKV_ERR_UNSUPPORTED, "block_size must be 16, got %d", block_size);
     if (!is_act(qo_dtype)) return fail(FFKV_ERR_UNSUPPORTED, "unsupported q/out dtype %d", qo_dtype);
     if (!is_cache(cache_dtype)) return fail(FFKV_ERR_UNSUPPORTED, "unsupported cache dtype %d", cache_dtype);
-    if (!head_dim_ok(head_dim)) return fail(FFKV_ERR_UNSUPPORTED, "head_dim must be 64, 128 or 256, got %d", head_dim);
+    if (!head_dim_ok(head_dim))
+        return fail(FFKV_ERR_UNSUPPORTED, "head_dim must be a multiple of 8 up to 128, or 256, got %d", head_dim);
     if (batch < 0 || num_heads <= 0 || num_kv_heads <= 0 || max_blocks < 0 || num_blocks < 0)
         return fail(FFKV_ERR_INVALID_ARGUMENT, "bad size (batch %d heads %d kv_heads %d max_blocks %d num_blocks %d)",
                     batch, num_heads, num_kv_heads, max_blocks, num_blocks);
@@ -423,7 +429,7 @@ int decode_impl(const void* q, void* out, int qo_dtype, const void* k_cache, con
                     num_kv_heads);
     const int group = num_heads / num_kv_heads;
     // the matrix-core decode takes any group (one wave per block of 16 query heads); the fp32-cache kernel 16 at most
-    if (group > 16 && !ffkv::decode_use_mfma(cache_dtype, group))
+    if (group > 16 && !ffkv::decode_use_mfma(cache_dtype, group, head_dim))
         return fail(FFKV_ERR_UNSUPPORTED, "GQA group size %d exceeds 16 (fp32 caches, or the generic decode forced)",
                     group);
     if (batch > 65535 || num_heads > 65535)
@@ -443,7 +449,7 @@ int decode_impl(const void* q, void* out, int qo_dtype, const void* k_cache, con
     if (shared_blocks < 0 || shared_blocks > max_blocks)
         return fail(FFKV_ERR_INVALID_ARGUMENT, "shared_blocks %d outside 0 .. max_blocks %d", shared_blocks,
                     max_blocks);
-    const bool mfma = ffkv::decode_use_mfma(cache_dtype, group);
+    const bool mfma = ffkv::decode_use_mfma(cache_dtype, group, head_dim);
     // shared-prefix split: matrix-core decode (16- and 8-bit caches; fp32 caches take the plain decode, same results)
     const int skip = mfma ? std::min(shared_blocks, static_cast<int>(ceil_div(cap, FFKV_BLOCK_SIZE))) : 0;
     int pfx_chunks = 0, pfx_chunk_pages = 0;

@@ -143,7 +143,7 @@ constexpr int kMfmaMaxItems = 2048;
 int decode_mfma_items(const void* kernel, int threads, int grid_y);
 // decode_mfma_items for the kernel instance launch_decode_mfma selects for `a` (its dtypes, head_dim and heads).
 int decode_mfma_launch_items(const DecodeArgs& a);
-bool decode_use_mfma(int cache_dtype, int group);
+bool decode_use_mfma(int cache_dtype, int group, int head_dim);
 size_t decode_mfma_workspace_bytes(int batch, int num_heads, int head_dim);  // upper bound (kMfmaMaxItems items)
 
 // Split-K geometry shared by the workspace query and the launcher.

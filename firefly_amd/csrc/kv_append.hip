@@ -16,13 +16,14 @@ namespace ffkv
 // Quantize or convert one lane's 8 elements of a (token, head) row for the cache and store them; int8 also writes
 // the row's scale (lane 0 of the row).  LPR lanes hold a row; the cross-lane absmax stays inside them.
 // fp8: head_scale is the row's kv-head scale (loaded by the caller with the row's addressing).
+// act: the lane holds dims of the row (lanes past head_dim / 8 take part in the int8 max with zeros, store nothing).
 template <int SRC, int CACHE, int LPR>
 __device__ __forceinline__ void put_row8(const Raw8& raw, void* cache, size_t dst, float* scale_out, size_t dst_row,
-                                         float head_scale, int lane)
+                                         float head_scale, int lane, bool act)
 {
     if constexpr (SRC == CACHE)
     {
-        store_raw8<CACHE>(cache, dst, raw);
+        if (act) store_raw8<CACHE>(cache, dst, raw);
     }
     else
     {
@@ -61,12 +62,13 @@ __device__ __forceinline__ void put_row8(const Raw8& raw, void* cache, size_t ds
         {
             pack8<CACHE>(x, out);
         }
-        store_raw8<CACHE>(cache, dst, out);
+        if (act) store_raw8<CACHE>(cache, dst, out);
     }
 }
 
-// IDX: the row-index type, 32-bit when batch * seq_len * num_kv_heads fits (divisions by the head and token
-// counts are then 32-bit), 64-bit otherwise.  A workgroup iteration covers U groups of RPI consecutive rows; a
+// DT: head_dim, or 0 for a runtime head_dim (a multiple of 8 up to 8 * LPR); LPR: lanes per row (a power of two,
+// DT / 8 when DT is given).  IDX: the row-index type, 32-bit when batch * seq_len * num_kv_heads fits (divisions
+// by the head and token counts are then 32-bit), 64-bit otherwise.  A workgroup iteration covers U groups of RPI consecutive rows; a
 // lane takes one row of each group.  Its loads go out in dependency order: the addressing chain (context length,
 // then block-table entry, and for fp8 the head scales) before the source rows, so the wait for the table entries
 // does not also wait for the source rows.
@@ -74,13 +76,15 @@ __device__ __forceinline__ void put_row8(const Raw8& raw, void* cache, size_t ds
 #define FFKV_APPEND_U 2  // row groups per workgroup iteration (rows in flight per lane)
 #endif
 
-template <int SRC, int CACHE, int D, typename IDX>
+template <int SRC, int CACHE, int DT, int LPR, typename IDX>
 __global__ __launch_bounds__(256) void append_kernel(AppendArgs a)
 {
-    constexpr int LPR = D / 8;      // lanes per (token, head) row
+    static_assert(DT == 0 || DT == 8 * LPR, "a given head_dim has head_dim / 8 lanes per row");
     constexpr int RPI = 256 / LPR;  // rows per group
     constexpr int U = FFKV_APPEND_U;
+    const int     D = DT != 0 ? DT : a.head_dim;
     const int     lane = threadIdx.x % LPR;
+    const bool    act = DT != 0 || lane * 8 < D;
     const IDX     rows = static_cast<IDX>(a.batch) * static_cast<IDX>(a.seq_len) * static_cast<IDX>(a.num_kv_heads);
     const IDX     step = static_cast<IDX>(gridDim.x) * (RPI * U);
     const IDX     hkv = static_cast<IDX>(a.num_kv_heads), sl = static_cast<IDX>(a.seq_len);
@@ -128,11 +132,16 @@ __global__ __launch_bounds__(256) void append_kernel(AppendArgs a)
 #pragma unroll
         for (int u = 0; u < U; ++u)
         {
-            if (live[u])
+            if (live[u] && act)
             {
                 const size_t src = static_cast<size_t>(base + static_cast<IDX>(u * RPI)) * D + lane * 8;  // :39
                 load_raw8<SRC>(a.k_src, src, kr[u]);
                 load_raw8<SRC>(a.v_src, src, vr[u]);
+            }
+            else
+            {
+                kr[u] = Raw8{};
+                vr[u] = Raw8{};
             }
         }
 #pragma unroll
@@ -143,8 +152,8 @@ __global__ __launch_bounds__(256) void append_kernel(AppendArgs a)
             const size_t dst_row =
                 (static_cast<size_t>(phys[u]) * kBlockSize + (pos[u] & 15)) * a.num_kv_heads + h[u];
             const size_t dst = dst_row * D + lane * 8;  // qwen_model.cu:41-42
-            put_row8<SRC, CACHE, LPR>(kr[u], a.k_cache, dst, a.k_scale, dst_row, ksc[u], lane);
-            put_row8<SRC, CACHE, LPR>(vr[u], a.v_cache, dst, a.v_scale, dst_row, vsc[u], lane);
+            put_row8<SRC, CACHE, LPR>(kr[u], a.k_cache, dst, a.k_scale, dst_row, ksc[u], lane, act);
+            put_row8<SRC, CACHE, LPR>(vr[u], a.v_cache, dst, a.v_scale, dst_row, vsc[u], lane, act);
         }
     }
 }
@@ -163,16 +172,20 @@ void launch_i(const AppendArgs& a, int64_t rows, hipStream_t stream)
     switch (a.head_dim)
     {
         case 64:
-            hipLaunchKernelGGL((append_kernel<SRC, CACHE, 64, IDX>), dim3(grid_for(32 * FFKV_APPEND_U)), dim3(256), 0,
-                               stream, a);
-            break;
-        case 128:
-            hipLaunchKernelGGL((append_kernel<SRC, CACHE, 128, IDX>), dim3(grid_for(16 * FFKV_APPEND_U)), dim3(256),
+            hipLaunchKernelGGL((append_kernel<SRC, CACHE, 64, 8, IDX>), dim3(grid_for(32 * FFKV_APPEND_U)), dim3(256),
                                0, stream, a);
             break;
-        default:
-            hipLaunchKernelGGL((append_kernel<SRC, CACHE, 256, IDX>), dim3(grid_for(8 * FFKV_APPEND_U)), dim3(256), 0,
-                               stream, a);
+        case 128:
+            hipLaunchKernelGGL((append_kernel<SRC, CACHE, 128, 16, IDX>), dim3(grid_for(16 * FFKV_APPEND_U)),
+                               dim3(256), 0, stream, a);
+            break;
+        case 256:
+            hipLaunchKernelGGL((append_kernel<SRC, CACHE, 256, 32, IDX>), dim3(grid_for(8 * FFKV_APPEND_U)), dim3(256),
+                               0, stream, a);
+            break;
+        default:  // any other multiple of 8 up to 128: 16 lanes per row, those past head_dim / 8 idle
+            hipLaunchKernelGGL((append_kernel<SRC, CACHE, 0, 16, IDX>), dim3(grid_for(16 * FFKV_APPEND_U)), dim3(256),
+                               0, stream, a);
             break;
     }
 }

@@ -9,7 +9,8 @@
 // state (m, l, acc) that paged_decode_merge combines.
 //
 // Lane layout: head_dim/8 lanes per token (one 8-element, 16-byte chunk each for 16-bit KV), so a wave64 covers
-// 64/(D/8) tokens per step and the workgroup 256/(D/8).  Each token slot keeps its own online-softmax state in
+// 64/(D/8) tokens per step and the workgroup 256/(D/8).  Head dims other than 64, 128 and 256 (multiples of 8 up
+// to 128, which the reference's decode takes) run with 16 lanes per token, those past head_dim/8 idle.  Each token slot keeps its own online-softmax state in
 // registers; the slots are merged with cross-lane shuffles inside a wave and through LDS across waves.
 // The softmax runs in base 2 with log2(e) folded into the score scale.
 #include "ffkv_device.h"
@@ -33,8 +34,9 @@ __device__ __forceinline__ int row_tokens(const DecodeArgs& a, int b)
 }
 
 // Load 8 dequantized cache elements of row `row` (page*16 + slot)*Hkv + h at dims [d0, d0+8).
-template <int CT, int D>
-__device__ __forceinline__ void load_kv8(const void* cache, const float* scale, size_t row, int h, int d0, float* x)
+template <int CT>
+__device__ __forceinline__ void load_kv8(const void* cache, const float* scale, size_t row, int D, int h, int d0,
+                                         float* x)
 {
     Raw8 raw;
     load_raw8<CT>(cache, row * D + d0, raw);
@@ -55,12 +57,16 @@ __device__ __forceinline__ void load_kv8(const void* cache, const float* scale, 
 
 }  // namespace
 
-template <int CT, int D, int GP>
+// DT: head_dim, or 0 for a runtime head_dim (a multiple of 8 up to 8 * LPT); LPT: lanes per token, a power of two
+// (DT / 8 when DT is given).  Lanes past head_dim / 8 hold zeros and store nothing.
+template <int CT, int DT, int LPT, int GP>
 __global__ __launch_bounds__(256) void paged_decode_generic(DecodeArgs a)
 {
-    constexpr int LPT = D / 8;     // lanes per token
+    static_assert(DT == 0 || DT == 8 * LPT, "a given head_dim has head_dim / 8 lanes per token");
     constexpr int TPI = 256 / LPT; // token slots per workgroup
     constexpr int WAVES = 4;
+    constexpr int DMAX = 8 * LPT;
+    const int     D = DT != 0 ? DT : a.head_dim;
 
     const int chunk_id = blockIdx.x;
     const int kvh = blockIdx.y;
@@ -69,6 +75,7 @@ __global__ __launch_bounds__(256) void paged_decode_generic(DecodeArgs a)
     const int lane = tid % LPT;
     const int slot = tid / LPT;
     const int wave = tid / 64;
+    const bool act = DT != 0 || lane * 8 < D;  // this lane holds dims of the head
 
     const int L = row_tokens(a, b);
     const int nch = (L + a.chunk - 1) / a.chunk;
@@ -81,7 +88,7 @@ __global__ __launch_bounds__(256) void paged_decode_generic(DecodeArgs a)
 #pragma unroll
     for (int g = 0; g < GP; ++g)
     {
-        if (g < G)
+        if (g < G && act)
             load_act8(a.q, a.qo_dtype, (static_cast<size_t>(b) * a.num_heads + kvh * G + g) * D + lane * 8, q[g]);
         else
 #pragma unroll
@@ -113,11 +120,11 @@ __global__ __launch_bounds__(256) void paged_decode_generic(DecodeArgs a)
 
         float s[GP];
         float v[8];
-        if (valid)
+        if (valid && act)
         {
             float k[8];
-            load_kv8<CT, D>(a.k_cache, a.k_scale, row, kvh, lane * 8, k);
-            load_kv8<CT, D>(a.v_cache, a.v_scale, row, kvh, lane * 8, v);
+            load_kv8<CT>(a.k_cache, a.k_scale, row, D, kvh, lane * 8, k);
+            load_kv8<CT>(a.v_cache, a.v_scale, row, D, kvh, lane * 8, v);
 #pragma unroll
             for (int g = 0; g < GP; ++g)
             {
@@ -131,6 +138,8 @@ __global__ __launch_bounds__(256) void paged_decode_generic(DecodeArgs a)
         {
 #pragma unroll
             for (int g = 0; g < GP; ++g) s[g] = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = 0.0f;
         }
         // every lane takes part in the shuffles; a token's lanes are a contiguous, aligned group
 #pragma unroll
@@ -175,10 +184,10 @@ __global__ __launch_bounds__(256) void paged_decode_generic(DecodeArgs a)
     }
 
     // merge the waves through LDS, one wave at a time
-    __shared__ float s_acc[GP][D];
+    __shared__ float s_acc[GP][DMAX];
     __shared__ float s_m[GP];
     __shared__ float s_l[GP];
-    const bool holder = (tid % 64) < LPT;
+    const bool holder = (tid % 64) < LPT && act;
     for (int w = 0; w < WAVES; ++w)
     {
         if (wave == w && holder)
@@ -247,9 +256,9 @@ __global__ __launch_bounds__(256) void paged_decode_generic(DecodeArgs a)
 }
 
 // Combine the chunk partials of rows that needed more than one chunk.  One workgroup per (query head, row).
-template <int D>
 __global__ __launch_bounds__(256) void paged_decode_merge(DecodeArgs a)
 {
+    const int D = a.head_dim;
     const int hq = blockIdx.x;
     const int b = blockIdx.y;
     const int L = row_tokens(a, b);
@@ -274,27 +283,27 @@ __global__ __launch_bounds__(256) void paged_decode_merge(DecodeArgs a)
 namespace
 {
 
-template <int CT, int D, int GP>
+template <int CT, int DT, int LPT, int GP>
 hipError_t launch3(const DecodeArgs& a, hipStream_t stream)
 {
     dim3 grid(static_cast<unsigned>(a.max_chunks), static_cast<unsigned>(a.num_kv_heads),
               static_cast<unsigned>(a.batch));
-    hipLaunchKernelGGL((paged_decode_generic<CT, D, GP>), grid, dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((paged_decode_generic<CT, DT, LPT, GP>), grid, dim3(256), 0, stream, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || a.max_chunks <= 1) return e;
-    hipLaunchKernelGGL((paged_decode_merge<D>), dim3(static_cast<unsigned>(a.num_heads), static_cast<unsigned>(a.batch)),
-                       dim3(D < 256 ? D : 256), 0, stream, a);
+    hipLaunchKernelGGL(paged_decode_merge, dim3(static_cast<unsigned>(a.num_heads), static_cast<unsigned>(a.batch)),
+                       dim3(a.head_dim < 256 ? a.head_dim : 256), 0, stream, a);
     return hipGetLastError();
 }
 
-template <int CT, int D>
+template <int CT, int DT, int LPT>
 hipError_t launch2(const DecodeArgs& a, hipStream_t stream)
 {
-    if (a.group <= 1) return launch3<CT, D, 1>(a, stream);
-    if (a.group <= 2) return launch3<CT, D, 2>(a, stream);
-    if (a.group <= 4) return launch3<CT, D, 4>(a, stream);
-    if (a.group <= 8) return launch3<CT, D, 8>(a, stream);
-    return launch3<CT, D, 16>(a, stream);
+    if (a.group <= 1) return launch3<CT, DT, LPT, 1>(a, stream);
+    if (a.group <= 2) return launch3<CT, DT, LPT, 2>(a, stream);
+    if (a.group <= 4) return launch3<CT, DT, LPT, 4>(a, stream);
+    if (a.group <= 8) return launch3<CT, DT, LPT, 8>(a, stream);
+    return launch3<CT, DT, LPT, 16>(a, stream);
 }
 
 template <int CT>
@@ -303,11 +312,13 @@ hipError_t launch1(const DecodeArgs& a, hipStream_t stream)
     switch (a.head_dim)
     {
         case 64:
-            return launch2<CT, 64>(a, stream);
+            return launch2<CT, 64, 8>(a, stream);
         case 128:
-            return launch2<CT, 128>(a, stream);
-        default:
-            return launch2<CT, 256>(a, stream);
+            return launch2<CT, 128, 16>(a, stream);
+        case 256:
+            return launch2<CT, 256, 32>(a, stream);
+        default:  // any other multiple of 8 up to 128: 16 lanes per token, those past head_dim / 8 idle
+            return launch2<CT, 0, 16>(a, stream);
     }
 }
 

@@ -73,7 +73,8 @@ extern "C" {
  * block_table[b*max_blocks + pos/16], slot pos%16.  src_dtype is F32, F16 or BF16; cache_dtype is F32, F16,
  * BF16 (copy, rounding to nearest even when narrowing), I8 or FP8_E4M3 (quantize, see above).
  * k_scale / v_scale: I8 -> written, [num_blocks, 16, num_kv_heads]; FP8 -> read, [num_kv_heads]; else unused.
- * head_dim must be 64, 128 or 256; block_size must be 16.  Source and cache pointers must be 16-byte aligned.
+ * head_dim is a multiple of 8 up to 128 (the reference's append takes any head_dim up to its 128-thread block),
+ * or 256; block_size must be 16.  Source and cache pointers must be 16-byte aligned.
  */
 FFKV_API int ffkv_append(const void* k_src, const void* v_src, int src_dtype, void* k_cache, void* v_cache, int cache_dtype,
                 float* k_scale, float* v_scale, const int32_t* block_table, const int32_t* context_lens, int batch,
@@ -96,8 +97,9 @@ FFKV_API size_t ffkv_decode_workspace_bytes(int batch, int num_heads, int head_d
  *
  * qo_dtype (q and out) is F32, F16 or BF16; cache_dtype as for ffkv_append.  scale <= 0 selects
  * 1/sqrt(head_dim) (src/kernels/attention.cu:458).  num_heads must be a multiple of num_kv_heads (any group
- * size for 16- and 8-bit caches, at most 16 for fp32 caches) and at most 65535; head_dim 64, 128 or 256; q,
- * out, cache and workspace pointers 16-byte aligned.  Rows are
+ * size for 16- and 8-bit caches at head_dim 64, 128 and 256, at most 16 otherwise) and at most 65535; head_dim a
+ * multiple of 8 up to 128 (as the reference's decode, src/kernels/attention.cu:307-316), or 256 (64, 128 and 256
+ * run the matrix-core kernels, the others a vector kernel); q, out, cache and workspace pointers 16-byte aligned.  Rows are
  * split over the context and the pieces merged; the partials live in `workspace` (ffkv_decode_workspace_bytes;
  * any initial contents), or, when workspace is NULL, in stream-ordered memory the library allocates and frees on
  * `stream`.  Calls sharing one workspace must not overlap in time (use one workspace per stream).  Rows whose

@@ -48,7 +48,8 @@ int decode(int qo = 2, int cache = 2, int batch = 1, int hq = 32, int hkv = 8, i
 int main()
 {
     expect(append(2, 2, 1, 1, 8, 128, 32), FFKV_ERR_UNSUPPORTED, "append block_size 32");
-    expect(append(2, 2, 1, 1, 8, 96), FFKV_ERR_UNSUPPORTED, "append head_dim 96");
+    expect(append(2, 2, 1, 1, 8, 100), FFKV_ERR_UNSUPPORTED, "append head_dim 100 (not a multiple of 8)");
+    expect(append(2, 2, 1, 1, 8, 136), FFKV_ERR_UNSUPPORTED, "append head_dim 136 (over 128, not 256)");
     expect(append(3), FFKV_ERR_UNSUPPORTED, "append int8 source");
     expect(append(2, 7), FFKV_ERR_UNSUPPORTED, "append UNKNOWN cache");
     expect(append(2, 2, -1), FFKV_ERR_INVALID_ARGUMENT, "append negative batch");
@@ -62,7 +63,11 @@ int main()
     expect(append(2, 2, 1, 0), FFKV_OK, "append empty sequence");
 
     expect(decode(2, 2, 1, 32, 8, 128, 8), FFKV_ERR_UNSUPPORTED, "decode block_size 8");
-    expect(decode(2, 2, 1, 32, 8, 80), FFKV_ERR_UNSUPPORTED, "decode head_dim 80");
+    expect(decode(2, 2, 1, 32, 8, 84), FFKV_ERR_UNSUPPORTED, "decode head_dim 84 (not a multiple of 8)");
+    expect(decode(2, 2, 1, 32, 8, 0), FFKV_ERR_UNSUPPORTED, "decode head_dim 0");
+    expect(ffkv_paged_prefill(P(16), P(16), 2, P(16), P(16), 2, nullptr, nullptr, I(16), I(16), 1, 4, 32, 8, 96, 16,
+                              4, 4, 0, 0.0f, nullptr),
+           FFKV_ERR_UNSUPPORTED, "prefill head_dim 96");
     expect(decode(3), FFKV_ERR_UNSUPPORTED, "decode int8 q");
     expect(decode(2, 2, 1, 30, 8), FFKV_ERR_INVALID_ARGUMENT, "decode heads not a multiple of kv heads");
     expect(decode(2, 0, 1, 8 * 17, 8), FFKV_ERR_UNSUPPORTED, "decode group 17 on an fp32 cache");

@@ -48,7 +48,9 @@ def _decode(ff, **kw):
 
 @pytest.mark.parametrize("kw,code", [
     (dict(block_size=32), -2),
-    (dict(head_dim=96), -2),
+    (dict(head_dim=100), -2),         # not a multiple of 8
+    (dict(head_dim=136), -2),         # over 128 and not 256
+    (dict(head_dim=0), -2),
     (dict(src_dtype=3), -2),          # int8 is not an activation dtype
     (dict(cache_dtype=7), -2),        # the reference's UNKNOWN
     (dict(batch=-1), -1),
@@ -72,7 +74,8 @@ def test_append_empty_is_ok(ff):
 
 @pytest.mark.parametrize("kw,code", [
     (dict(block_size=8), -2),
-    (dict(head_dim=80), -2),
+    (dict(head_dim=84), -2),          # not a multiple of 8
+    (dict(head_dim=144), -2),         # over 128 and not 256
     (dict(qo_dtype=3), -2),
     (dict(num_heads=30), -1),         # not a multiple of num_kv_heads
     (dict(num_heads=8 * 17, cache_dtype=0), -2),  # GQA group above 16 on an fp32 cache (the generic kernel)

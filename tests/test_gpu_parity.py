@@ -79,6 +79,27 @@ def test_head_dim_256_dtypes(ff, gpu, act, kv):
     _check(ff, gpu, c, 2e-3 if kv in ("f16", "bf16") else 2e-2)
 
 
+@pytest.mark.parametrize("D", [8, 40, 96, 112])
+@pytest.mark.parametrize("act,kv", [("bf16", "bf16"), ("f16", "f16"), ("f32", "f32"), ("bf16", "i8"),
+                                    ("bf16", "fp8"), ("f32", "fp8")])
+def test_head_dims_multiple_of_8(ff, gpu, D, act, kv):
+    """Any head_dim that is a multiple of 8 up to 128, as the reference's decode takes (one 8-element vector per
+    lane of a 16-lane group, src/kernels/attention.cu:307-316) and its append (any head_dim up to 128,
+    src/model/qwen_model.cu:21-47): pages and int8 scales bit-exact, outputs within the bar.  These head dims run
+    the generic decode kernel with 16 lanes per token, those past head_dim / 8 idle."""
+    rng = np.random.default_rng(D * 7 + len(act) + len(kv))
+    ctx = rng.integers(0, 600, size=5)
+    c = cases.make_case(80 + D, 5, 16, 4, D, ctx, act=act, kv=kv, input_scale=1 / math.sqrt(D))
+    _check(ff, gpu, c, TOL[(act, kv)])
+
+
+@pytest.mark.parametrize("kv", ["bf16", "i8"])
+def test_head_dim_96_multi_token_append(ff, gpu, kv):
+    """A 37-token chunk appended per row at head_dim 96 (12 of 16 lanes per row active), then decode."""
+    c = cases.make_case(96, 3, 16, 4, 96, [0, 45, 300], act="bf16", kv=kv, S=37)
+    _check(ff, gpu, c, 2e-3 if kv == "bf16" else 2e-2)
+
+
 @pytest.mark.parametrize("G,Hkv,D,act,kv", [(17, 2, 128, "bf16", "bf16"), (32, 1, 128, "bf16", "bf16"),
                                              (48, 2, 128, "f16", "f16"), (24, 2, 64, "bf16", "fp8"),
                                              (32, 2, 128, "bf16", "i8"), (20, 1, 256, "f32", "bf16")])

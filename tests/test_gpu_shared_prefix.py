@@ -147,3 +147,11 @@ def test_workspace_with_garbage_reused(ff, gpu):
         c = cases.make_case(51 + i, B, 32, 8, 128, ctx, act="bf16", shared_prefix_blocks=shared, max_blocks=200)
         got, _, ref = _run(ff, gpu, c, shared, workspace=ws)
         _check(got, ref, c.act, 2e-3, f"call {i}")
+
+
+def test_head_dim_96_takes_the_plain_decode(ff, gpu):
+    """head_dim 96 has no matrix-core kernels: the shared-prefix entry point runs the plain decode, same results."""
+    rng = np.random.default_rng(96)
+    ctx = 8 * 16 + rng.integers(1, 200, size=10) - 1
+    c = cases.make_case(96, 10, 16, 4, 96, ctx, act="bf16", shared_prefix_blocks=8)
+    _both(ff, gpu, c, 8)

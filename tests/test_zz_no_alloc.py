@@ -30,7 +30,7 @@ def test_noalloc_rejects_sizes_beyond_scratch(ff):
     (fake pointers are never dereferenced).  Argument checks come first, as in ffkv_paged_decode."""
     assert _call(ff, batch=8192) == FFKV_ERR_WORKSPACE
     assert "noalloc" in ff.lib.ffkv_last_error().decode()
-    assert _call(ff, head_dim=80) == -2
+    assert _call(ff, head_dim=84) == -2
     assert _call(ff, batch=0) == 0
 
 
