@@ -92,10 +92,10 @@ __device__ __forceinline__ int32_t quant_i8(float x, float s)
 // The quantizers below give exactly the codes of quant_i8(x, s) and f32_to_e4m3(x / s) without a divide per
 // element.  A code depends on the quotient fl(x / s) only through where it falls between the target format's
 // rounding boundaries (int8: half-integers; e4m3: the midpoints between neighbouring codes).  y = x * rcp(s) is
-// within a few ulps of x / s (v_rcp_f32 is accurate to 1 ulp and the product rounds once), and fl(x / s) within
-// half an ulp, so when y lies more than 64 of its ulps from every boundary both round to the same code.  Only
-// when it does not (a fraction of about 1e-4 of random inputs), or for non-finite values, is the IEEE divide
-// evaluated.
+// within 1.5 * 2^-23 * |y| of x / s (v_rcp_f32 is accurate to 1 ulp and the product rounds once), at most 3 of
+// y's ulps, and fl(x / s) within half an ulp more, so when y lies more than FFKV_QUANT_MARGIN (8) of its ulps from
+// every boundary both round to the same code.  Only when it does not (about 2e-5 of random inputs), for e4m3's
+// subnormal range and for NaN is the IEEE divide evaluated.
 
 // 1/s for the quantizers: NaN unless s is positive, normal and finite, which sends every element to the divide.
 __device__ __forceinline__ float quant_rcp(float s)
@@ -107,20 +107,27 @@ __device__ __forceinline__ float quant_rcp(float s)
 #define FFKV_FP8_HW_CVT 1  // fp8 codes of safe values from v_cvt_pk_fp8_f32 (0: the integer conversion)
 #endif
 
-// int8: y = x * rs is safe when it is more than 64 ulps from the half-integers, i.e. |y - rint(y)| < 0.5 - 64 ulp.
-// NaN and infinite y fail the test.
+// Distance from a rounding boundary, in ulps of y, beyond which y is "safe" (see above).
+#ifndef FFKV_QUANT_MARGIN
+#define FFKV_QUANT_MARGIN 8
+#endif
+
+// int8: the boundaries are the half-integers: safe when |y - rint(y)| < 0.5 - margin * 2^-23 * |y|.  NaN and
+// infinite y fail the test.
 __device__ __forceinline__ bool quant_i8_safe(float y, float r)
 {
-    return __builtin_fabsf(y - r) < __builtin_fmaf(-__builtin_fabsf(y), 0x1p-17f, 0.5f - 0x1p-40f);
+    return __builtin_fabsf(y - r) <
+           __builtin_fmaf(-__builtin_fabsf(y), FFKV_QUANT_MARGIN * 0x1p-23f, 0.5f - 0x1p-40f);
 }
 
-// e4m3: y is safe when 2^-6 <= |y| < inf (e4m3 normal range, saturating above 448) and the 20 mantissa bits below
-// the 3 kept ones are more than 64 from the midpoint pattern 0x80000.  Subnormal-range y take the divide.
+// e4m3: in the normal range the boundaries are the midpoints between neighbouring codes, where the 20 fp32
+// mantissa bits below the 3 kept ones equal 0x80000: safe when they are more than the margin from it and
+// |y| >= 2^-6 (one compare, false for NaN).  Smaller y (the subnormal grid, and zero) take the divide; infinite
+// and huge y are safe: they clamp to 448, as the conversion saturates them.
 __device__ __forceinline__ bool quant_e4m3_safe(float y)
 {
     const uint32_t u = f2u(y);
-    const uint32_t a = u & 0x7fffffffu;
-    return a - 0x3c800000u < 0x7f800000u - 0x3c800000u && (u & 0xfffffu) + (64u - 0x80000u) > 128u;
+    return __builtin_fabsf(y) >= 0x1p-6f && (u & 0xfffffu) + (FFKV_QUANT_MARGIN - 0x80000u) > 2u * FFKV_QUANT_MARGIN;
 }
 
 // Quantize 8 values to packed codes (element i in byte i % 4 of w[i / 4]) with the fast forms; only in a wave

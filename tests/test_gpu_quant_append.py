@@ -1,8 +1,9 @@
 """Quantize-on-append at the rounding boundaries, byte for byte against the CPU checker.
 
 The append's int8 and fp8 quantizers compute y = x * (1/s) and keep the divide x / s only where y lies within
-64 ulps of a rounding boundary of the target format (int8: the half-integers; e4m3: the midpoints between
-neighbouring codes and the subnormal grid); fp8 codes of the other values come from the hardware conversion.
+8 ulps of a rounding boundary of the target format (int8: the half-integers; e4m3: the midpoints between
+neighbouring codes, and the whole subnormal range); fp8 codes of the other values (infinite ones included: they
+clamp to 448, as the conversion saturates) come from the hardware conversion.
 These cases put fp32 source values on, and a few ulps to either side of, every such boundary and every e4m3
 code, plus values at and beyond the saturation point, subnormal-range values, signed zeros, infinities and NaN,
 so that both paths and their seam are exercised.  Pages and int8 scales must equal the checker's bytes.
@@ -18,7 +19,7 @@ pytestmark = pytest.mark.gpu
 D = 128
 
 
-def _neighbours(v: np.ndarray, ulps=(0, 1, 2, 3, 5, 63, 64, 65, 66, 70, 200)) -> np.ndarray:
+def _neighbours(v: np.ndarray, ulps=(0, 1, 2, 3, 5, 7, 8, 9, 10, 16, 17, 63, 64, 65, 66, 70, 200)) -> np.ndarray:
     """v and the fp32 values `ulps` steps above and below it."""
     out = [v]
     for k in ulps[1:]:
