@@ -51,3 +51,19 @@ def test_random_prefill(ff, gpu, seed):
         S //= 2
     c, qn = _prefill_case(9500 + seed, B, G * Hkv, Hkv, D, ctx, S, act=act, kv=kv)
     _prefill_check(*_prefill_run(ff, gpu, c, qn), c.act, 2e-3 if kv in ("bf16", "f16") else 2e-2)
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_random_decode_head_dims(ff, gpu, seed):
+    """head_dim drawn from the multiples of 8 up to 128 (the vector decode's range besides 64 and 128), groups up
+    to 16 query heads per KV head."""
+    rng = np.random.default_rng(9800 + seed)
+    act, kv = DECODE_PAIRS[(seed * 3) % len(DECODE_PAIRS)]
+    D = 8 * int(rng.integers(1, 17))
+    G = int(rng.choice([g for g in GROUPS if g <= 16]))
+    Hkv = int(rng.choice([1, 2, 4]))
+    B = int(rng.integers(1, 25))
+    ctx = rng.integers(0, 1200, size=B)
+    ctx[rng.random(B) < 0.1] = 0
+    c = cases.make_case(9800 + seed, B, G * Hkv, Hkv, D, ctx, act=act, kv=kv, input_scale=1 / math.sqrt(D))
+    _decode_check(ff, gpu, c, TOL[(act, kv)])
