@@ -250,10 +250,11 @@ void paged_prefill_dma(PrefillArgs a)
     constexpr int  NT = D / 16;
     constexpr bool NEED_LO = !((QT == BF16 && BF) || (QT == F16 && !BF));
     // Load issue per page (one table select and page base per page, then the page's runs) or per run (a 64-bit
-    // page-offset select per run).  The per-page form has a third less scalar work; measured on the chunked
-    // prefill it is 2-6 % faster for f16 / f32 queries, int8 caches and head_dim 64 / 256, and 2-3 % slower for
-    // bf16 queries over bf16 / fp8 caches at head_dim 128, where the per-run form stays.
-    constexpr bool PAGE_ISSUE = !PFX && !(QT == BF16 && D == 128 && CT != I8);
+    // page-offset select per run).  The per-page form has a third less scalar work and measured 1-6 % faster on the
+    // chunked prefill for every cache type and head_dim (since the f16 PV products of 8-bit caches, bf16 queries
+    // over bf16 / fp8 caches at head_dim 128 too, where the per-run form had been 2-3 % ahead); the shared-prefix
+    // partials keep the per-run form.
+    constexpr bool PAGE_ISSUE = !PFX;
     // 8-bit codes are exact in f16 as in bf16: with bf16 score products (BF), their PV products still take f16
     // V^T and P^T, so P needs one product instead of a bf16 hi + lo pair.
     constexpr bool V16 = FFKV_PREFILL_V16 && Q8 && BF;
