@@ -155,3 +155,43 @@ def test_head_dim_96_takes_the_plain_decode(ff, gpu):
     ctx = 8 * 16 + rng.integers(1, 200, size=10) - 1
     c = cases.make_case(96, 10, 16, 4, 96, ctx, act="bf16", shared_prefix_blocks=8)
     _both(ff, gpu, c, 8)
+
+
+
+def test_decode_and_prefill_on_two_streams(ff, gpu):
+    """A C4-style step with the decode rows (append + shared-prefix decode) on a second stream beside the chunk
+    rows (append + prefill) on the first, forked and joined with events: the halves touch disjoint rows (shared
+    prefix pages are only read), so outputs and pages equal the one-stream step's bit for bit."""
+    import torch
+
+    import gpu_util as gu
+
+    rng = np.random.default_rng(97)
+    Bd, Bc, S, shared = 12, 2, 40, 8
+    ctx = shared * 16 + rng.integers(1, 300, size=Bd + Bc) - 1
+    c = cases.make_case(97, Bd + Bc, 32, 8, 128, ctx, act="bf16", S=S, shared_prefix_blocks=shared)
+    print(f"case two-stream step Bd={Bd} Bc={Bc} S={S} shared={shared}", flush=True)
+    tbl = torch.from_numpy(c.block_table).to(gpu)
+    cx = torch.from_numpy(c.ctx).to(gpu)
+    kn, vn, q = gu.to_dev(c.k_new, c.act, gpu), gu.to_dev(c.v_new, c.act, gpu), gu.to_dev(c.q, c.act, gpu)
+    qc = gu.to_dev(cases.encode(rng.standard_normal((Bc, S, 32, 128), dtype=np.float32), c.act), c.act, gpu)
+
+    def run(two):
+        kp, vp = gu.to_dev(c.k_pool, c.kv, gpu), gu.to_dev(c.v_pool, c.kv, gpu)
+        s1 = torch.cuda.current_stream()
+        s2 = torch.cuda.Stream(device=gpu) if two else s1
+        fork, join = torch.cuda.Event(), torch.cuda.Event()
+        fork.record(s1)
+        s2.wait_event(fork)
+        ff.append_kv_cache(kn[:Bd, :1].contiguous(), vn[:Bd, :1].contiguous(), kp, vp, tbl[:Bd], cx[:Bd], stream=s2)
+        od = ff.paged_attention_shared_prefix(q[:Bd], kp, vp, tbl[:Bd], cx[:Bd], shared, stream=s2)
+        ff.append_kv_cache(kn[Bd:].contiguous(), vn[Bd:].contiguous(), kp, vp, tbl[Bd:], cx[Bd:], stream=s1)
+        oc = ff.paged_prefill(qc, kp, vp, tbl[Bd:], cx[Bd:], stream=s1)
+        join.record(s2)
+        s1.wait_event(join)
+        torch.cuda.synchronize()
+        return [gu.to_host(t, np.uint16) for t in (od, oc, kp, vp)]
+
+    one, two = run(False), run(True)
+    for what, a, b in zip(("decode out", "prefill out", "K pages", "V pages"), one, two):
+        assert np.array_equal(a, b), what
