@@ -8,6 +8,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace ffkv
 {
 
@@ -79,6 +81,34 @@ __device__ __forceinline__ float e4m3_to_f32(uint32_t q)
     return u2f(f2u(v) | ((q & 0x80u) << 24));
 }
 
+// Largest of v over aligned groups of N lanes (N a power of two up to 32), in every lane of the group; v is never
+// NaN here (absolute-value maxima that skip NaN).  Quad permutations and the 8- and 16-lane mirrors are DPP
+// operands of the compare, the step between 16-lane rows gfx950's row swap: no LDS round trip.
+template <int N>
+__device__ __forceinline__ float group_max(float v)
+{
+    static_assert(N >= 1 && N <= 32 && (N & (N - 1)) == 0, "groups of 1, 2, 4, 8, 16 or 32 lanes");
+    auto take = [&v](float o) { v = o > v ? o : v; };
+    auto dpp = [](float x, auto ctrl)
+    {
+        return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x),
+                                                                      decltype(ctrl)::value, 0xf, 0xf, false));
+    };
+    if constexpr (N >= 2) take(dpp(v, std::integral_constant<int, 0xb1>{}));   // quad lanes 1, 0, 3, 2
+    if constexpr (N >= 4) take(dpp(v, std::integral_constant<int, 0x4e>{}));   // quad lanes 2, 3, 0, 1
+    if constexpr (N >= 8) take(dpp(v, std::integral_constant<int, 0x141>{}));  // lane 7 - i of its 8
+    if constexpr (N >= 16) take(dpp(v, std::integral_constant<int, 0x140>{})); // lane 15 - i of its 16
+    if constexpr (N >= 32)
+    {
+        const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, v), __builtin_bit_cast(uint32_t, v),
+                                                        false, false);  // rows (0, 0, 2, 2) and (1, 1, 3, 3)
+        const float a = __builtin_bit_cast(float, static_cast<uint32_t>(r[0]));
+        const float b = __builtin_bit_cast(float, static_cast<uint32_t>(r[1]));
+        v = a > b ? a : b;
+    }
+    return v;
+}
+
 __device__ __forceinline__ int32_t quant_i8(float x, float s)
 {
     float y = x / s;  // IEEE divide (hipcc keeps fp32 division correctly rounded by default)
@@ -95,7 +125,8 @@ __device__ __forceinline__ int32_t quant_i8(float x, float s)
 // within 1.5 * 2^-23 * |y| of x / s (v_rcp_f32 is accurate to 1 ulp and the product rounds once), at most 3 of
 // y's ulps, and fl(x / s) within half an ulp more, so when y lies more than FFKV_QUANT_MARGIN (8) of its ulps from
 // every boundary both round to the same code.  Only when it does not (about 2e-5 of random inputs), for e4m3's
-// subnormal range and for NaN is the IEEE divide evaluated.
+// subnormal range and for NaN is the IEEE divide evaluated.  The compiler may fuse the product into the following
+// add or subtract; the unrounded product is closer to x / s still, so the bound holds either way.
 
 // 1/s for the quantizers: NaN unless s is positive, normal and finite, which sends every element to the divide.
 __device__ __forceinline__ float quant_rcp(float s)
@@ -112,12 +143,13 @@ __device__ __forceinline__ float quant_rcp(float s)
 #define FFKV_QUANT_MARGIN 8
 #endif
 
-// int8: the boundaries are the half-integers: safe when |y - rint(y)| < 0.5 - margin * 2^-23 * |y|.  NaN and
-// infinite y fail the test.
+// int8: the boundaries are the half-integers: safe when |y - r| < 0.5 - margin * 2^-23 * (|r| + 0.5), r = rint(y).
+// Where the test can pass |y| <= |r| + 0.5, so the margin is at least FFKV_QUANT_MARGIN of y's ulps; taking it from
+// r leaves y itself only in the difference.  NaN and infinite y fail the test.
 __device__ __forceinline__ bool quant_i8_safe(float y, float r)
 {
-    return __builtin_fabsf(y - r) <
-           __builtin_fmaf(-__builtin_fabsf(y), FFKV_QUANT_MARGIN * 0x1p-23f, 0.5f - 0x1p-40f);
+    return __builtin_fabsf(y - r) < __builtin_fmaf(-__builtin_fabsf(r), FFKV_QUANT_MARGIN * 0x1p-23f,
+                                                   0.5f - FFKV_QUANT_MARGIN * 0x1p-24f - 0x1p-40f);
 }
 
 // e4m3: in the normal range the boundaries are the midpoints between neighbouring codes, where the 20 fp32
@@ -139,20 +171,26 @@ template <bool INT8>
 __device__ __forceinline__ void quant8(const float* x, float s, uint32_t* w)
 {
     const float rs = quant_rcp(s);
-    bool        safe = true;
+    bool        safe = true;  // fp8: every value of the lane is safe
+    uint64_t    bad = 0;      // int8: the lanes holding an unsafe value (one compare and a scalar OR per value)
     if constexpr (INT8)
     {
+        // y + 1.5 * 2^23 rounds y to the nearest integer r, ties to even (|y| < 2^22), and holds r in the low bits
+        // of the sum: the sum's low byte is r's two's-complement code.  With s = absmax / 127 (the row's finite
+        // absmax) |y| <= 127 * (1 + 3 * 2^-24), so r needs no clamp; with any other s, rs is NaN and so is y.
         uint32_t c[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i)
         {
             const float y = x[i] * rs;
-            const float r = __builtin_rintf(y);
-            safe = safe && quant_i8_safe(y, r);
-            c[i] = static_cast<uint32_t>(static_cast<int32_t>(__builtin_fminf(__builtin_fmaxf(r, -127.0f), 127.0f)));
+            const float m = y + 0x1.8p23f;
+            bad |= __builtin_amdgcn_ballot_w64(!quant_i8_safe(y, m - 0x1.8p23f));
+            c[i] = f2u(m);
         }
-        w[0] = (c[0] & 0xffu) | ((c[1] & 0xffu) << 8) | ((c[2] & 0xffu) << 16) | (c[3] << 24);
-        w[1] = (c[4] & 0xffu) | ((c[5] & 0xffu) << 8) | ((c[6] & 0xffu) << 16) | (c[7] << 24);
+#pragma unroll
+        for (int k = 0; k < 2; ++k)  // bytes 0 of c[4k .. 4k+3]
+            w[k] = __builtin_amdgcn_perm(__builtin_amdgcn_perm(c[4 * k + 3], c[4 * k + 2], 0x04000c0cu),
+                                         __builtin_amdgcn_perm(c[4 * k + 1], c[4 * k], 0x0c0c0400u), 0x07060100u);
     }
     else
     {
@@ -178,7 +216,7 @@ __device__ __forceinline__ void quant8(const float* x, float s, uint32_t* w)
                    (f32_to_e4m3(y[4 * k + 3]) << 24);
 #endif
     }
-    if (__builtin_expect(!__all(safe), 0))
+    if (__builtin_expect(INT8 ? bad != 0 : !__all(safe), 0))
     {
 #pragma unroll
         for (int i = 0; i < 8; ++i)

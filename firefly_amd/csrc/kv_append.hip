@@ -42,12 +42,7 @@ __device__ __forceinline__ void put_row8(const Raw8& raw, void* cache, size_t ds
                     const float v = __builtin_fabsf(x[i]);
                     amax = v > amax ? v : amax;  // NaN never compares greater: ignored
                 }
-#pragma unroll
-                for (int off = 1; off < LPR; off <<= 1)
-                {
-                    const float o = __shfl_xor(amax, off, 64);
-                    amax = o > amax ? o : amax;
-                }
+                amax = group_max<LPR>(amax);
                 sc = amax / 127.0f;
                 if (lane == 0) scale_out[dst_row] = amax == 0.0f ? 0.0f : sc;
                 if (amax == 0.0f) sc = 1.0f;  // an all-zero row gives codes 0 either way

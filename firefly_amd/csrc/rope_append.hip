@@ -85,12 +85,7 @@ __device__ __forceinline__ void append_row(void* cache, float* scales, int h, si
             amax = u > amax ? u : amax;  // NaN never compares greater: ignored
             amax = w > amax ? w : amax;
         }
-#pragma unroll
-        for (int off = 1; off < LPR; off <<= 1)
-        {
-            const float o = __shfl_xor(amax, off, 64);
-            amax = o > amax ? o : amax;
-        }
+        amax = group_max<LPR>(amax);
         sc = amax == 0.0f ? 0.0f : amax / 127.0f;
         if (lane == 0) scales[dst_row] = sc;
     }
