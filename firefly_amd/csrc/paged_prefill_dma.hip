@@ -692,7 +692,7 @@ void paged_prefill_dma(PrefillArgs a)
     };
 
     // Online softmax of a step's scores: the probabilities pv (int8: times the keys' V scales).
-    auto softmax = [&](int si, const uint8_t* stage, int okm, const f32x4 (&s)[RG][KP], float (&pv)[RG][KP * 4])
+    auto softmax = [&](int si, const uint8_t* stage, int okm, f32x4 (&s)[RG][KP], float (&pv)[RG][KP * 4])
     {
         const int pg0 = pg_lo + si * KP;
         // uniform: every key of the step is visible to every column of the wave
@@ -700,20 +700,11 @@ void paged_prefill_dma(PrefillArgs a)
 #pragma unroll
         for (int gi = 0; gi < RG; ++gi)
         {
-            float sc[KP * 4];
-            float mt = kNegInf;
-            if (unmasked)
-            {
+            // the scores are masked in place, so both paths leave them in the product registers (no copies)
+            if constexpr (CT == FP8)
 #pragma unroll
-                for (int u = 0; u < KP; ++u)
-#pragma unroll
-                    for (int i = 0; i < 4; ++i)
-                    {
-                        sc[4 * u + i] = CT == FP8 ? s[gi][u][i] * k_sign : s[gi][u][i];
-                        mt = fmaxf(mt, sc[4 * u + i]);
-                    }
-            }
-            else
+                for (int u = 0; u < KP; ++u) s[gi][u] *= k_sign;
+            if (!unmasked)
             {
                 const int kr = kend[gi] - pg0 * kBlockSize - 4 * g;  // key 4g + i of page u visible iff 16u + i < kr
 #pragma unroll
@@ -722,10 +713,19 @@ void paged_prefill_dma(PrefillArgs a)
                     for (int i = 0; i < 4; ++i)
                     {
                         const bool vis = ((okm >> u) & 1) && u * kBlockSize + i < kr;
-                        sc[4 * u + i] = vis ? (CT == FP8 ? s[gi][u][i] * k_sign : s[gi][u][i]) : kNegInf;
-                        mt = fmaxf(mt, sc[4 * u + i]);
+                        s[gi][u][i] = vis ? s[gi][u][i] : kNegInf;
                     }
             }
+            float sc[KP * 4];
+            float mt = kNegInf;
+#pragma unroll
+            for (int u = 0; u < KP; ++u)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                {
+                    sc[4 * u + i] = s[gi][u][i];
+                    mt = fmaxf(mt, sc[4 * u + i]);
+                }
             mt = swap_max(mt);
             const bool upd = mt > m_run[gi] + thr_raw;  // false while the column has seen no key (mt = -inf)
             if (__any(upd))
