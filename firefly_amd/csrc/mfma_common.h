@@ -214,15 +214,17 @@ __device__ __forceinline__ float xor_sum(float x)
 // The same reductions with gfx950's row swaps, which move the values between rows in VALU without an LDS round
 // trip: permlane16_swap(x, x) returns rows (0, 0, 2, 2) and (1, 1, 3, 3) of x, permlane32_swap(x, x) halves
 // (0, 0) and (1, 1).  Both operand orders give the same bits, and the same bits as xor_max / xor_sum.  (Measured:
-// about 4 % faster in the LDS-bound prefill; no gain in the decode, which keeps the LDS permutes.)
+// about 4 % faster in the LDS-bound prefill; no gain in the decode, which keeps the LDS permutes.)  swap_max takes
+// IEEE maximum (one v_maximum3_f32; fmaxf would first quiet both swapped values, two more instructions), which
+// differs from xor_max only for NaN, which it propagates.
 __device__ __forceinline__ float swap_max(float x)
 {
     const uint32_t u = __float_as_uint(x);
     const auto     r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
-    const float    y = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    const float    y = __builtin_elementwise_maximum(__uint_as_float(r[0]), __uint_as_float(r[1]));
     const uint32_t v = __float_as_uint(y);
     const auto     h = __builtin_amdgcn_permlane32_swap(v, v, false, false);
-    return fmaxf(__uint_as_float(h[0]), __uint_as_float(h[1]));
+    return __builtin_elementwise_maximum(__uint_as_float(h[0]), __uint_as_float(h[1]));
 }
 
 __device__ __forceinline__ float swap_sum(float x)

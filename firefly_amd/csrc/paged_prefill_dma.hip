@@ -258,6 +258,10 @@ void paged_prefill_dma(PrefillArgs a)
     // 8-bit codes are exact in f16 as in bf16: with bf16 score products (BF), their PV products still take f16
     // V^T and P^T, so P needs one product instead of a bf16 hi + lo pair.
     constexpr bool V16 = FFKV_PREFILL_V16 && Q8 && BF;
+    // f16 P (f16 caches, and the f16 PV products of fp8 caches): the denominator sums the rounded P that the
+    // products take, two values per v_dot2_f32_f16, in place of one add per p.  int8's P carries the keys' V
+    // scales, so its denominator sums p itself, as do bf16's hi + lo pairs.
+    constexpr bool L_DOT = !(BF && !V16) && CT != I8;
 
     // NS stages (three by default), each [K tile | V tile | int8 scales] of KP pages, key-major, swizzled chunks
     __shared__ __align__(16) uint8_t s_st0[2 * C::TILEB + C::SCB];
@@ -606,6 +610,7 @@ void paged_prefill_dma(PrefillArgs a)
     }
     const float thr_raw = 8.0f / c_log2;
     float       m_run[RG], l_run[RG];
+    float       m_thr[RG], m_neg[RG];  // m_run + thr_raw, and -m_run * c_log2 (0 before the first key)
     f32x4       acc[RG][NT];
 
     // Smallest causal limit over the wave's active columns: steps wholly below it need no mask.
@@ -726,22 +731,25 @@ void paged_prefill_dma(PrefillArgs a)
                     sc[4 * u + i] = s[gi][u][i];
                     mt = fmaxf(mt, sc[4 * u + i]);
                 }
-            mt = swap_max(mt);
-            const bool upd = mt > m_run[gi] + thr_raw;  // false while the column has seen no key (mt = -inf)
-            if (__any(upd))
+            // the lane's maximum decides whether any column needs a new reference; only then do the column
+            // maxima cross the lanes (a column's 16 keys sit in 4 lanes)
+            if (__any(mt > m_thr[gi]))  // false while the column has seen no key (mt = -inf)
             {
+                mt = swap_max(mt);
+                const bool  upd = mt > m_thr[gi];
                 const float alpha = upd ? __builtin_amdgcn_exp2f((m_run[gi] - mt) * c_log2) : 1.0f;  // 0 at first
                 l_run[gi] *= alpha;
 #pragma unroll
                 for (int n = 0; n < NT; ++n) acc[gi][n] *= alpha;
                 m_run[gi] = upd ? mt : m_run[gi];
+                m_thr[gi] = m_run[gi] + thr_raw;
+                m_neg[gi] = m_run[gi] == kNegInf ? 0.0f : -m_run[gi] * c_log2;  // no key yet: every p is 0
             }
-            const float mneg = m_run[gi] == kNegInf ? 0.0f : -m_run[gi] * c_log2;  // no key yet: every p is 0
 #pragma unroll
             for (int e = 0; e < KP * 4; ++e)
             {
-                pv[gi][e] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[e], c_log2, mneg));
-                l_run[gi] += pv[gi][e];
+                pv[gi][e] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[e], c_log2, m_neg[gi]));
+                if constexpr (!L_DOT) l_run[gi] += pv[gi][e];
             }
         }
         if constexpr (CT == I8)  // per-token V scales multiply P (the denominator keeps the unscaled p)
@@ -810,8 +818,10 @@ void paged_prefill_dma(PrefillArgs a)
                     }
                     else
                     {
-                        ph[e] = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, h2));
+                        const h2 hp = __builtin_convertvector(v, h2);
+                        ph[e] = __builtin_bit_cast(uint32_t, hp);
                         pl[e] = 0u;
+                        if constexpr (L_DOT) l_run[gi] = __builtin_amdgcn_fdot2(hp, h2{1, 1}, l_run[gi], false);
                     }
                 }
                 phi[gi] = __builtin_bit_cast(XP, u32x4{ph[0], ph[1], ph[2], ph[3]});
@@ -846,6 +856,8 @@ void paged_prefill_dma(PrefillArgs a)
     for (int gi = 0; gi < RG; ++gi)
     {
         m_run[gi] = kNegInf;
+        m_thr[gi] = kNegInf;
+        m_neg[gi] = 0.0f;
         l_run[gi] = 0.0f;
 #pragma unroll
         for (int n = 0; n < NT; ++n) acc[gi][n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
