@@ -68,6 +68,16 @@ def test_head_shapes(ff, gpu, D, G):
     _check(ff, gpu, c, 2e-3)
 
 
+@pytest.mark.parametrize("kv", ["i8", "fp8"])
+def test_head_dim_64_quantized(ff, gpu, kv):
+    """Quantize-on-append with 8 lanes per row (head_dim 64: the int8 row maximum over two quads and their
+    mirror), pages and scales bit-exact, then the decode."""
+    rng = np.random.default_rng(64 + len(kv))
+    ctx = rng.integers(0, 500, size=6)
+    c = cases.make_case(640 + len(kv), 6, 8, 2, 64, ctx, act="bf16", kv=kv, S=3, input_scale=1 / 8)
+    _check(ff, gpu, c, 2e-2)
+
+
 @pytest.mark.parametrize("act,kv", [("f16", "f16"), ("f32", "bf16"), ("bf16", "f16"), ("bf16", "i8"), ("f16", "i8"),
                                     ("bf16", "fp8"), ("f32", "fp8")])
 def test_head_dim_256_dtypes(ff, gpu, act, kv):

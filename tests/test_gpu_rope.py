@@ -79,15 +79,18 @@ def test_rope_append_bit_exact(ff, gpu, act, kv, S):
 
 
 @pytest.mark.parametrize("D", [64, 256])
-def test_rope_append_head_dims(ff, gpu, D):
-    c, qn = _setup(ff, gpu, 50 + D, 3, 8, 2, D, [5, 31, 1000], "bf16", "bf16", 3)
-    print(f"case rope_append D={D}", flush=True)
+@pytest.mark.parametrize("kv", ["bf16", "i8", "fp8"])
+def test_rope_append_head_dims(ff, gpu, D, kv):
+    """Other head dims (4 and 16 lanes per head row: the int8 row maximum over one quad, and over a full 16-lane
+    row with its mirrors)."""
+    c, qn = _setup(ff, gpu, 50 + D + len(kv), 3, 8, 2, D, [5, 31, 1000], "bf16", kv, 3)
+    print(f"case rope_append D={D} kv={kv}", flush=True)
     import torch
 
     q, k, v = gu.to_dev(qn, c.act, gpu), gu.to_dev(c.k_new, c.act, gpu), gu.to_dev(c.v_new, c.act, gpu)
     kp, vp, ks, vs = _pools(c, gpu)
     ff.rope_append_kv_cache(q, k, v, kp, vp, torch.from_numpy(c.block_table).to(gpu),
-                            torch.from_numpy(c.ctx).to(gpu), THETA)
+                            torch.from_numpy(c.ctx).to(gpu), THETA, k_scale=ks, v_scale=vs)
     torch.cuda.synchronize()
     k_ref = O.rope(c.k_new, c.act, c.ctx, THETA)
     assert np.array_equal(_host(q, c.act), O.rope(qn, c.act, c.ctx, THETA))
