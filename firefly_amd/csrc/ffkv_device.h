@@ -81,14 +81,20 @@ __device__ __forceinline__ float e4m3_to_f32(uint32_t q)
     return u2f(f2u(v) | ((q & 0x80u) << 24));
 }
 
-// Largest of v over aligned groups of N lanes (N a power of two up to 32), in every lane of the group; v is never
-// NaN here (absolute-value maxima that skip NaN).  Quad permutations and the 8- and 16-lane mirrors are DPP
+// Largest of v (or with SUM its sum) over aligned groups of N lanes (N a power of two up to 32), in every lane of the
+// group; for the maximum v is never NaN here (absolute-value maxima that skip NaN).  Every lane must be active.  Quad permutations and the 8- and 16-lane mirrors are DPP
 // operands of the compare, the step between 16-lane rows gfx950's row swap: no LDS round trip.
-template <int N>
-__device__ __forceinline__ float group_max(float v)
+template <int N, bool SUM = false>
+__device__ __forceinline__ float group_reduce(float v)
 {
     static_assert(N >= 1 && N <= 32 && (N & (N - 1)) == 0, "groups of 1, 2, 4, 8, 16 or 32 lanes");
-    auto take = [&v](float o) { v = o > v ? o : v; };
+    auto take = [&v](float o)
+    {
+        if constexpr (SUM)
+            v += o;
+        else
+            v = o > v ? o : v;
+    };
     auto dpp = [](float x, auto ctrl)
     {
         return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x),
@@ -104,9 +110,22 @@ __device__ __forceinline__ float group_max(float v)
                                                         false, false);  // rows (0, 0, 2, 2) and (1, 1, 3, 3)
         const float a = __builtin_bit_cast(float, static_cast<uint32_t>(r[0]));
         const float b = __builtin_bit_cast(float, static_cast<uint32_t>(r[1]));
-        v = a > b ? a : b;
+        v = SUM ? a + b : (a > b ? a : b);
     }
     return v;
+}
+
+template <int N>
+__device__ __forceinline__ float group_max(float v)
+{
+    return group_reduce<N, false>(v);
+}
+
+// Sum of v over aligned groups of N lanes, in every lane of the group, with the same lane steps as group_max.
+template <int N>
+__device__ __forceinline__ float group_sum(float v)
+{
+    return group_reduce<N, true>(v);
 }
 
 __device__ __forceinline__ int32_t quant_i8(float x, float s)

@@ -12,7 +12,10 @@
 // 64/(D/8) tokens per step and the workgroup 256/(D/8).  Head dims other than 64, 128 and 256 (multiples of 8 up
 // to 128, which the reference's decode takes) run with 16 lanes per token, those past head_dim/8 idle.  Each token slot keeps its own online-softmax state in
 // registers; the slots are merged with cross-lane shuffles inside a wave and through LDS across waves.
-// The softmax runs in base 2 with log2(e) folded into the score scale.
+// The softmax runs in base 2 with log2(e) folded into the score scale, against a reference maximum that moves only
+// when a score passes it by 2^8.  A token's dot product crosses its lanes with DPP steps (no LDS), and each loop
+// trip issues the loads of several token groups (and the next trip's block-table entries) before using them: the
+// kernel is bound by memory latency, not by its arithmetic.
 #include "ffkv_device.h"
 #include "ffkv_internal.h"
 
@@ -21,6 +24,13 @@ namespace ffkv
 
 namespace
 {
+
+#ifndef FFKV_GENERIC_U16
+#define FFKV_GENERIC_U16 4
+#endif
+#ifndef FFKV_GENERIC_U32
+#define FFKV_GENERIC_U32 2
+#endif
 
 constexpr float kNegBig = -1e30f;  // finite "minus infinity" seed, as in attention.cu:323
 
@@ -31,28 +41,6 @@ __device__ __forceinline__ int row_tokens(const DecodeArgs& a, int b)
     int64_t L = static_cast<int64_t>(a.context_lens[b]) + 1;  // +1: the token appended this step (:320)
     if (L > a.cap_tokens) L = a.cap_tokens;
     return L < 0 ? 0 : static_cast<int>(L);
-}
-
-// Load 8 dequantized cache elements of row `row` (page*16 + slot)*Hkv + h at dims [d0, d0+8).
-template <int CT>
-__device__ __forceinline__ void load_kv8(const void* cache, const float* scale, size_t row, int D, int h, int d0,
-                                         float* x)
-{
-    Raw8 raw;
-    load_raw8<CT>(cache, row * D + d0, raw);
-    unpack8<CT>(raw, x);
-    if constexpr (CT == I8)
-    {
-        const float s = scale[row];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) x[i] *= s;
-    }
-    else if constexpr (CT == FP8)
-    {
-        const float s = scale[h];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) x[i] *= s;
-    }
 }
 
 }  // namespace
@@ -105,26 +93,69 @@ __global__ __launch_bounds__(256) void paged_decode_generic(DecodeArgs a)
         for (int i = 0; i < 8; ++i) acc[g][i] = 0.0f;
     }
 
+    // U consecutive token groups per loop trip: their table entries, then all their K / V loads, go out before
+    // any of them is used, so U times the bytes of one group are in flight per wave (fewer for fp32 caches, whose
+    // raw rows take twice the registers, and none extra for the 16-head groups, which already fill them).
+    constexpr int  U = GP >= 16 ? 1 : (Storage<CT>::bytes == 4 ? FFKV_GENERIC_U32 : FFKV_GENERIC_U16);
+    // The table entries of the next trip are requested while this trip's tokens are computed.
     const int32_t* table = a.block_table + static_cast<int64_t>(b) * a.max_blocks;
-    for (int base = begin; base < end; base += TPI)
+    auto load_phys = [&](int base, int (&ph)[U])
     {
-        const int j = base + slot;
-        bool      valid = j < end;
-        int       phys = -1;
-        if (valid)
+#pragma unroll
+        for (int u = 0; u < U; ++u)
         {
-            phys = table[j >> 4];
-            valid = phys >= 0 && phys < a.num_blocks;
+            const int j = base + u * TPI + slot;
+            ph[u] = j < end ? table[j >> 4] : -1;
         }
-        const size_t row = (static_cast<size_t>(valid ? phys : 0) * kBlockSize + (j & 15)) * a.num_kv_heads + kvh;
-
-        float s[GP];
-        float v[8];
-        if (valid && act)
+    };
+    int phys[U];
+    load_phys(begin, phys);
+    for (int base = begin; base < end; base += U * TPI)
+    {
+        bool   valid[U];
+        size_t row[U];
+        float  ks[U], vs[U];  // int8: the tokens' scales
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+        {
+            const int j = base + u * TPI + slot;
+            valid[u] = j < end && phys[u] >= 0 && phys[u] < a.num_blocks;
+            row[u] = (static_cast<size_t>(valid[u] ? phys[u] : 0) * kBlockSize + (j & 15)) * a.num_kv_heads + kvh;
+        }
+        Raw8 kr[U], vr[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+        {
+            ks[u] = vs[u] = 1.0f;
+            if (valid[u] && act)
+            {
+                load_raw8<CT>(a.k_cache, row[u] * D + lane * 8, kr[u]);
+                load_raw8<CT>(a.v_cache, row[u] * D + lane * 8, vr[u]);
+                if constexpr (CT == I8)
+                {
+                    ks[u] = a.k_scale[row[u]];
+                    vs[u] = a.v_scale[row[u]];
+                }
+            }
+            else
+            {
+                kr[u] = Raw8{};
+                vr[u] = Raw8{};
+            }
+        }
+        load_phys(base + U * TPI, phys);
+#pragma unroll
+        for (int u = 0; u < U; ++u)
         {
             float k[8];
-            load_kv8<CT>(a.k_cache, a.k_scale, row, D, kvh, lane * 8, k);
-            load_kv8<CT>(a.v_cache, a.v_scale, row, D, kvh, lane * 8, v);
+            unpack8<CT>(kr[u], k);
+            if constexpr (CT == I8 || CT == FP8)
+            {
+                const float sk = CT == I8 ? ks[u] : a.k_scale[kvh];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) k[i] *= sk;
+            }
+            float s[GP];
 #pragma unroll
             for (int g = 0; g < GP; ++g)
             {
@@ -133,33 +164,39 @@ __global__ __launch_bounds__(256) void paged_decode_generic(DecodeArgs a)
                 for (int i = 0; i < 8; ++i) d = __builtin_fmaf(q[g][i], k[i], d);
                 s[g] = d;
             }
-        }
-        else
-        {
+            // every lane takes part in the sums (DPP lane steps); a token's lanes are a contiguous, aligned group
 #pragma unroll
-            for (int g = 0; g < GP; ++g) s[g] = 0.0f;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) v[i] = 0.0f;
-        }
-        // every lane takes part in the shuffles; a token's lanes are a contiguous, aligned group
-#pragma unroll
-        for (int g = 0; g < GP; ++g)
-#pragma unroll
-            for (int off = LPT / 2; off > 0; off >>= 1) s[g] += shfl_xor(s[g], off);
+            for (int g = 0; g < GP; ++g) s[g] = group_sum<LPT>(s[g]);
 
-        if (valid)
-        {
-#pragma unroll
-            for (int g = 0; g < GP; ++g)
+            // Online softmax with a lazy reference: m moves (and l, acc are rescaled) only when a score exceeds it
+            // by more than 8 (log2 units), so p = 2^(s - m) < 2^8 and most tokens only add p and p * v.
+            if (valid[u])
             {
-                const float sg = s[g] * a.scale_log2;
-                const float mn = fmaxf(m[g], sg);
-                const float alpha = fast_exp2(m[g] - mn);
-                const float p = fast_exp2(sg - mn);
-                l[g] = __builtin_fmaf(l[g], alpha, p);
+                float v[8];  // unpacked only now: fewer registers live across the dot products and sums
+                unpack8<CT>(vr[u], v);
+                if constexpr (CT == I8 || CT == FP8)
+                {
+                    const float sv = CT == I8 ? vs[u] : a.v_scale[kvh];
 #pragma unroll
-                for (int i = 0; i < 8; ++i) acc[g][i] = __builtin_fmaf(acc[g][i], alpha, p * v[i]);
-                m[g] = mn;
+                    for (int i = 0; i < 8; ++i) v[i] *= sv;
+                }
+#pragma unroll
+                for (int g = 0; g < GP; ++g)
+                {
+                    const float sg = s[g] * a.scale_log2;
+                    if (sg > m[g] + 8.0f)
+                    {
+                        const float alpha = fast_exp2(m[g] - sg);  // 0 for the slot's first token
+                        l[g] *= alpha;
+#pragma unroll
+                        for (int i = 0; i < 8; ++i) acc[g][i] *= alpha;
+                        m[g] = sg;
+                    }
+                    const float p = fast_exp2(sg - m[g]);
+                    l[g] += p;
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) acc[g][i] = __builtin_fmaf(p, v[i], acc[g][i]);
+                }
             }
         }
     }
