@@ -419,6 +419,21 @@ void paged_prefill_dma(PrefillArgs a)
             }
         }
 
+    if constexpr (CT == FP8)
+    {
+        // A negative K scale negates every score: q's signs are flipped once here instead of the scores at every
+        // step (exact: a sign flip commutes with the products and their rounding).
+        if (a.k_scale[kvh] < 0.0f)
+#pragma unroll
+            for (int gi = 0; gi < RG; ++gi)
+#pragma unroll
+                for (int j = 0; j < KSTEPS; ++j)
+                {
+                    qhi[gi][j] = __builtin_bit_cast(X8, __builtin_bit_cast(u32x4, qhi[gi][j]) ^ 0x80008000u);
+                    qlo[gi][j] = __builtin_bit_cast(X8, __builtin_bit_cast(u32x4, qlo[gi][j]) ^ 0x80008000u);
+                }
+    }
+
     // Nothing else is in flight from here on but the page loads: the pipeline's waits count only those.
     wait_vm<0>();
 
@@ -598,11 +613,9 @@ void paged_prefill_dma(PrefillArgs a)
     // denominator share the reference, so the result is the same softmax.
     float c_log2 = a.scale_log2;
     float v_head_scale = 1.0f;
-    float k_sign = 1.0f;  // fp8: the sign of the head's K scale, applied to the raw scores
-    if constexpr (CT == FP8)  // per-head scales: K's into the score scale, V's onto the output
+    if constexpr (CT == FP8)  // per-head scales: K's into the score scale (its sign into q), V's onto the output
     {
         const float ks = a.k_scale[kvh];
-        k_sign = ks < 0.0f ? -1.0f : 1.0f;
         // a zero scale (every score 0: uniform weights, as in decode) keeps a tiny positive factor, so the raw
         // reference maximum, its threshold and masked keys' -inf scores stay well defined
         c_log2 = fmaxf(c_log2 * __builtin_fabsf(ks), 1e-30f);
@@ -706,9 +719,6 @@ void paged_prefill_dma(PrefillArgs a)
         for (int gi = 0; gi < RG; ++gi)
         {
             // the scores are masked in place, so both paths leave them in the product registers (no copies)
-            if constexpr (CT == FP8)
-#pragma unroll
-                for (int u = 0; u < KP; ++u) s[gi][u] *= k_sign;
             if (!unmasked)
             {
                 const int kr = kend[gi] - pg0 * kBlockSize - 4 * g;  // key 4g + i of page u visible iff 16u + i < kr
