@@ -531,6 +531,9 @@ def main(argv=None) -> int:
     ap.add_argument("--skip-c2", action="store_true",
                     help="skip the C2 steps, the device copy and the CPU baseline (profiling other configurations "
                          "alone); the headline fields are then null")
+    ap.add_argument("--lib", default=None,
+                    help="time another build of libffkv.so (for example one made from an earlier commit in a git "
+                         "worktree) instead of firefly_amd/libffkv.so")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run one 1 GiB device-to-device copy (a kernel of known read/write bytes, used to "
                          "scale rocprofv3 FETCH_SIZE/WRITE_SIZE counters)")
@@ -546,6 +549,11 @@ def main(argv=None) -> int:
 
     import firefly_amd as ff
 
+    if args.lib is not None:
+        from pathlib import Path
+
+        ff.LIB_PATH = Path(args.lib).resolve()
+        ff.lib = ff._load()
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
