@@ -101,12 +101,23 @@ def device_copy_rate(torch, dev, stream, nbytes: int = 1 << 30) -> dict:
 BF16_MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense bf16
 
 
-def _events_us(fn, n: int, stream) -> float:
-    """Mean duration in us of fn(i) over n back-to-back calls, HIP events on the launch stream."""
+def _events_us(fn, n: int, stream, warm_ms: float = 50.0) -> float:
+    """Mean duration in us of fn(i) over n back-to-back calls, HIP events on the launch stream, after at least
+    warm_ms of untimed calls (a GPU that has been idle runs its first tens of milliseconds of work up to 15 % slow,
+    which would otherwise bias whichever configuration is measured first)."""
+    import time
+
     import torch
 
-    for i in range(3):
+    t0 = time.perf_counter()
+    i = 0
+    while True:
         fn(i)
+        i += 1
+        if i >= 3 and i % 4 == 0:
+            torch.cuda.synchronize()
+            if (time.perf_counter() - t0) * 1e3 >= warm_ms or i >= 400:
+                break
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(stream)
