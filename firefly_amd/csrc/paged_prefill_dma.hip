@@ -75,7 +75,7 @@ constexpr int kXcds = 8;  // MI355X: workgroups are dealt to 8 XCDs (separate L2
 #endif
 
 #ifndef FFKV_PREFILL_I8_BF
-#define FFKV_PREFILL_I8_BF 1  // int8 with bf16 q: bf16 score products (q whole) and f16 PV products (P whole)
+#define FFKV_PREFILL_I8_BF 0  // int8 with bf16 q: bf16 score products (1) or f16 ones with q converted whole (0)
 #endif
 
 #ifndef FFKV_PREFILL_RG
@@ -240,15 +240,20 @@ void paged_prefill_dma(PrefillArgs a)
     constexpr int  W = 8 / RG;  // waves per workgroup
     constexpr int  EB = kElemBytes<CT>;
     constexpr bool Q8 = EB == 1;
-    // int8 codes take bf16 score products beside a bf16 q (exact: 8 significant bits), so q needs no hi / lo split
+    // int8 codes are exact in bf16 and f16 alike; beside a bf16 q they take f16 products (QX16 below) unless
+    // FFKV_PREFILL_I8_BF selects bf16 ones (q whole, codes converted through fp32)
     constexpr bool BF = CT == I8 ? (FFKV_PREFILL_I8_BF && QT != F16) : kBF<CT, QT>;
+    // int8 with a bf16 q and f16 score products (QX16): q converts to f16 exactly (8 significant bits fit in 11),
+    // scaled by a power of two when the wave's largest |q| would not fit f16's range, so it needs no lo part, and
+    // the codes convert to f16 with the one-instruction bias trick instead of through fp32.
+    constexpr bool QX16 = CT == I8 && QT == BF16 && !BF;
     using C = DmaCfg<D, EB, CT == I8, W, PFX>;  // the scale bytes (and their loads, counted in the waits) only for int8
     using M = MType<BF>;
     using X8 = typename M::x8;
     constexpr int  KP = C::KP;
     constexpr int  KSTEPS = D / 32;
     constexpr int  NT = D / 16;
-    constexpr bool NEED_LO = !((QT == BF16 && BF) || (QT == F16 && !BF));
+    constexpr bool NEED_LO = !((QT == BF16 && BF) || (QT == F16 && !BF) || QX16);
     // Load issue per page (one table select and page base per page, then the page's runs) or per run (a 64-bit
     // page-offset select per run).  The per-page form has a third less scalar work and measured 1-6 % faster on the
     // chunked prefill for every cache type and head_dim (since the f16 PV products of 8-bit caches, bf16 queries
@@ -382,7 +387,47 @@ void paged_prefill_dma(PrefillArgs a)
     const bool wave_active = row0 + 16 * RG * wave < R;
 
     // ---- Q^T operands of the wave's RG x 16 query rows -----------------------------------------------------
-    X8 qhi[RG][KSTEPS], qlo[RG][KSTEPS];
+    X8    qhi[RG][KSTEPS], qlo[RG][KSTEPS];
+    float q_unscale = 1.0f;  // QX16: the scores come out scaled by 1 / q_unscale
+    if constexpr (QX16)
+    {
+        float x[RG][KSTEPS][8];
+        float amax = 0.0f;
+#pragma unroll
+        for (int gi = 0; gi < RG; ++gi)
+#pragma unroll
+            for (int j = 0; j < KSTEPS; ++j)
+            {
+                if (col_ok[gi])
+                    load_q8<QT>(a.q, qrow[gi] * D + 32 * j + 8 * g, x[gi][j]);
+                else
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) x[gi][j][e] = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) amax = fmaxf(amax, __builtin_fabsf(x[gi][j][e]));
+            }
+        amax = group_max<32>(fmaxf(amax, __shfl_xor(amax, 32, 64)));  // the wave's largest |q| (NaN skipped)
+        float qs = 1.0f;
+        if (__builtin_expect(amax >= 32768.0f, 0))  // uniform: scale q into f16's range by a power of two
+        {
+            const int e = __builtin_amdgcn_frexp_expf(amax);  // amax < 2^e
+            qs = __builtin_ldexpf(1.0f, 15 - e);              // amax * qs < 2^15
+            q_unscale = __builtin_ldexpf(1.0f, e - 15);
+        }
+#pragma unroll
+        for (int gi = 0; gi < RG; ++gi)
+#pragma unroll
+            for (int j = 0; j < KSTEPS; ++j)
+            {
+                uint32_t w[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    w[e] = __builtin_bit_cast(uint32_t, __builtin_convertvector(
+                                                            f32x2{x[gi][j][2 * e] * qs, x[gi][j][2 * e + 1] * qs}, h2));
+                qhi[gi][j] = qlo[gi][j] = __builtin_bit_cast(X8, u32x4{w[0], w[1], w[2], w[3]});
+            }
+    }
+    else
 #pragma unroll
     for (int gi = 0; gi < RG; ++gi)
 #pragma unroll
@@ -611,7 +656,7 @@ void paged_prefill_dma(PrefillArgs a)
     // with c = scale * log2(e).  The reference moves (and acc / l_run are rescaled) only when a new maximum
     // exceeds it by more than 8 / c, so p stays below 2^8 and most steps rescale nothing; numerator and
     // denominator share the reference, so the result is the same softmax.
-    float c_log2 = a.scale_log2;
+    float c_log2 = a.scale_log2 * q_unscale;
     float v_head_scale = 1.0f;
     if constexpr (CT == FP8)  // per-head scales: K's into the score scale (its sign into q), V's onto the output
     {

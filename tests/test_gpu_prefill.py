@@ -27,7 +27,7 @@ def half_ulp(x, act):
     return 2.0 ** (e - mant - 1)
 
 
-def _run(ff, dev, c, qn, tbl=None, ctx=None, contiguous=False):
+def _run(ff, dev, c, qn, tbl=None, ctx=None, contiguous=False, scale=0.0):
     """Append the case's chunk (k_new/v_new) to its pools, then prefill; returns (out f32 [B,S,Hq,D], ref f64)."""
     import torch
 
@@ -49,13 +49,13 @@ def _run(ff, dev, c, qn, tbl=None, ctx=None, contiguous=False):
         cx = torch.from_numpy(np.ascontiguousarray(ctx)).to(dev)
         ff.append_kv_cache(gu.to_dev(c.k_new, c.act, dev), gu.to_dev(c.v_new, c.act, dev), kp, vp, bt, cx, ks, vs)
         q = gu.to_dev(qn, c.act, dev)
-        out = ff.paged_prefill(q, kp, vp, bt, cx, k_scale=ks, v_scale=vs)
+        out = ff.paged_prefill(q, kp, vp, bt, cx, k_scale=ks, v_scale=vs, scale=scale)
         torch.cuda.synchronize()
         rk, rv = c.k_pool.copy(), c.v_pool.copy()
         rks = None if c.k_scale is None else c.k_scale.copy()
         rvs = None if c.v_scale is None else c.v_scale.copy()
         O.append(c.k_new, c.v_new, c.act, rk, rv, c.kv, tbl, ctx, rks, rvs)
-        ref = O.paged_prefill_f64(qn, c.act, rk, rv, c.kv, tbl, ctx, rks, rvs)
+        ref = O.paged_prefill_f64(qn, c.act, rk, rv, c.kv, tbl, ctx, rks, rvs, scale=scale)
     got = out.float().cpu().numpy().reshape(ref.shape)
     return got, ref
 
@@ -217,6 +217,17 @@ def test_fp8_degenerate_k_scales(ff, gpu, k_scale_kind):
         g = out.float().cpu().numpy().reshape(out32.shape)
         assert np.isfinite(g).all(), f"shared={shared}"
         _check(g, out32.astype(np.float64), d.act, 2e-2)
+
+
+@pytest.mark.parametrize("D", [64, 128, 256])
+def test_prefill_int8_large_q(ff, gpu, D):
+    """bf16 queries beyond f16's range over an int8 cache: the f16 score products take q scaled into range by a
+    power of two (exact) and the softmax scale compensates.  q is N(0,1) * 2^17 and the score scale 2^-17 /
+    sqrt(D), so the softmax is the ordinary one; outputs within the quantized bar of the float64 closed form."""
+    c, qn = _case(170 + D, 3, 16, 4, D, [17, 300, 5], 37, kv="i8")
+    qf = cases.decode(qn, c.act) * np.float32(2.0 ** 17)
+    qn = cases.encode(qf, c.act)
+    _check(*_run(ff, gpu, c, qn, scale=2.0 ** -17 / math.sqrt(D)), c.act, 2e-2)
 
 
 @pytest.mark.parametrize("big", [7.0e4, 3.0e5, float("inf")])
