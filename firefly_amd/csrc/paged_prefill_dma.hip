@@ -74,6 +74,9 @@ constexpr int kXcds = 8;  // MI355X: workgroups are dealt to 8 XCDs (separate L2
 #define FFKV_PREFILL_XCD 1
 #endif
 
+#ifndef FFKV_PREFILL_VCONV
+#define FFKV_PREFILL_VCONV 1  // bf16 pages: V tiles converted to f16 in LDS by the waves that load them
+#endif
 #ifndef FFKV_PREFILL_I8_BF
 #define FFKV_PREFILL_I8_BF 0  // int8 with bf16 q: bf16 score products (1) or f16 ones with q converted whole (0)
 #endif
@@ -214,6 +217,9 @@ __device__ __forceinline__ void mfma_priority(int level)
     }
 }
 
+// Wait for this wave's LDS operations (and scalar loads), leaving the vector-memory counter alone.
+__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xF | (0x7 << 4) | (0x3 << 14)); }
+
 template <int VM>
 __device__ __forceinline__ void wait_vm()
 {
@@ -274,9 +280,12 @@ void paged_prefill_dma(PrefillArgs a)
     __shared__ __align__(16) uint8_t s_st2[kDmaStages<D> >= 3 ? 2 * C::TILEB + C::SCB : 16];
     __shared__ __align__(16) uint8_t s_st3[kDmaStages<D> == 4 ? 2 * C::TILEB + C::SCB : 16];
 
+    __shared__ int s_vover;  // a V value of this workgroup's keys does not fit f16 (VCONV)
+
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    if (tid == 0) s_vover = 0;
     const int c = lane & 15;
     const int g = lane >> 4;
     // Workgroup -> (group, row block).  A group is (row b, kv head) for prefill and (kv head, chunk of prefix
@@ -483,6 +492,20 @@ void paged_prefill_dma(PrefillArgs a)
     wait_vm<0>();
 
     // ---- loads: wave w fetches runs w*RPW .. w*RPW + RPW - 1 (64 chunks each) of the K tile and of the V tile --
+    // (bf16 pages, whose V tiles are converted to f16 in LDS (VCONV): wave w fetches runs w*RPW/2 ..
+    // w*RPW/2 + RPW/2 - 1 of the K tile and the same runs of the V tile, so that every wave converts the same share)
+    constexpr bool VCONV = FFKV_PREFILL_VCONV && CT == BF16;
+    static_assert(!VCONV || C::RPW % 2 == 0, "a wave loads as many V runs as K runs");
+    constexpr int RPP = VCONV ? (C::RPW / 2 < C::CHUNKS / 64 ? C::RPW / 2 : C::CHUNKS / 64) : C::RPP;  // runs per page
+    constexpr int NPW = C::RPW / RPP;  // pages (or parts of one) a wave loads per step
+    static_assert(C::RPW % RPP == 0 && (!VCONV || (C::RPW / 2) % RPP == 0), "a wave's runs cover whole page parts");
+    auto run_is_v = [&](int k) { return VCONV ? k >= C::RPW / 2 : wave * C::RPW + k >= C::IPR; };
+    auto run_lr = [&](int k)
+    {
+        if constexpr (VCONV) return wave * (C::RPW / 2) + (k >= C::RPW / 2 ? k - C::RPW / 2 : k);
+        const int run = wave * C::RPW + k;
+        return run >= C::IPR ? run - C::IPR : run;
+    };
     const FFKV_CONST int32_t* table_row =  // prefix: row 0's table, whose first pfx_blocks entries every row shares
         a.paged ? (const FFKV_CONST int32_t*)(a.block_table + static_cast<int64_t>(b) * a.max_blocks) : nullptr;
     const char* zero_src = reinterpret_cast<const char*>(g_zero_chunks) + 16 * lane;
@@ -494,9 +517,8 @@ void paged_prefill_dma(PrefillArgs a)
 #pragma unroll
     for (int k = 0; k < C::RPW; ++k)
     {
-        const int  run = wave * C::RPW + k;
-        const bool is_v = run >= C::IPR;                  // uniform
-        const int  lr = is_v ? run - C::IPR : run;          // run within its tile
+        const bool is_v = run_is_v(k);                     // uniform
+        const int  lr = run_lr(k);                          // run within its tile
         const int  u = lr * 64 / C::CHUNKS;                 // page of the step
         const int  p = lr * 64 % C::CHUNKS + lane;          // chunk position within the page
         const int  tok = p / C::CPT;
@@ -511,11 +533,7 @@ void paged_prefill_dma(PrefillArgs a)
     }
     const size_t row_bytes = static_cast<size_t>(Hkv) * C::RB;  // one key row of all kv heads
 
-    // This wave's runs lie in one tile (K or V) and cover NPW consecutive pages of the step from page w_u0 on,
-    // RPP runs each; run k lands 1 KiB after run k - 1 in the stage (per-page issue).
-    const int w_run0 = wave * C::RPW;
-    const int w_lr0 = w_run0 >= C::IPR ? w_run0 - C::IPR : w_run0;
-    const int w_u0 = w_lr0 * 64 / C::CHUNKS;
+    // A wave's runs j*RPP .. j*RPP + RPP - 1 lie in one page of one tile (per-page issue).
     // Per-run constants of this wave's loads (uniform): source tensor at kv head kvh, page of the step, LDS
     // destination.  A page's byte offset is row_base + index * page_bytes, with index the physical page (paged) or
     // the page of the row (contiguous keys).
@@ -525,9 +543,8 @@ void paged_prefill_dma(PrefillArgs a)
 #pragma unroll
     for (int k = 0; k < C::RPW; ++k)
     {
-        const int  run = wave * C::RPW + k;
-        const bool is_v = run >= C::IPR;
-        const int  lr = is_v ? run - C::IPR : run;
+        const bool is_v = run_is_v(k);
+        const int  lr = run_lr(k);
         run_u[k] = lr * 64 / C::CHUNKS;
         run_src[k] = static_cast<const char*>(is_v ? a.v_cache : a.k_cache) + static_cast<size_t>(kvh) * C::RB;
         run_dst[k] = (is_v ? C::TILEB : 0) + lr * 64 * 16;
@@ -573,34 +590,34 @@ void paged_prefill_dma(PrefillArgs a)
         if constexpr (PAGE_ISSUE)
         {
 #pragma unroll
-            for (int j = 0; j < C::NPW; ++j)
+            for (int j = 0; j < NPW; ++j)
             {
-                const int u = w_u0 + j;
+                const int u = run_u[j * RPP];
                 uint32_t  idx = page_row[0];  // page_row[u] without a dynamic index (u is uniform, not constant)
 #pragma unroll
                 for (int uu = 1; uu < KP; ++uu) idx = u == uu ? page_row[uu] : idx;
-                const char* base = run_src[0] + row_base + static_cast<uint64_t>(idx) * page_bytes;
+                const char* base = run_src[j * RPP] + row_base + static_cast<uint64_t>(idx) * page_bytes;
                 const bool  fl = (full >> u) & 1;
                 const bool  pres = (okm >> u) & 1;
                 const int   tok0 = (pg_lo + si * KP + u) * kBlockSize;
                 if (fl)
                 {
 #pragma unroll
-                    for (int r = 0; r < C::RPP; ++r)
+                    for (int r = 0; r < RPP; ++r)
                     {
-                        const int k = j * C::RPP + r;
-                        load_lds16(base, voff[k], (const FFKV_LDS void*)(stage + run_dst[0] + k * 1024));
+                        const int k = j * RPP + r;
+                        load_lds16(base, voff[k], (const FFKV_LDS void*)(stage + run_dst[k]));
                     }
                 }
                 else
                 {
 #pragma unroll
-                    for (int r = 0; r < C::RPP; ++r)
+                    for (int r = 0; r < RPP; ++r)
                     {
-                        const int  k = j * C::RPP + r;
+                        const int  k = j * RPP + r;
                         const bool take = pres && tok0 + vtok[k] < L;
                         load_lds16(take ? static_cast<const void*>(base + voff[k]) : static_cast<const void*>(zero_src),
-                                   (const FFKV_LDS void*)(stage + run_dst[0] + k * 1024));
+                                   (const FFKV_LDS void*)(stage + run_dst[k]));
                     }
                 }
             }
@@ -755,8 +772,9 @@ void paged_prefill_dma(PrefillArgs a)
     };
 
     // Online softmax of a step's scores: the probabilities pv (int8: times the keys' V scales).
-    auto softmax = [&](int si, const uint8_t* stage, int okm, f32x4 (&s)[RG][KP], float (&pv)[RG][KP * 4])
+    auto softmax = [&]<bool VC>(int si, const uint8_t* stage, int okm, f32x4 (&s)[RG][KP], float (&pv)[RG][KP * 4])
     {
+        constexpr bool LD = L_DOT || VC;  // the f16 P of converted bf16 V tiles sums by dot products too
         const int pg0 = pg_lo + si * KP;
         // uniform: every key of the step is visible to every column of the wave
         const bool unmasked = okm == (1 << KP) - 1 && (pg0 + KP) * kBlockSize <= kmin;
@@ -804,7 +822,7 @@ void paged_prefill_dma(PrefillArgs a)
             for (int e = 0; e < KP * 4; ++e)
             {
                 pv[gi][e] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[e], c_log2, m_neg[gi]));
-                if constexpr (!L_DOT) l_run[gi] += pv[gi][e];
+                if constexpr (!LD) l_run[gi] += pv[gi][e];
             }
         }
         if constexpr (CT == I8)  // per-token V scales multiply P (the denominator keeps the unscaled p)
@@ -826,7 +844,8 @@ void paged_prefill_dma(PrefillArgs a)
     // one product (11 bits); otherwise bf16 P is a hi + lo pair, which keeps 16 significant bits in two products.
     auto pv_mma = [&]<bool V16>(const uint8_t* stage, const float (&pv)[RG][KP * 4])
     {
-        constexpr bool PBF = BF && !V16;  // P^T and V^T operand type
+        constexpr bool PBF = BF && !V16;           // P^T and V^T operand type
+        constexpr bool LD = L_DOT || (CT == BF16 && V16);  // bf16 pages with V tiles converted to f16
         using MP = MType<PBF>;
         using XP = typename MP::x8;
         auto vread = [&](int n, int u0) -> XP  // V^T operand of output tile n over pages u0, u0 + 1
@@ -876,7 +895,7 @@ void paged_prefill_dma(PrefillArgs a)
                         const h2 hp = __builtin_convertvector(v, h2);
                         ph[e] = __builtin_bit_cast(uint32_t, hp);
                         pl[e] = 0u;
-                        if constexpr (L_DOT) l_run[gi] = __builtin_amdgcn_fdot2(hp, h2{1, 1}, l_run[gi], false);
+                        if constexpr (LD) l_run[gi] = __builtin_amdgcn_fdot2(hp, h2{1, 1}, l_run[gi], false);
                     }
                 }
                 phi[gi] = __builtin_bit_cast(XP, u32x4{ph[0], ph[1], ph[2], ph[3]});
@@ -907,21 +926,42 @@ void paged_prefill_dma(PrefillArgs a)
     // reads), so "step si has landed" is always vmcnt <= the loads of steps si + 1 .. si + NS - 2.
     constexpr int NS = kDmaStages<D>;
     constexpr int LPS = C::RPW + C::SCB / 256;  // loads per wave and step
-#pragma unroll
-    for (int gi = 0; gi < RG; ++gi)
+
+    // bf16 pages (VCONV): every wave converts the V runs it loads to f16 in place, in LDS, as soon as its own loads
+    // of them have landed and before the barrier that publishes the step; the PV products then take f16 V^T and P
+    // in one product instead of bf16 P's hi + lo pair.  bf16 values are exact in f16 from 2^-14 to 65280 (below
+    // 2^-14 they round to f16 subnormals, an absolute error of at most 2^-25).  A value of 65520 or more (or
+    // infinite) becomes infinite and makes the accumulators infinite or NaN (p * inf, 0 * inf): the workgroup then
+    // runs the whole pipeline again on the bf16 path.
+    auto convert_v = [&](uint8_t* stage)
     {
-        m_run[gi] = kNegInf;
-        m_thr[gi] = kNegInf;
-        m_neg[gi] = 0.0f;
-        l_run[gi] = 0.0f;
 #pragma unroll
-        for (int n = 0; n < NT; ++n) acc[gi][n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    }
+        for (int k = C::RPW / 2; k < C::RPW; ++k)
+        {
+            auto* p = (FFKV_LDS u32x4*)(stage + run_dst[k] + 16 * lane);
+            const u32x4 w = *p;
+            u32x4       o;
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+            {
+                const float lo = __builtin_bit_cast(float, w[e] << 16);
+                const float hi = __builtin_bit_cast(float, w[e] & 0xffff0000u);
+                o[e] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, h2));
+            }
+            *p = o;
+        }
+    };
+
     // The scores' products are issued before the next loads' scalar address work, which then runs while they
     // execute.
-    auto body = [&](int si, uint8_t* cur, int okm_cur, uint8_t* nxt, int& okm_nxt)
+    auto body = [&]<bool VC>(int si, uint8_t* cur, int okm_cur, uint8_t* nxt, int& okm_nxt)
     {
         wait_vm<(NS - 2) * LPS>();
+        if constexpr (VC)
+        {
+            convert_v(cur);
+            wait_lgkm0();  // the converted runs are written before the barrier publishes them
+        }
         __builtin_amdgcn_s_barrier();  // step si visible to all; every wave is past step si - 1 (stage of si+NS-1)
         f32x4 sx[RG][KP];
         if (wave_active) qk(cur, sx);
@@ -929,43 +969,77 @@ void paged_prefill_dma(PrefillArgs a)
         if (wave_active)
         {
             float pv[RG][KP * 4];
-            softmax(si, cur, okm_cur, sx, pv);
-            pv_mma.template operator()<V16>(cur, pv);
+            softmax.template operator()<VC>(si, cur, okm_cur, sx, pv);
+            pv_mma.template operator()<V16 || VC>(cur, pv);
         }
     };
 
-    int okm0 = issue(0, s_st0);
-    int okm1 = 0, okm2 = 0, okm3 = 0;
-    if constexpr (NS >= 3) okm1 = issue(1, s_st1);
-    if constexpr (NS == 4) okm2 = issue(2, s_st2);
-    for (int si = 0; si < steps; si += NS)
+    auto pipeline = [&]<bool VC>()
     {
-        if constexpr (NS == 2)
+#pragma unroll
+        for (int gi = 0; gi < RG; ++gi)
         {
-            body(si, s_st0, okm0, s_st1, okm1);
-            if (si + 1 >= steps) break;
-            body(si + 1, s_st1, okm1, s_st0, okm0);
+            m_run[gi] = kNegInf;
+            m_thr[gi] = kNegInf;
+            m_neg[gi] = 0.0f;
+            l_run[gi] = 0.0f;
+#pragma unroll
+            for (int n = 0; n < NT; ++n) acc[gi][n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
         }
-        else if constexpr (NS == 3)
+        int okm0 = issue(0, s_st0);
+        int okm1 = 0, okm2 = 0, okm3 = 0;
+        if constexpr (NS >= 3) okm1 = issue(1, s_st1);
+        if constexpr (NS == 4) okm2 = issue(2, s_st2);
+        for (int si = 0; si < steps; si += NS)
         {
-            body(si, s_st0, okm0, s_st2, okm2);
-            if (si + 1 >= steps) break;
-            body(si + 1, s_st1, okm1, s_st0, okm0);
-            if (si + 2 >= steps) break;
-            body(si + 2, s_st2, okm2, s_st1, okm1);
+            if constexpr (NS == 2)
+            {
+                body.template operator()<VC>(si, s_st0, okm0, s_st1, okm1);
+                if (si + 1 >= steps) break;
+                body.template operator()<VC>(si + 1, s_st1, okm1, s_st0, okm0);
+            }
+            else if constexpr (NS == 3)
+            {
+                body.template operator()<VC>(si, s_st0, okm0, s_st2, okm2);
+                if (si + 1 >= steps) break;
+                body.template operator()<VC>(si + 1, s_st1, okm1, s_st0, okm0);
+                if (si + 2 >= steps) break;
+                body.template operator()<VC>(si + 2, s_st2, okm2, s_st1, okm1);
+            }
+            else
+            {
+                body.template operator()<VC>(si, s_st0, okm0, s_st3, okm3);
+                if (si + 1 >= steps) break;
+                body.template operator()<VC>(si + 1, s_st1, okm1, s_st0, okm0);
+                if (si + 2 >= steps) break;
+                body.template operator()<VC>(si + 2, s_st2, okm2, s_st1, okm1);
+                if (si + 3 >= steps) break;
+                body.template operator()<VC>(si + 3, s_st3, okm3, s_st2, okm2);
+            }
         }
-        else
-        {
-            body(si, s_st0, okm0, s_st3, okm3);
-            if (si + 1 >= steps) break;
-            body(si + 1, s_st1, okm1, s_st0, okm0);
-            if (si + 2 >= steps) break;
-            body(si + 2, s_st2, okm2, s_st1, okm1);
-            if (si + 3 >= steps) break;
-            body(si + 3, s_st3, okm3, s_st2, okm2);
-        }
+        wait_vm<0>();  // no load may still be writing this workgroup's LDS when it ends
+    };
+
+    if constexpr (VCONV)
+    {
+        pipeline.template operator()<true>();
+        float t = 0.0f;  // 0 if every accumulator is finite, else NaN
+#pragma unroll
+        for (int gi = 0; gi < RG; ++gi)
+#pragma unroll
+            for (int n = 0; n < NT; ++n)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) t = __builtin_fmaf(acc[gi][n][i], 0.0f, t);
+        if (__any(!(t == 0.0f))) s_vover = 1;
+        wait_lgkm0();
+        __builtin_amdgcn_s_barrier();  // flags written; every wave is past its last reads of the stages
+        if (s_vover != 0)              // uniform: some V value of the workgroup's keys does not fit f16
+            pipeline.template operator()<false>();
     }
-    wait_vm<0>();  // no load may still be writing this workgroup's LDS when it ends
+    else
+    {
+        pipeline.template operator()<false>();
+    }
 
 #pragma unroll
     for (int gi = 0; gi < RG; ++gi)

@@ -230,12 +230,27 @@ def test_prefill_int8_large_q(ff, gpu, D):
     _check(*_run(ff, gpu, c, qn, scale=2.0 ** -17 / math.sqrt(D)), c.act, 2e-2)
 
 
-@pytest.mark.parametrize("big", [7.0e4, 3.0e5, float("inf")])
+@pytest.mark.parametrize("D", [64, 128, 256])
+def test_prefill_bf16_small_v(ff, gpu, D):
+    """V values of order 2^-16, below f16's normal range: where the PV products take V in f16, each value rounds
+    to an f16 subnormal (an absolute error of at most 2^-25), so the outputs stay within 2^-23 of the float64
+    closed form beyond their own rounding (values flushed to zero would miss by about 2^-18)."""
+    c, qn = _case(160 + D, 3, 16, 4, D, [17, 300, 5], 37)
+    s = np.float32(2.0 ** -16)
+    c.v_pool = cases.encode(cases.decode(c.v_pool, c.kv) * s, c.kv)
+    c.v_new = cases.encode(cases.decode(c.v_new, c.act) * s, c.act)
+    got, ref = _run(ff, gpu, c, qn)
+    assert float(np.abs(ref).max()) > 2.0 ** -19
+    _check(got, ref, c.act, 2.0 ** -23)
+
+
+@pytest.mark.parametrize("big", [6.0e4, 7.0e4, 3.0e5, float("inf")])
 def test_prefill_bf16_large_v(ff, gpu, big):
-    """V values far beyond the N(0,1) data (and beyond f16's range, so no product may pass through f16): row 1,
-    kv head 3 gets them in its cached pages and in its chunk.  Its outputs must match the float64 closed form
-    relative to the row's largest |v| (infinite V: the same non-finite outputs as the closed form), and rows 0
-    and 2 keep the ordinary bar."""
+    """V values far beyond the N(0,1) data: row 1, kv head 3 gets them in its cached pages and in its chunk.
+    6e4 still fits f16 (the PV products may take V in f16); the others do not, and the workgroups that meet them
+    must fall back to products that keep V in bf16.  Row 1's outputs must match the float64 closed form relative
+    to its largest |v| (infinite V: the same non-finite outputs as the closed form), and rows 0 and 2 keep the
+    ordinary bar."""
     c, qn = _case(150, 3, 32, 8, 128, [17, 300, 5], 37)
     rng = np.random.default_rng(151)
     vals = np.array([big, -big, big / 3], np.float32)
