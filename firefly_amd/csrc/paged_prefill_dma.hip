@@ -77,6 +77,9 @@ constexpr int kXcds = 8;  // MI355X: workgroups are dealt to 8 XCDs (separate L2
 #ifndef FFKV_PREFILL_VCONV
 #define FFKV_PREFILL_VCONV 1  // bf16 pages: V tiles converted to f16 in LDS by the waves that load them
 #endif
+#ifndef FFKV_PREFILL_C16
+#define FFKV_PREFILL_C16 1  // int8 pages at head_dim <= 128: tiles converted to f16 in LDS by the waves that load them
+#endif
 #ifndef FFKV_PREFILL_I8_BF
 #define FFKV_PREFILL_I8_BF 0  // int8 with bf16 q: bf16 score products (1) or f16 ones with q converted whole (0)
 #endif
@@ -253,7 +256,16 @@ void paged_prefill_dma(PrefillArgs a)
     // scaled by a power of two when the wave's largest |q| would not fit f16's range, so it needs no lo part, and
     // the codes convert to f16 with the one-instruction bias trick instead of through fp32.
     constexpr bool QX16 = CT == I8 && QT == BF16 && !BF;
-    using C = DmaCfg<D, EB, CT == I8, W, PFX>;  // the scale bytes (and their loads, counted in the waits) only for int8
+    // int8 pages with f16 score products at head_dim <= 128 (C16): the loads land the codes in LDS and each wave
+    // converts the runs it loaded to f16, into the 16-bit tile layout, before the step's barrier; the products then
+    // read f16 tiles as for an f16 cache, where otherwise every wave converts every K and V operand it reads (the
+    // whole tile).  The 16-bit tiles take twice the LDS, which head_dim 256 cannot spare.
+    constexpr bool C16 = FFKV_PREFILL_C16 && CT == I8 && !BF && D <= 128;
+    constexpr bool R8 = Q8 && !C16;  // tiles read from LDS as 8-bit codes
+    // LC: the load runs over the pages' bytes; C: the LDS tiles (16-bit for C16).  The scale bytes (and their
+    // loads, counted in the waits) only for int8.
+    using LC = DmaCfg<D, EB, CT == I8, W, PFX>;
+    using C = DmaCfg<D, C16 ? 2 : EB, CT == I8, W, PFX>;
     using M = MType<BF>;
     using X8 = typename M::x8;
     constexpr int  KP = C::KP;
@@ -495,16 +507,16 @@ void paged_prefill_dma(PrefillArgs a)
     // (bf16 pages, whose V tiles are converted to f16 in LDS (VCONV): wave w fetches runs w*RPW/2 ..
     // w*RPW/2 + RPW/2 - 1 of the K tile and the same runs of the V tile, so that every wave converts the same share)
     constexpr bool VCONV = FFKV_PREFILL_VCONV && CT == BF16;
-    static_assert(!VCONV || C::RPW % 2 == 0, "a wave loads as many V runs as K runs");
-    constexpr int RPP = VCONV ? (C::RPW / 2 < C::CHUNKS / 64 ? C::RPW / 2 : C::CHUNKS / 64) : C::RPP;  // runs per page
-    constexpr int NPW = C::RPW / RPP;  // pages (or parts of one) a wave loads per step
-    static_assert(C::RPW % RPP == 0 && (!VCONV || (C::RPW / 2) % RPP == 0), "a wave's runs cover whole page parts");
-    auto run_is_v = [&](int k) { return VCONV ? k >= C::RPW / 2 : wave * C::RPW + k >= C::IPR; };
+    static_assert(!VCONV || LC::RPW % 2 == 0, "a wave loads as many V runs as K runs");
+    constexpr int RPP = VCONV ? (LC::RPW / 2 < LC::CHUNKS / 64 ? LC::RPW / 2 : LC::CHUNKS / 64) : LC::RPP;  // runs per page
+    constexpr int NPW = LC::RPW / RPP;  // pages (or parts of one) a wave loads per step
+    static_assert(LC::RPW % RPP == 0 && (!VCONV || (LC::RPW / 2) % RPP == 0), "a wave's runs cover whole page parts");
+    auto run_is_v = [&](int k) { return VCONV ? k >= LC::RPW / 2 : wave * LC::RPW + k >= LC::IPR; };
     auto run_lr = [&](int k)
     {
-        if constexpr (VCONV) return wave * (C::RPW / 2) + (k >= C::RPW / 2 ? k - C::RPW / 2 : k);
-        const int run = wave * C::RPW + k;
-        return run >= C::IPR ? run - C::IPR : run;
+        if constexpr (VCONV) return wave * (LC::RPW / 2) + (k >= LC::RPW / 2 ? k - LC::RPW / 2 : k);
+        const int run = wave * LC::RPW + k;
+        return run >= LC::IPR ? run - LC::IPR : run;
     };
     const FFKV_CONST int32_t* table_row =  // prefix: row 0's table, whose first pfx_blocks entries every row shares
         a.paged ? (const FFKV_CONST int32_t*)(a.block_table + static_cast<int64_t>(b) * a.max_blocks) : nullptr;
@@ -512,43 +524,60 @@ void paged_prefill_dma(PrefillArgs a)
     // Wave w loads runs w*RPW .. w*RPW + RPW - 1 of the step (runs 0 .. IPR - 1 are K, the rest V).  Per-lane part
     // of each load's source, the same for every page: key row `tok` of the page, chunk `ch` (swizzled to where
     // this lane's 16 bytes land), as a byte offset from the page's (row, kv head) base.
-    uint32_t voff[C::RPW];
-    int      vtok[C::RPW];
+    uint32_t voff[LC::RPW];
+    int      vtok[LC::RPW];
 #pragma unroll
-    for (int k = 0; k < C::RPW; ++k)
+    for (int k = 0; k < LC::RPW; ++k)
     {
         const bool is_v = run_is_v(k);                     // uniform
         const int  lr = run_lr(k);                          // run within its tile
-        const int  u = lr * 64 / C::CHUNKS;                 // page of the step
-        const int  p = lr * 64 % C::CHUNKS + lane;          // chunk position within the page
-        const int  tok = p / C::CPT;
+        const int  u = lr * 64 / LC::CHUNKS;                 // page of the step
+        const int  p = lr * 64 % LC::CHUNKS + lane;          // chunk position within the page
+        const int  tok = p / LC::CPT;
         int        sw;
-        if constexpr (Q8)
+        if constexpr (C16)
+            sw = 0;  // landed in order: the conversion puts the chunks in place
+        else if constexpr (Q8)
             sw = is_v ? v8_swizzle<D>(tok, u) : k8_swizzle<D>(tok);
         else
             sw = is_v ? v_swizzle<D>(tok) : k_swizzle(tok);
-        const int ch = (p % C::CPT) ^ sw;
+        const int ch = (p % LC::CPT) ^ sw;
         vtok[k] = tok;
-        voff[k] = static_cast<uint32_t>(tok * Hkv * C::RB + 16 * ch);
+        voff[k] = static_cast<uint32_t>(tok * Hkv * LC::RB + 16 * ch);
     }
-    const size_t row_bytes = static_cast<size_t>(Hkv) * C::RB;  // one key row of all kv heads
+    const size_t row_bytes = static_cast<size_t>(Hkv) * LC::RB;  // one key row of all kv heads
 
     // A wave's runs j*RPP .. j*RPP + RPP - 1 lie in one page of one tile (per-page issue).
     // Per-run constants of this wave's loads (uniform): source tensor at kv head kvh, page of the step, LDS
     // destination.  A page's byte offset is row_base + index * page_bytes, with index the physical page (paged) or
     // the page of the row (contiguous keys).
-    const char* run_src[C::RPW];
-    int         run_u[C::RPW];
-    int         run_dst[C::RPW];
+    const char* run_src[LC::RPW];
+    int         run_u[LC::RPW];
+    int         run_dst[LC::RPW];
 #pragma unroll
-    for (int k = 0; k < C::RPW; ++k)
+    for (int k = 0; k < LC::RPW; ++k)
     {
         const bool is_v = run_is_v(k);
         const int  lr = run_lr(k);
-        run_u[k] = lr * 64 / C::CHUNKS;
-        run_src[k] = static_cast<const char*>(is_v ? a.v_cache : a.k_cache) + static_cast<size_t>(kvh) * C::RB;
-        run_dst[k] = (is_v ? C::TILEB : 0) + lr * 64 * 16;
+        run_u[k] = lr * 64 / LC::CHUNKS;
+        run_src[k] = static_cast<const char*>(is_v ? a.v_cache : a.k_cache) + static_cast<size_t>(kvh) * LC::RB;
+        // C16: run lr's codes land in the upper half of the 2 KiB its rows take in the 16-bit tile
+        run_dst[k] = (is_v ? C::TILEB : 0) + (C16 ? lr * 2048 + 1024 : lr * 64 * 16);
     }
+    // C16: where this lane's 16 codes go once converted (the 16-bit chunks 2ch and 2ch + 1 of its key row, at
+    // their swizzled places), relative to run_dst[k]
+    int c16_dst[C16 ? LC::RPW : 1][2];
+    if constexpr (C16)
+#pragma unroll
+        for (int k = 0; k < LC::RPW; ++k)
+        {
+            const int p = run_lr(k) * 64 % LC::CHUNKS + lane;
+            const int tok = p / LC::CPT;
+            const int ch = p % LC::CPT;
+            const int sw = run_is_v(k) ? v_swizzle<D>(tok) : k_swizzle(tok);
+#pragma unroll
+            for (int h = 0; h < 2; ++h) c16_dst[k][h] = 32 * (lane - ch) - 1024 + 16 * ((2 * ch + h) ^ sw);
+        }
     const uint32_t page_bytes = static_cast<uint32_t>(kBlockSize * row_bytes);
     const uint64_t row_base = a.paged ? 0 : static_cast<uint64_t>(b) * S * row_bytes;
 
@@ -625,7 +654,7 @@ void paged_prefill_dma(PrefillArgs a)
         else
         {
 #pragma unroll
-            for (int k = 0; k < C::RPW; ++k)
+            for (int k = 0; k < LC::RPW; ++k)
             {
                 const int u = run_u[k];
                 uint64_t  poff = page_off[0];  // page_off[u] without a dynamic index (u is uniform but not constant)
@@ -724,7 +753,7 @@ void paged_prefill_dma(PrefillArgs a)
             for (int u = 0; u < KP; ++u) s[gi][u] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
         auto kread = [&](int j, int u) -> X8
         {
-            if constexpr (Q8)
+            if constexpr (R8)
             {
                 const int   ka = u * kBlockSize * C::RB + k8base + (((2 * j + (g >> 1)) ^ k8sw) << 4);
                 const u32x2 w = *reinterpret_cast<const u32x2*>(stage + ka);
@@ -737,7 +766,7 @@ void paged_prefill_dma(PrefillArgs a)
             }
         };
         // every K operand read from LDS feeds the products of all RG row groups
-        mfma_priority<Q8>(1);
+        mfma_priority<R8>(1);
         X8 kc[KP];
 #pragma unroll
         for (int u = 0; u < KP; ++u) kc[u] = kread(0, u);
@@ -758,7 +787,7 @@ void paged_prefill_dma(PrefillArgs a)
 #pragma unroll
             for (int u = 0; u < KP; ++u) kc[u] = kn[u];
         }
-        mfma_priority<Q8>(0);
+        mfma_priority<R8>(0);
         if constexpr (CT == I8)  // per-token K scales of keys 4g .. 4g + 3 of each page
         {
 #pragma unroll
@@ -850,7 +879,7 @@ void paged_prefill_dma(PrefillArgs a)
         using XP = typename MP::x8;
         auto vread = [&](int n, int u0) -> XP  // V^T operand of output tile n over pages u0, u0 + 1
         {
-            if constexpr (Q8)
+            if constexpr (R8)
             {
                 const auto raw = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
                     (FFKV_LDS i32x2*)(stage + u0 * kBlockSize * C::RB + v8base + ((n ^ v8sw) << 4)));
@@ -902,7 +931,7 @@ void paged_prefill_dma(PrefillArgs a)
                 plo[gi] = __builtin_bit_cast(XP, u32x4{pl[0], pl[1], pl[2], pl[3]});
             }
             // every V^T operand read from LDS feeds the products of all RG row groups
-            mfma_priority<Q8>(1);
+            mfma_priority<R8>(1);
             XP vcur = vread(0, u0);
 #pragma unroll
             for (int n = 0; n < NT; ++n)
@@ -917,7 +946,7 @@ void paged_prefill_dma(PrefillArgs a)
                 }
                 vcur = vnxt;
             }
-            mfma_priority<Q8>(0);
+            mfma_priority<R8>(0);
         }
     };
 
@@ -925,7 +954,7 @@ void paged_prefill_dma(PrefillArgs a)
     // Every step issues the same number of loads (steps past the end fetch the zero block into a stage nobody
     // reads), so "step si has landed" is always vmcnt <= the loads of steps si + 1 .. si + NS - 2.
     constexpr int NS = kDmaStages<D>;
-    constexpr int LPS = C::RPW + C::SCB / 256;  // loads per wave and step
+    constexpr int LPS = LC::RPW + C::SCB / 256;  // loads per wave and step
 
     // bf16 pages (VCONV): every wave converts the V runs it loads to f16 in place, in LDS, as soon as its own loads
     // of them have landed and before the barrier that publishes the step; the PV products then take f16 V^T and P
@@ -936,7 +965,7 @@ void paged_prefill_dma(PrefillArgs a)
     auto convert_v = [&](uint8_t* stage)
     {
 #pragma unroll
-        for (int k = C::RPW / 2; k < C::RPW; ++k)
+        for (int k = LC::RPW / 2; k < LC::RPW; ++k)
         {
             auto* p = (FFKV_LDS u32x4*)(stage + run_dst[k] + 16 * lane);
             const u32x4 w = *p;
@@ -952,6 +981,23 @@ void paged_prefill_dma(PrefillArgs a)
         }
     };
 
+    // int8 pages (C16): every wave converts the runs it loads (K and V) to f16 in the 16-bit tile layout, as soon
+    // as its own loads of them have landed and before the barrier that publishes the step.  A run's codes sit in
+    // the upper half of the region its f16 values fill, which no other run touches; the whole run is read before
+    // any of it is written.
+    auto convert_c16 = [&](uint8_t* stage)
+    {
+#pragma unroll
+        for (int k = 0; k < (C16 ? LC::RPW : 0); ++k)
+        {
+            const u32x4 w = *(FFKV_LDS u32x4*)(stage + run_dst[k] + 16 * lane);
+            const u32x4 lo = codes_to_m<CT, false>(w[0], w[1]);
+            const u32x4 hi = codes_to_m<CT, false>(w[2], w[3]);
+            *(FFKV_LDS u32x4*)(stage + run_dst[k] + c16_dst[k][0]) = lo;
+            *(FFKV_LDS u32x4*)(stage + run_dst[k] + c16_dst[k][1]) = hi;
+        }
+    };
+
     // The scores' products are issued before the next loads' scalar address work, which then runs while they
     // execute.
     auto body = [&]<bool VC>(int si, uint8_t* cur, int okm_cur, uint8_t* nxt, int& okm_nxt)
@@ -961,6 +1007,11 @@ void paged_prefill_dma(PrefillArgs a)
         {
             convert_v(cur);
             wait_lgkm0();  // the converted runs are written before the barrier publishes them
+        }
+        if constexpr (C16)
+        {
+            convert_c16(cur);
+            wait_lgkm0();
         }
         __builtin_amdgcn_s_barrier();  // step si visible to all; every wave is past step si - 1 (stage of si+NS-1)
         f32x4 sx[RG][KP];
