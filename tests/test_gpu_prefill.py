@@ -244,6 +244,27 @@ def test_prefill_bf16_small_v(ff, gpu, D):
     _check(got, ref, c.act, 2.0 ** -23)
 
 
+@pytest.mark.parametrize("D", [64, 128, 256])
+def test_prefill_int8_large_v(ff, gpu, D):
+    """int8 pages whose dequantized V reaches 3e4 (per-token scales of 3e4 / 127): P carries the keys' V scales
+    into the f16 PV products, p < 2^8, so p times a scale stays within f16's range up to |V| of about 32,500, the
+    documented limit.  Row 1, kv head 3 gets such tokens in its cached pages and in its chunk; its outputs match
+    the float64 closed form relative to the largest |v|, and rows 0 and 2 keep the quantized bar."""
+    big = 3.0e4
+    c, qn = _case(190 + D, 3, 16, 4, D, [17, 300, 5], 37, kv="i8")
+    rng = np.random.default_rng(191)
+    for t in rng.choice(300, size=6, replace=False):
+        page, slot = c.block_table[1, t // 16], t % 16
+        c.v_scale[page, slot, 3] = np.float32(big / 127.0)
+    c.v_new[1, 5, 3, 7] = cases.encode(np.array([big], np.float32), c.act)[0]
+    got, ref = _run(ff, gpu, c, qn)
+    for b in (0, 2):
+        _check(got[b:b + 1], ref[b:b + 1], c.act, 2e-2)
+    err = float(np.abs(got[1].astype(np.float64) - ref[1]).max())
+    print(f"  row 1 max-abs err {err:.3e} against |v| up to {big:.1e}", flush=True)
+    assert np.isfinite(got[1]).all() and err <= 2e-2 * big
+
+
 @pytest.mark.parametrize("big", [6.0e4, 7.0e4, 3.0e5, float("inf")])
 def test_prefill_bf16_large_v(ff, gpu, big):
     """V values far beyond the N(0,1) data: row 1, kv head 3 gets them in its cached pages and in its chunk.
