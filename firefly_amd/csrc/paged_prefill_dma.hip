@@ -1,5 +1,5 @@
 // paged_prefill_dma.hip - chunked / paged prefill attention on gfx950, with the K/V pages streamed into LDS by
-// asynchronous global->LDS loads (16-bit caches, and 8-bit int8 / fp8 e4m3 codes converted at operand-read time).
+// asynchronous global->LDS loads (16-bit caches, and 8-bit int8 / fp8 e4m3 codes).
 //
 // Replaces the reference's prefill branch of kernels::attention (flash_attn_wmma_kernel,
 // src/kernels/attention.cu:22-286, dispatched at :460-474 and routed from src/model/qwen_model.cu:147-151), which
@@ -17,7 +17,7 @@
 //
 // Pages reach LDS without passing through registers: every 16-byte chunk of a step's K and V pages goes from HBM
 // straight into LDS with global_load_lds_dwordx4 (each lane's 16 bytes land at the instruction's LDS base +
-// 16 * lane), with no staging registers and no LDS stores by the waves.  NS stages rotate (two at head_dim 128
+// 16 * lane), with no staging registers.  NS stages rotate (two at head_dim 128
 // and 256, three at 64): step i + NS - 1 is requested as soon as every wave has finished step i - 1, so NS - 1
 // steps of loads are in flight behind the step being computed, with one barrier per step.  Each stage is its own LDS object and the main loop is unrolled by NS, so the compiler can tell
 // which stage a load writes and does not hold the compute of one stage behind the loads into another.
@@ -42,6 +42,11 @@
 // types, and f16's 11 bits hold P in one product where bf16 P needs a hi + lo pair (C4-shaped prefill: fp8 300 ->
 // 240 us, int8 356 -> 333 us).  int8 per-token scales (fp32 [N, 16, Hkv]) travel with their page into the stage
 // by 4-byte loads; fp8 per-head scales fold into the score scale and the output.
+//
+// Two kinds of pages are converted in LDS instead, each wave converting the runs it loaded, in place, after its
+// own wait for them and before the barrier that publishes the step (no barrier of its own): bf16 pages' V tiles
+// to f16, so that their PV products take f16 P in one product (a V value beyond f16's range reruns the
+// workgroup on bf16 products), and int8 pages at head_dim <= 128 to 16-bit f16 tiles read as an f16 cache's.
 //
 // Keys past the row's end and keys on invalid pages are fetched from a zero block instead, so masked keys meet
 // zero V rows (their probabilities are exactly zero) and no lane reads outside the cache.
