@@ -69,6 +69,30 @@ def test_shared_prefix_bf16(ff, gpu, shared, suffix):
     _both(ff, gpu, c, shared)
 
 
+@pytest.mark.parametrize("big", [7.0e4, float("inf")])
+def test_shared_prefix_large_v(ff, gpu, big):
+    """bf16 V values beyond f16's range in the shared pages: the prefix kernel's f16 PV products overflow, and
+    its workgroups that meet them must redo their pages with bf16 products.  Outputs match the checker relative
+    to the largest |v| (infinite V: the same non-finite outputs)."""
+    rng = np.random.default_rng(47)
+    shared, B = 16, 24
+    ctx = shared * 16 + rng.integers(1, 200, size=B) - 1
+    c = cases.make_case(47, B, 32, 8, 128, ctx, act="bf16", shared_prefix_blocks=shared)
+    enc = cases.encode(np.array([big, -big], np.float32), O.DTYPE_BF16)
+    for t in rng.choice(shared * 16, size=5, replace=False):
+        c.v_pool[c.block_table[0, t // 16], t % 16, 3, rng.integers(0, 128)] = enc[rng.integers(0, 2)]
+    got, plain, ref = _run(ff, gpu, c, shared)
+    for g, what in ((got, "shared-prefix decode"), (plain, "plain decode")):
+        fin = np.isfinite(ref)
+        assert np.array_equal(np.isfinite(g), fin), f"{what}: non-finite outputs differ from the checker"
+        if np.isfinite(big):
+            err = float(np.abs(g.astype(np.float64) - ref).max())
+            print(f"  {what}: max-abs err {err:.3e} against |v| up to {big:.1e}", flush=True)
+            assert err <= 2e-3 * big
+        else:  # kv head 3's heads (12..15) hold the infinities; the others keep the ordinary bar
+            _check(g[:, :12], ref[:, :12], c.act, 2e-3, what)
+
+
 def test_c4_shape(ff, gpu):
     """BASELINE config 4's decode: 120 rows over one 2048-token prefix, private suffixes U[64, 1024]."""
     rng = np.random.default_rng(44)
