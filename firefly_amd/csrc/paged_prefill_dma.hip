@@ -286,12 +286,12 @@ void paged_prefill_dma(PrefillArgs a)
     // 8-bit codes are exact in f16 as in bf16: with bf16 score products (BF), their PV products still take f16
     // V^T and P^T, so P needs one product instead of a bf16 hi + lo pair.
     constexpr bool V16 = FFKV_PREFILL_V16 && Q8 && BF;
-    // f16 P (f16 caches, and the f16 PV products of fp8 caches): the denominator sums the rounded P that the
-    // products take, two values per v_dot2_f32_f16, in place of one add per p.  int8's P carries the keys' V
-    // scales, so its denominator sums p itself, as do bf16's hi + lo pairs.
+    // f16 P (f16 caches, the f16 PV products of fp8 caches, and bf16 pages' f16 V tiles, VCONV below): the
+    // denominator sums the rounded P that the products take, two values per v_dot2_f32_f16, in place of one add
+    // per p.  int8's P carries the keys' V scales, so its denominator sums p itself, as do bf16's hi + lo pairs.
     constexpr bool L_DOT = !(BF && !V16) && CT != I8;
 
-    // NS stages (three by default), each [K tile | V tile | int8 scales] of KP pages, key-major, swizzled chunks
+    // kDmaStages<D> stages, each [K tile | V tile | int8 scales] of KP pages, key-major, swizzled chunks
     __shared__ __align__(16) uint8_t s_st0[2 * C::TILEB + C::SCB];
     __shared__ __align__(16) uint8_t s_st1[2 * C::TILEB + C::SCB];
     __shared__ __align__(16) uint8_t s_st2[kDmaStages<D> >= 3 ? 2 * C::TILEB + C::SCB : 16];
