@@ -121,7 +121,9 @@ def test_prefill_long_chunk_over_long_prefix(ff, gpu):
 # both load-issue forms of the kernel: per run (bf16 q over a bf16 cache, head_dim 128) and per page (the others)
 @pytest.mark.parametrize("act,kv,D,tol", [("bf16", "bf16", 128, 2e-3), ("f16", "f16", 128, 2e-3),
                                           ("bf16", "bf16", 64, 2e-3), ("bf16", "bf16", 256, 2e-3),
-                                          ("bf16", "i8", 128, 2e-2), ("f32", "bf16", 128, 2e-3)])
+                                          ("bf16", "i8", 128, 2e-2), ("f32", "bf16", 128, 2e-3),
+                                          ("bf16", "i8", 64, 2e-2), ("f16", "i8", 128, 2e-2),
+                                          ("bf16", "i8", 256, 2e-2), ("bf16", "fp8", 64, 2e-2)])
 def test_prefill_invalid_pages_and_rows_without_keys(ff, gpu, act, kv, D, tol):
     c, qn = _case(500, 4, 8, 2, D, [40, 0, 64, 20], 9, act=act, kv=kv)
     tbl = c.block_table.copy()

@@ -129,6 +129,16 @@ def test_dtypes(ff, gpu, act, kv, tol):
     _both(ff, gpu, c, 16, tol=tol)
 
 
+@pytest.mark.parametrize("kv,D,G", [("i8", 64, 4), ("i8", 256, 2), ("fp8", 64, 4), ("bf16", 64, 4)])
+def test_quantized_head_shapes(ff, gpu, kv, D, G):
+    """The prefix kernel's other load layouts: int8 pages at head_dim 64 (codes converted to f16 tiles in LDS,
+    one run per wave) and 256 (8-bit tiles), fp8 at 64, bf16 at 64 (f16 V tiles)."""
+    rng = np.random.default_rng(49 + D + G)
+    ctx = 176 + rng.integers(0, 300, size=10)
+    c = cases.make_case(49 + D + G, 10, 2 * G, 2, D, ctx, act="bf16", kv=kv, shared_prefix_blocks=11)
+    _both(ff, gpu, c, 11, tol=2e-3 if kv == "bf16" else 2e-2)
+
+
 def test_truncated_context(ff, gpu):
     """max_context_len below some rows' lengths, and below the prefix itself."""
     rng = np.random.default_rng(48)
