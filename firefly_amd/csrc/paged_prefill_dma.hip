@@ -82,6 +82,9 @@ constexpr int kXcds = 8;  // MI355X: workgroups are dealt to 8 XCDs (separate L2
 #ifndef FFKV_PREFILL_VCONV
 #define FFKV_PREFILL_VCONV 1  // bf16 pages: V tiles converted to f16 in LDS by the waves that load them
 #endif
+#ifndef FFKV_PREFILL_AHEAD
+#define FFKV_PREFILL_AHEAD 1  // with three or more stages: tiles converted in LDS one step ahead, behind the scores
+#endif
 #ifndef FFKV_PREFILL_C16
 #define FFKV_PREFILL_C16 1  // int8 pages at head_dim <= 128: tiles converted to f16 in LDS by the waves that load them
 #endif
@@ -1005,22 +1008,38 @@ void paged_prefill_dma(PrefillArgs a)
 
     // The scores' products are issued before the next loads' scalar address work, which then runs while they
     // execute.
-    auto body = [&]<bool VC>(int si, uint8_t* cur, int okm_cur, uint8_t* nxt, int& okm_nxt)
+    // With three or more stages, step si + 1 has been requested a step before step si is computed, so its tiles
+    // are converted while step si's score products run (AH), instead of at the head of step si + 1.
+    auto body = [&]<bool VC>(int si, uint8_t* cur, int okm_cur, uint8_t* nxt, int& okm_nxt, uint8_t* ahead)
     {
+        constexpr bool AH = FFKV_PREFILL_AHEAD && NS >= 3 && (VC || C16);
         wait_vm<(NS - 2) * LPS>();
-        if constexpr (VC)
+        if constexpr (AH)
         {
-            convert_v(cur);
-            wait_lgkm0();  // the converted runs are written before the barrier publishes them
+            wait_lgkm0();  // this wave's conversion of step si (at step si - 1) is written before the barrier
         }
-        if constexpr (C16)
+        else
         {
-            convert_c16(cur);
-            wait_lgkm0();
+            if constexpr (VC)
+            {
+                convert_v(cur);
+                wait_lgkm0();  // the converted runs are written before the barrier publishes them
+            }
+            if constexpr (C16)
+            {
+                convert_c16(cur);
+                wait_lgkm0();
+            }
         }
         __builtin_amdgcn_s_barrier();  // step si visible to all; every wave is past step si - 1 (stage of si+NS-1)
         f32x4 sx[RG][KP];
         if (wave_active) qk(cur, sx);
+        if constexpr (AH)
+        {
+            wait_vm<(NS - 3) * LPS>();  // step si + 1 has landed (its stage's last readers were past step si - 1)
+            if constexpr (VC) convert_v(ahead);
+            if constexpr (C16) convert_c16(ahead);
+        }
         okm_nxt = issue(si + NS - 1, nxt);
         if (wave_active)
         {
@@ -1046,31 +1065,37 @@ void paged_prefill_dma(PrefillArgs a)
         int okm1 = 0, okm2 = 0, okm3 = 0;
         if constexpr (NS >= 3) okm1 = issue(1, s_st1);
         if constexpr (NS == 4) okm2 = issue(2, s_st2);
+        if constexpr (FFKV_PREFILL_AHEAD && NS >= 3 && (VC || C16))  // step 0's tiles, converted ahead of the loop
+        {
+            wait_vm<(NS - 2) * LPS>();
+            if constexpr (VC) convert_v(s_st0);
+            if constexpr (C16) convert_c16(s_st0);
+        }
         for (int si = 0; si < steps; si += NS)
         {
             if constexpr (NS == 2)
             {
-                body.template operator()<VC>(si, s_st0, okm0, s_st1, okm1);
+                body.template operator()<VC>(si, s_st0, okm0, s_st1, okm1, s_st1);
                 if (si + 1 >= steps) break;
-                body.template operator()<VC>(si + 1, s_st1, okm1, s_st0, okm0);
+                body.template operator()<VC>(si + 1, s_st1, okm1, s_st0, okm0, s_st0);
             }
             else if constexpr (NS == 3)
             {
-                body.template operator()<VC>(si, s_st0, okm0, s_st2, okm2);
+                body.template operator()<VC>(si, s_st0, okm0, s_st2, okm2, s_st1);
                 if (si + 1 >= steps) break;
-                body.template operator()<VC>(si + 1, s_st1, okm1, s_st0, okm0);
+                body.template operator()<VC>(si + 1, s_st1, okm1, s_st0, okm0, s_st2);
                 if (si + 2 >= steps) break;
-                body.template operator()<VC>(si + 2, s_st2, okm2, s_st1, okm1);
+                body.template operator()<VC>(si + 2, s_st2, okm2, s_st1, okm1, s_st0);
             }
             else
             {
-                body.template operator()<VC>(si, s_st0, okm0, s_st3, okm3);
+                body.template operator()<VC>(si, s_st0, okm0, s_st3, okm3, s_st1);
                 if (si + 1 >= steps) break;
-                body.template operator()<VC>(si + 1, s_st1, okm1, s_st0, okm0);
+                body.template operator()<VC>(si + 1, s_st1, okm1, s_st0, okm0, s_st2);
                 if (si + 2 >= steps) break;
-                body.template operator()<VC>(si + 2, s_st2, okm2, s_st1, okm1);
+                body.template operator()<VC>(si + 2, s_st2, okm2, s_st1, okm1, s_st3);
                 if (si + 3 >= steps) break;
-                body.template operator()<VC>(si + 3, s_st3, okm3, s_st2, okm2);
+                body.template operator()<VC>(si + 3, s_st3, okm3, s_st2, okm2, s_st0);
             }
         }
         wait_vm<0>();  // no load may still be writing this workgroup's LDS when it ends
