@@ -191,8 +191,9 @@ FFKV_API int ffkv_paged_decode_shared_prefix(const void* q, void* out, int qo_dt
  * weighs the keys uniformly, a negative one negates the scores, as in decode).  Range limit of int8 caches: the
  * attention weights meet their V scales in f16, so per-token V scales must stay below 256 (|V| below 32,512).
  * bf16 caches: V enters the products in f16 (a workgroup that meets |V| >= 65520 reruns in bf16), so V values
- * below 2^-14 carry an absolute error of at most 2^-25; an infinite V value also makes NaN, in its dim, the
- * outputs of the queries whose causal limit masks its key (it meets them with weight 0 in the tile products).
+ * below 2^-14 carry an absolute error of at most 2^-25.  Any cache type: an infinite V value also makes NaN, in
+ * its dim, the outputs of the queries whose causal limit masks its key (it meets them with weight 0 in the tile
+ * products).
  */
 FFKV_API int ffkv_paged_prefill(const void* q, void* out, int qo_dtype, const void* k_cache, const void* v_cache,
                                 int cache_dtype, const float* k_scale, const float* v_scale, const int32_t* block_table,
