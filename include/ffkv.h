@@ -191,7 +191,7 @@ FFKV_API int ffkv_paged_decode_shared_prefix(const void* q, void* out, int qo_dt
  * weighs the keys uniformly, a negative one negates the scores, as in decode).  Range limit of int8 caches: the
  * attention weights meet their V scales in f16, so per-token V scales must stay below 256 (|V| below 32,512).
  * bf16 caches: V enters the products in f16 (a workgroup that meets |V| >= 65520 reruns in bf16), so V values
- * below 2^-14 carry an absolute error of at most 2^-25.  Any cache type: an infinite V value also makes NaN, in
+ * below 2^-14 carry an absolute error of at most 2^-25.  16-bit caches: an infinite V value also makes NaN, in
  * its dim, the outputs of the queries whose causal limit masks its key (it meets them with weight 0 in the tile
  * products).
  */
