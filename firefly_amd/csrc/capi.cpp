@@ -89,7 +89,10 @@ namespace ffkv
 
 bool decode_use_mfma(int cache_dtype, int /*group*/, int head_dim)
 {
-    return !env_force_generic() && cache_dtype != FFKV_DTYPE_F32 && head_dim_mfma(head_dim);
+    // head_dim 96 on the matrix cores for 16-bit caches (three k-steps of 32 dims); 8-bit codes load two k-steps
+    // at a time, so their head_dim 96 takes the vector kernel
+    const bool b16 = cache_dtype == FFKV_DTYPE_BF16 || cache_dtype == FFKV_DTYPE_F16;
+    return !env_force_generic() && cache_dtype != FFKV_DTYPE_F32 && (head_dim_mfma(head_dim) || (head_dim == 96 && b16));
 }
 
 // MFMA workspace layout: [row meta: batch x 2 int32 | (m, l): slots x num_heads x 2 fp32 | acc: slots x num_heads
@@ -451,7 +454,9 @@ int decode_impl(const void* q, void* out, int qo_dtype, const void* k_cache, con
                     max_blocks);
     const bool mfma = ffkv::decode_use_mfma(cache_dtype, group, head_dim);
     // shared-prefix split: matrix-core decode (16- and 8-bit caches; fp32 caches take the plain decode, same results)
-    const int skip = mfma ? std::min(shared_blocks, static_cast<int>(ceil_div(cap, FFKV_BLOCK_SIZE))) : 0;
+    const int skip = mfma && head_dim_mfma(head_dim)  // the prefix partials' kernel takes 64, 128 and 256
+                         ? std::min(shared_blocks, static_cast<int>(ceil_div(cap, FFKV_BLOCK_SIZE)))
+                         : 0;
     int pfx_chunks = 0, pfx_chunk_pages = 0;
     if (skip > 0) ffkv::prefix_chunking(batch, group, num_kv_heads, skip, pfx_chunks, pfx_chunk_pages);
     const int  chunk = ffkv::decode_chunk(batch, num_kv_heads, cap);

@@ -106,6 +106,7 @@ constexpr int kMfmaDepth =
 template <int CT, int QT, int D>
 constexpr int kMfmaWaves =
     D == 256 ? 2
+    : D == 96 ? (QT == CT ? 3 : 2)  // a q of another type needs its lo part: three waves' registers would spill
              : (D == 128 ? (kElemBytes<CT> == 2 ? FFKV_MFMA_WAVES128_16
                                                 : (CT == FP8 ? FFKV_MFMA_WAVES128_FP8 : FFKV_MFMA_WAVES128_I8))
                          : (kMfmaDepth<CT, D> > 1 ? 3 : 4));
@@ -119,7 +120,9 @@ constexpr int kMfmaWaves =
 template <int D>
 __device__ __forceinline__ int vt_pos(int t, int d)
 {
-    const int sw = D == 64 ? 2 * ((t >> 1) & 3) : 2 * (t & 7);
+    // head_dim 96 (12 chunks a row, whose 192-byte stride already spreads a read's four rows over the banks): the
+    // swizzle stays within aligned groups of four chunks, so it never leaves the row
+    const int sw = D == 64 ? 2 * ((t >> 1) & 3) : (D == 96 ? 2 * ((t >> 2) & 1) : 2 * (t & 7));
     return t * D + (((d >> 3) ^ sw) << 3) + (d & 7);
 }
 
@@ -663,7 +666,7 @@ void paged_decode_mfma(DecodeArgs a)
 template <int QT, int D, int MW>
 __global__ __launch_bounds__(64 * MW) void paged_decode_mfma_merge(DecodeArgs a)
 {
-    constexpr int PER = D / 64;  // dims per lane
+    constexpr int PER = (D + 63) / 64;  // dims per lane (head_dim 96: lanes 0 .. 47 hold two)
     const int     b = blockIdx.x;
     const int     h = blockIdx.y;
     const int     lane = threadIdx.x & 63;
@@ -706,7 +709,7 @@ __global__ __launch_bounds__(64 * MW) void paged_decode_mfma_merge(DecodeArgs a)
                 ls[f] = a.ws_ml[(slot * a.num_heads + h) * 2 + 1];
                 const float* src = a.ws_acc + (slot * a.num_heads + h) * D + lane * PER;
 #pragma unroll
-                for (int k = 0; k < PER; ++k) x[f][k] = src[k];
+                for (int k = 0; k < PER; ++k) x[f][k] = lane * PER + k < D ? src[k] : 0.0f;
             }
         }
 #pragma unroll
@@ -728,7 +731,8 @@ __global__ __launch_bounds__(64 * MW) void paged_decode_mfma_merge(DecodeArgs a)
         s_l[wave] = l;
     }
 #pragma unroll
-    for (int k = 0; k < PER; ++k) s_o[wave][lane * PER + k] = o[k];
+    for (int k = 0; k < PER; ++k)
+        if (lane * PER + k < D) s_o[wave][lane * PER + k] = o[k];
     __syncthreads();
     if (threadIdx.x < D)
     {
@@ -865,6 +869,9 @@ int items_m2(const DecodeArgs& a)
     {
         case 64:
             return items_m3<CT, QT, 64>(a);
+        case 96:  // 16-bit caches only (8-bit codes load two k-steps at once)
+            if constexpr (kElemBytes<CT> == 2) return items_m3<CT, QT, 96>(a);
+            return 1;
         case 128:
             return items_m3<CT, QT, 128>(a);
         default:
@@ -893,6 +900,9 @@ hipError_t launch_m2(const DecodeArgs& a, hipStream_t stream)
     {
         case 64:
             return launch_m3<CT, QT, 64>(a, stream);
+        case 96:  // 16-bit caches only (8-bit codes load two k-steps at once)
+            if constexpr (kElemBytes<CT> == 2) return launch_m3<CT, QT, 96>(a, stream);
+            return hipErrorInvalidValue;
         case 128:
             return launch_m3<CT, QT, 128>(a, stream);
         default:

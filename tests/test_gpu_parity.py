@@ -69,11 +69,12 @@ def test_head_shapes(ff, gpu, D, G):
 
 
 @pytest.mark.parametrize("D,act,kv", [(128, "bf16", "bf16"), (96, "bf16", "bf16"), (128, "f32", "f32"),
-                                      (128, "bf16", "i8"), (40, "f16", "f16")])
+                                      (128, "bf16", "i8"), (40, "f16", "f16"), (112, "bf16", "bf16")])
 def test_peaked_softmax(ff, gpu, D, act, kv):
     """Inputs at 3x the usual scale: scores spread over tens of log2 units, so the running maximum jumps often and
     far, and the lazily rescaled softmax state (rescaled only when a score passes the reference by 2^8) is
-    rescaled many times per row, on the matrix-core kernel (D 128) and the vector kernel (D 96 / 40, fp32 pages)."""
+    rescaled many times per row, on the matrix-core kernel (D 128 and 96) and the vector kernel (D 112 / 40,
+    fp32 pages)."""
     rng = np.random.default_rng(300 + D + len(act) + len(kv))
     ctx = rng.integers(0, 2500, size=6)
     c = cases.make_case(3000 + D, 6, 16, 4, D, ctx, act=act, kv=kv, input_scale=3.0)
