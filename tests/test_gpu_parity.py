@@ -125,7 +125,8 @@ def test_head_dim_96_multi_token_append(ff, gpu, kv):
 
 @pytest.mark.parametrize("G,Hkv,D,act,kv", [(17, 2, 128, "bf16", "bf16"), (32, 1, 128, "bf16", "bf16"),
                                              (48, 2, 128, "f16", "f16"), (24, 2, 64, "bf16", "fp8"),
-                                             (32, 2, 128, "bf16", "i8"), (20, 1, 256, "f32", "bf16")])
+                                             (32, 2, 128, "bf16", "i8"), (20, 1, 256, "f32", "bf16"),
+                                             (20, 2, 96, "bf16", "bf16"), (40, 1, 96, "f16", "f16")])
 def test_groups_over_16(ff, gpu, G, Hkv, D, act, kv):
     """GQA groups above 16 query heads per KV head (MQA-style): one wave per block of 16 heads of the group."""
     rng = np.random.default_rng(G * 10 + Hkv)
