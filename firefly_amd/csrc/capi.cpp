@@ -89,10 +89,8 @@ namespace ffkv
 
 bool decode_use_mfma(int cache_dtype, int /*group*/, int head_dim)
 {
-    // head_dim 96 on the matrix cores for 16-bit caches (three k-steps of 32 dims); 8-bit codes load two k-steps
-    // at a time, so their head_dim 96 takes the vector kernel
-    const bool b16 = cache_dtype == FFKV_DTYPE_BF16 || cache_dtype == FFKV_DTYPE_F16;
-    return !env_force_generic() && cache_dtype != FFKV_DTYPE_F32 && (head_dim_mfma(head_dim) || (head_dim == 96 && b16));
+    // head_dim 96 on the matrix cores too (three k-steps of 32 dims)
+    return !env_force_generic() && cache_dtype != FFKV_DTYPE_F32 && (head_dim_mfma(head_dim) || head_dim == 96);
 }
 
 // MFMA workspace layout: [row meta: batch x 2 int32 | (m, l): slots x num_heads x 2 fp32 | acc: slots x num_heads

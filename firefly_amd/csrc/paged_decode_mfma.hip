@@ -145,7 +145,15 @@ void paged_decode_mfma(DecodeArgs a)
     constexpr bool NEED_LO = !((QT == BF16 && BF) || (QT == F16 && !BF));
     constexpr bool P_LO = VBF;  // bf16 P: hi + lo parts
     constexpr int  DEPTH = kMfmaDepth<CT, D>;
-    constexpr int  NW = kElemBytes<CT> == 2 ? KSTEPS : KSTEPS / 2;
+    constexpr int  NW = kElemBytes<CT> == 2 ? KSTEPS : (KSTEPS + 1) / 2;
+    // First dim of k-step j's 8 values in lane group g.  8-bit codes pair k-steps in one 16-byte read; an odd last
+    // k-step (head_dim 96) reads its 8 codes alone, at dims 32j + 8g.
+    auto dimof = [](int j, int g)
+    {
+        if constexpr (kElemBytes<CT> == 1 && KSTEPS % 2 == 1)
+            if (j == KSTEPS - 1) return 32 * j + 8 * g;
+        return dim_of<CT>(j, g);
+    };
 
     __shared__ uint16_t s_v[FFKV_MFMA_MAX_WAVES][kBlockSize * D];
 
@@ -373,8 +381,18 @@ void paged_decode_mfma(DecodeArgs a)
 #pragma unroll
             for (int j = 0; j < KSTEPS; j += 2)
             {
-                r.k[j / 2] = *reinterpret_cast<const u32x4*>(kp + dim_of<CT>(j, g));
-                r.v[j / 2] = *reinterpret_cast<const u32x4*>(vp + dim_of<CT>(j, g));
+                if (j + 1 < KSTEPS)
+                {
+                    r.k[j / 2] = *reinterpret_cast<const u32x4*>(kp + dimof(j, g));
+                    r.v[j / 2] = *reinterpret_cast<const u32x4*>(vp + dimof(j, g));
+                }
+                else  // an odd last k-step: its 8 codes alone
+                {
+                    const u32x2 tk = *reinterpret_cast<const u32x2*>(kp + dimof(j, g));
+                    const u32x2 tv = *reinterpret_cast<const u32x2*>(vp + dimof(j, g));
+                    r.k[j / 2] = u32x4{tk[0], tk[1], 0u, 0u};
+                    r.v[j / 2] = u32x4{tv[0], tv[1], 0u, 0u};
+                }
             }
         }
     };
@@ -392,7 +410,7 @@ void paged_decode_mfma(DecodeArgs a)
                 if (c < gc)
                     w = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.q) +
                                                         (static_cast<size_t>(b) * a.num_heads + kvh * G + h0 + c) * D +
-                                                        dim_of<CT>(j, g));
+                                                        dimof(j, g));
                 qhi[j] = __builtin_bit_cast(X8, w);
                 qlo[j] = qhi[j];
             }
@@ -400,7 +418,7 @@ void paged_decode_mfma(DecodeArgs a)
             {
                 float x[8];
                 if (c < gc)
-                    load_q8<QT>(a.q, (static_cast<size_t>(b) * a.num_heads + kvh * G + h0 + c) * D + dim_of<CT>(j, g),
+                    load_q8<QT>(a.q, (static_cast<size_t>(b) * a.num_heads + kvh * G + h0 + c) * D + dimof(j, g),
                                 x);
                 else
 #pragma unroll
@@ -460,9 +478,9 @@ void paged_decode_mfma(DecodeArgs a)
         {
             const u32x4 w = tok_ok ? mword.template operator()<VBF>(r.v, j) : u32x4{0u, 0u, 0u, 0u};
 #if FFKV_DECODE_TRV
-            *reinterpret_cast<u32x4*>(sv + vt_pos<D>(c, dim_of<CT>(j, g))) = w;
+            *reinterpret_cast<u32x4*>(sv + vt_pos<D>(c, dimof(j, g))) = w;
 #else
-            *reinterpret_cast<u32x4*>(sv + lds_pos<D>(c, dim_of<CT>(j, g))) = w;
+            *reinterpret_cast<u32x4*>(sv + lds_pos<D>(c, dimof(j, g))) = w;
 #endif
         }
         s = f32x4{0.0f, 0.0f, 0.0f, 0.0f};  // lane (c, g) gets tokens 4g + i of head c
@@ -869,9 +887,8 @@ int items_m2(const DecodeArgs& a)
     {
         case 64:
             return items_m3<CT, QT, 64>(a);
-        case 96:  // 16-bit caches only (8-bit codes load two k-steps at once)
-            if constexpr (kElemBytes<CT> == 2) return items_m3<CT, QT, 96>(a);
-            return 1;
+        case 96:
+            return items_m3<CT, QT, 96>(a);
         case 128:
             return items_m3<CT, QT, 128>(a);
         default:
@@ -900,9 +917,8 @@ hipError_t launch_m2(const DecodeArgs& a, hipStream_t stream)
     {
         case 64:
             return launch_m3<CT, QT, 64>(a, stream);
-        case 96:  // 16-bit caches only (8-bit codes load two k-steps at once)
-            if constexpr (kElemBytes<CT> == 2) return launch_m3<CT, QT, 96>(a, stream);
-            return hipErrorInvalidValue;
+        case 96:
+            return launch_m3<CT, QT, 96>(a, stream);
         case 128:
             return launch_m3<CT, QT, 128>(a, stream);
         default:

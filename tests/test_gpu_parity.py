@@ -108,8 +108,9 @@ def test_head_dim_256_dtypes(ff, gpu, act, kv):
 def test_head_dims_multiple_of_8(ff, gpu, D, act, kv):
     """Any head_dim that is a multiple of 8 up to 128, as the reference's decode takes (one 8-element vector per
     lane of a 16-lane group, src/kernels/attention.cu:307-316) and its append (any head_dim up to 128,
-    src/model/qwen_model.cu:21-47): pages and int8 scales bit-exact, outputs within the bar.  These head dims run
-    the generic decode kernel with 16 lanes per token, those past head_dim / 8 idle."""
+    src/model/qwen_model.cu:21-47): pages and int8 scales bit-exact, outputs within the bar.  head_dim 96 runs on
+    the matrix cores (three k-steps of 32 dims; 8-bit codes read the odd last k-step's 8 codes alone), the others
+    on the vector kernel with 16 lanes per token, those past head_dim / 8 idle."""
     rng = np.random.default_rng(D * 7 + len(act) + len(kv))
     ctx = rng.integers(0, 600, size=5)
     c = cases.make_case(80 + D, 5, 16, 4, D, ctx, act=act, kv=kv, input_scale=1 / math.sqrt(D))
