@@ -43,6 +43,7 @@
 
 #include <math.h>
 #include <pthread.h>
+#include <sched.h>
 #include <stdatomic.h>
 #include <stdlib.h>
 #include <string.h>
@@ -564,9 +565,12 @@ static void* decode_worker(void* arg)
     return NULL;
 }
 
+/* Worker threads: the CPUs this process may run on (its affinity mask), at most 16 (a GPU box's host share). */
 int ffo_default_threads(void)
 {
-    long n = sysconf(_SC_NPROCESSORS_ONLN);
+    cpu_set_t set;
+    long      n = sched_getaffinity(0, sizeof(set), &set) == 0 ? CPU_COUNT(&set) : sysconf(_SC_NPROCESSORS_ONLN);
+    if (n > 16) n = 16;
     return n > 0 ? (int)n : 1;
 }
 
@@ -687,8 +691,136 @@ int ffo_paged_decode_f64(const void* q, int qo_dtype, const void* k_cache, const
  * the K/V are contiguous [batch, seq_len, Hkv, D] and ctx is 0: the causal attention of the reference's prefill
  * branch (flash_attn_wmma_kernel, src/kernels/attention.cu:22-286, key n masked when n >= seq_len or n > m at
  * :173-174, scale 1/sqrtf(D) at :458).  With seq_len = 1 it equals ffo_paged_decode_f64.  Closed form in
- * float64; out is [batch, seq_len, num_heads, head_dim].
+ * float64; out is [batch, seq_len, num_heads, head_dim].  The (row, query token) items run on worker threads;
+ * each item's arithmetic does not depend on the thread count.
  * -------------------------------------------------------------------------------------------------------- */
+
+typedef struct
+{
+    const void *q, *k_cache, *v_cache;
+    int qo_dtype, cache_dtype;
+    const float *k_scale, *v_scale;
+    const int32_t *block_table, *context_lens;
+    int batch, seq_len, num_heads, num_kv_heads, head_dim, max_blocks, num_blocks;
+    long long cap, max_keys;
+    double sc;
+    double* out;
+    atomic_int next;
+} prefill_job;
+
+enum { PREFILL_TOKENS_PER_ITEM = 32 };
+
+typedef struct
+{
+    double *kt, *kraw, *v, *s, *qd;
+    long long* pos;
+} prefill_scratch;
+
+/* One item: query tokens [t0, t1) of row b against kv head kvh, for the kv head's G query heads.  The row's keys
+ * (those on valid pages below the row's limit) are read once into float64 K^T [D][n] and V [n][D]; key k's
+ * score is the sum over d in increasing order of q[d]*K[k][d], so vectorising across keys keeps that order. */
+static void prefill_item(const prefill_job* j, int b, int kvh, int t0, int t1, prefill_scratch* w)
+{
+    const int D = j->head_dim, S = j->seq_len, H = j->num_heads, G = j->num_heads / j->num_kv_heads;
+    const int paged = j->block_table != NULL;
+    long long ctx = paged ? (long long)j->context_lens[b] : 0;
+    long long L = ctx + S;
+    if (paged && L > j->cap) L = j->cap;
+    if (L < 0) L = 0;
+    long long kmax = ctx + t1;  /* keys any query of the item may see */
+    if (kmax > L) kmax = L;
+    long long nk = 0;
+    for (long long k = 0; k < kmax; ++k)
+    {
+        long long row;
+        if (paged)
+        {
+            int phys = j->block_table[(size_t)b * (size_t)j->max_blocks + (size_t)(k / 16)];
+            if (phys < 0 || phys >= j->num_blocks) continue;
+            row = ((long long)phys * 16 + k % 16) * j->num_kv_heads + kvh;
+        }
+        else
+        {
+            row = ((long long)b * S + k) * j->num_kv_heads + kvh;
+        }
+        w->pos[nk++] = k;
+        for (int d = 0; d < D; ++d)
+        {
+            w->v[(size_t)(nk - 1) * (size_t)D + d] =
+                (double)load_cache(j->v_cache, j->cache_dtype, (size_t)row * D + d, j->v_scale, (size_t)row, kvh);
+            w->kraw[(size_t)(nk - 1) * (size_t)D + d] =
+                (double)load_cache(j->k_cache, j->cache_dtype, (size_t)row * D + d, j->k_scale, (size_t)row, kvh);
+        }
+    }
+    for (long long i = 0; i < nk; ++i)  /* K^T with row stride nk */
+        for (int d = 0; d < D; ++d) w->kt[(size_t)d * (size_t)nk + (size_t)i] = w->kraw[(size_t)i * (size_t)D + d];
+    for (int t = t0; t < t1; ++t)
+    {
+        long long kend = ctx + t + 1;  /* keys at positions < kend are visible */
+        long long m = 0;               /* visible keys: a prefix of the item's key list (positions increase) */
+        while (m < nk && w->pos[m] < kend) ++m;
+        for (int g = 0; g < G; ++g)
+        {
+            const int h = kvh * G + g;
+            double*   o = j->out + (((size_t)b * S + t) * H + (size_t)h) * (size_t)D;
+            size_t    qoff = (((size_t)b * S + t) * H + (size_t)h) * (size_t)D;
+            for (int d = 0; d < D; ++d) o[d] = 0.0;
+            if (m == 0) continue;
+            for (int d = 0; d < D; ++d) w->qd[d] = (double)load_act(j->q, j->qo_dtype, qoff + d);
+            double* s = w->s;
+            for (long long i = 0; i < m; ++i) s[i] = 0.0;
+            for (int d = 0; d < D; ++d)
+            {
+                const double  qv = w->qd[d];
+                const double* kr = w->kt + (size_t)d * (size_t)nk;
+                for (long long i = 0; i < m; ++i) s[i] += qv * kr[i];
+            }
+            double mx = -INFINITY;
+            for (long long i = 0; i < m; ++i)
+            {
+                s[i] *= j->sc;
+                if (s[i] > mx) mx = s[i];
+            }
+            double den = 0.0;
+            for (long long i = 0; i < m; ++i)
+            {
+                double p = exp(s[i] - mx);
+                den += p;
+                const double* vr = w->v + (size_t)i * (size_t)D;
+                for (int d = 0; d < D; ++d) o[d] += p * vr[d];
+            }
+            for (int d = 0; d < D; ++d) o[d] /= den;
+        }
+    }
+}
+
+static void* prefill_worker(void* arg)
+{
+    prefill_job*    j = (prefill_job*)arg;
+    size_t          nk = (size_t)(j->max_keys > 0 ? j->max_keys : 1);
+    size_t          D = (size_t)j->head_dim;
+    prefill_scratch w = {(double*)malloc(sizeof(double) * nk * D), (double*)malloc(sizeof(double) * nk * D),
+                         (double*)malloc(sizeof(double) * nk * D), (double*)malloc(sizeof(double) * nk),
+                         (double*)malloc(sizeof(double) * D), (long long*)malloc(sizeof(long long) * nk)};
+    const int chunks = (j->seq_len + PREFILL_TOKENS_PER_ITEM - 1) / PREFILL_TOKENS_PER_ITEM;
+    const int total = j->batch * j->num_kv_heads * chunks;
+    for (;;)
+    {
+        int item = atomic_fetch_add(&j->next, 1);
+        if (item >= total) break;
+        int c = item % chunks, r = item / chunks;
+        int t0 = c * PREFILL_TOKENS_PER_ITEM, t1 = t0 + PREFILL_TOKENS_PER_ITEM;
+        if (t1 > j->seq_len) t1 = j->seq_len;
+        prefill_item(j, r / j->num_kv_heads, r % j->num_kv_heads, t0, t1, &w);
+    }
+    free(w.kt);
+    free(w.kraw);
+    free(w.v);
+    free(w.s);
+    free(w.qd);
+    free(w.pos);
+    return NULL;
+}
 
 int ffo_paged_prefill_f64(const void* q, int qo_dtype, const void* k_cache, const void* v_cache, int cache_dtype,
                           const float* k_scale, const float* v_scale, const int32_t* block_table,
@@ -703,68 +835,32 @@ int ffo_paged_prefill_f64(const void* q, int qo_dtype, const void* k_cache, cons
     const int paged = block_table != NULL;
     if (!q || !k_cache || !v_cache || !out || (paged && !context_lens)) return ERR_ARG;
     if ((cache_dtype == DT_I8 || cache_dtype == DT_FP8) && (!k_scale || !v_scale)) return ERR_ARG;
-    const int    D = head_dim, S = seq_len, G = num_heads / num_kv_heads;
-    const double sc = scale > 0.0f ? (double)scale : 1.0 / sqrt((double)head_dim);
-    long long    cap = (long long)max_blocks * 16;
-    if (max_context_len > 0 && cap > max_context_len) cap = max_context_len;
 
+    prefill_job j = {q, k_cache, v_cache, qo_dtype, cache_dtype, k_scale, v_scale, block_table, context_lens,
+                     batch, seq_len, num_heads, num_kv_heads, head_dim, max_blocks, num_blocks, 0, 0,
+                     scale > 0.0f ? (double)scale : 1.0 / sqrt((double)head_dim), out, 0};
+    j.cap = (long long)max_blocks * 16;
+    if (max_context_len > 0 && j.cap > max_context_len) j.cap = max_context_len;
     for (int b = 0; b < batch; ++b)
     {
-        long long ctx = paged ? (long long)context_lens[b] : 0;
-        long long L = ctx + S;
-        if (paged && L > cap) L = cap;
-        if (L < 0) L = 0;
-        double*    s = (double*)malloc(sizeof(double) * (size_t)(L > 0 ? L : 1));
-        long long* rows = (long long*)malloc(sizeof(long long) * (size_t)(L > 0 ? L : 1));
-        for (int t = 0; t < S; ++t)
-        {
-            long long kend = ctx + t + 1;
-            if (kend > L) kend = L;
-            for (int h = 0; h < num_heads; ++h)
-            {
-                const int kvh = h / G;
-                double*   o = out + (((size_t)b * S + t) * num_heads + (size_t)h) * (size_t)D;
-                size_t    qoff = (((size_t)b * S + t) * num_heads + (size_t)h) * (size_t)D;
-                long long n = 0;
-                double    mx = -INFINITY;
-                for (long long j = 0; j < kend; ++j)
-                {
-                    long long row;
-                    if (paged)
-                    {
-                        int phys = block_table[(size_t)b * (size_t)max_blocks + (size_t)(j / 16)];
-                        if (phys < 0 || phys >= num_blocks) continue;
-                        row = ((long long)phys * 16 + j % 16) * num_kv_heads + kvh;
-                    }
-                    else
-                    {
-                        row = ((long long)b * S + j) * num_kv_heads + kvh;
-                    }
-                    double dot = 0.0;
-                    for (int d = 0; d < D; ++d)
-                        dot += (double)load_act(q, qo_dtype, qoff + d) *
-                               (double)load_cache(k_cache, cache_dtype, (size_t)row * D + d, k_scale, (size_t)row, kvh);
-                    s[n] = dot * sc;
-                    rows[n] = row;
-                    if (s[n] > mx) mx = s[n];
-                    ++n;
-                }
-                for (int d = 0; d < D; ++d) o[d] = 0.0;
-                if (n == 0) continue;
-                double den = 0.0;
-                for (long long i = 0; i < n; ++i)
-                {
-                    double p = exp(s[i] - mx);
-                    den += p;
-                    for (int d = 0; d < D; ++d)
-                        o[d] += p * (double)load_cache(v_cache, cache_dtype, (size_t)rows[i] * D + d, v_scale,
-                                                       (size_t)rows[i], kvh);
-                }
-                for (int d = 0; d < D; ++d) o[d] /= den;
-            }
-        }
-        free(s);
-        free(rows);
+        long long L = (paged ? (long long)context_lens[b] : 0) + seq_len;
+        if (paged && L > j.cap) L = j.cap;
+        if (L > j.max_keys) j.max_keys = L;
     }
+    atomic_init(&j.next, 0);
+
+    long long work = (long long)batch * seq_len * (j.max_keys > 0 ? j.max_keys : 1) * num_heads;
+    long long items = (long long)batch * num_kv_heads * ((seq_len + PREFILL_TOKENS_PER_ITEM - 1) / PREFILL_TOKENS_PER_ITEM);
+    int       threads = work >= (1LL << 20) ? ffo_default_threads() : 1;
+    if (threads > items) threads = (int)items;
+    if (threads <= 1)
+    {
+        prefill_worker(&j);
+        return 0;
+    }
+    pthread_t* tids = (pthread_t*)malloc(sizeof(pthread_t) * (size_t)threads);
+    for (int i = 0; i < threads; ++i) pthread_create(&tids[i], NULL, prefill_worker, &j);
+    for (int i = 0; i < threads; ++i) pthread_join(tids[i], NULL);
+    free(tids);
     return 0;
 }
