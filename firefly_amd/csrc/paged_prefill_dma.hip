@@ -300,7 +300,7 @@ void paged_prefill_dma(PrefillArgs a)
     __shared__ __align__(16) uint8_t s_st2[kDmaStages<D> >= 3 ? 2 * C::TILEB + C::SCB : 16];
     __shared__ __align__(16) uint8_t s_st3[kDmaStages<D> == 4 ? 2 * C::TILEB + C::SCB : 16];
 
-    __shared__ int s_vover;  // a V value of this workgroup's keys does not fit f16 (VCONV)
+    __shared__ int s_vover;  // some accumulator is not finite after the f16 PV products (bf16 and int8 pages)
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -721,6 +721,9 @@ void paged_prefill_dma(PrefillArgs a)
         v_head_scale = a.v_scale[kvh];
     }
     const float thr_raw = 8.0f / c_log2;
+    // int8 pages: on the rerun below every p is scaled by 2^kRerunShift, numerator and denominator alike, so the
+    // result is the same softmax
+    constexpr float kRerunShift = -12.0f;
     float       m_run[RG], l_run[RG];
     float       m_thr[RG], m_neg[RG];  // m_run + thr_raw, and -m_run * c_log2 (0 before the first key)
     f32x4       acc[RG][NT];
@@ -809,7 +812,8 @@ void paged_prefill_dma(PrefillArgs a)
     };
 
     // Online softmax of a step's scores: the probabilities pv (int8: times the keys' V scales).
-    auto softmax = [&]<bool VC>(int si, const uint8_t* stage, int okm, f32x4 (&s)[RG][KP], float (&pv)[RG][KP * 4])
+    auto softmax = [&]<bool VC, bool SH>(int si, const uint8_t* stage, int okm, f32x4 (&s)[RG][KP],
+                                         float (&pv)[RG][KP * 4])
     {
         constexpr bool LD = L_DOT || VC;  // the f16 P of converted bf16 V tiles sums by dot products too
         const int pg0 = pg_lo + si * KP;
@@ -854,6 +858,7 @@ void paged_prefill_dma(PrefillArgs a)
                 m_run[gi] = upd ? mt : m_run[gi];
                 m_thr[gi] = m_run[gi] + thr_raw;
                 m_neg[gi] = m_run[gi] == kNegInf ? 0.0f : -m_run[gi] * c_log2;  // no key yet: every p is 0
+                if constexpr (SH) m_neg[gi] += kRerunShift;
             }
 #pragma unroll
             for (int e = 0; e < KP * 4; ++e)
@@ -1010,7 +1015,7 @@ void paged_prefill_dma(PrefillArgs a)
     // execute.
     // With three or more stages, step si + 1 has been requested a step before step si is computed, so its tiles
     // are converted while step si's score products run (AH), instead of at the head of step si + 1.
-    auto body = [&]<bool VC>(int si, uint8_t* cur, int okm_cur, uint8_t* nxt, int& okm_nxt, uint8_t* ahead)
+    auto body = [&]<bool VC, bool SH>(int si, uint8_t* cur, int okm_cur, uint8_t* nxt, int& okm_nxt, uint8_t* ahead)
     {
         constexpr bool AH = FFKV_PREFILL_AHEAD && NS >= 3 && (VC || C16);
         wait_vm<(NS - 2) * LPS>();
@@ -1044,12 +1049,13 @@ void paged_prefill_dma(PrefillArgs a)
         if (wave_active)
         {
             float pv[RG][KP * 4];
-            softmax.template operator()<VC>(si, cur, okm_cur, sx, pv);
+            softmax.template operator()<VC, SH>(si, cur, okm_cur, sx, pv);
             pv_mma.template operator()<V16 || VC>(cur, pv);
         }
     };
 
-    auto pipeline = [&]<bool VC>()
+    // VC: bf16 pages' V tiles converted to f16.  SH: int8 pages' p scaled by 2^kRerunShift (the rerun).
+    auto pipeline = [&]<bool VC, bool SH>()
     {
 #pragma unroll
         for (int gi = 0; gi < RG; ++gi)
@@ -1075,35 +1081,34 @@ void paged_prefill_dma(PrefillArgs a)
         {
             if constexpr (NS == 2)
             {
-                body.template operator()<VC>(si, s_st0, okm0, s_st1, okm1, s_st1);
+                body.template operator()<VC, SH>(si, s_st0, okm0, s_st1, okm1, s_st1);
                 if (si + 1 >= steps) break;
-                body.template operator()<VC>(si + 1, s_st1, okm1, s_st0, okm0, s_st0);
+                body.template operator()<VC, SH>(si + 1, s_st1, okm1, s_st0, okm0, s_st0);
             }
             else if constexpr (NS == 3)
             {
-                body.template operator()<VC>(si, s_st0, okm0, s_st2, okm2, s_st1);
+                body.template operator()<VC, SH>(si, s_st0, okm0, s_st2, okm2, s_st1);
                 if (si + 1 >= steps) break;
-                body.template operator()<VC>(si + 1, s_st1, okm1, s_st0, okm0, s_st2);
+                body.template operator()<VC, SH>(si + 1, s_st1, okm1, s_st0, okm0, s_st2);
                 if (si + 2 >= steps) break;
-                body.template operator()<VC>(si + 2, s_st2, okm2, s_st1, okm1, s_st0);
+                body.template operator()<VC, SH>(si + 2, s_st2, okm2, s_st1, okm1, s_st0);
             }
             else
             {
-                body.template operator()<VC>(si, s_st0, okm0, s_st3, okm3, s_st1);
+                body.template operator()<VC, SH>(si, s_st0, okm0, s_st3, okm3, s_st1);
                 if (si + 1 >= steps) break;
-                body.template operator()<VC>(si + 1, s_st1, okm1, s_st0, okm0, s_st2);
+                body.template operator()<VC, SH>(si + 1, s_st1, okm1, s_st0, okm0, s_st2);
                 if (si + 2 >= steps) break;
-                body.template operator()<VC>(si + 2, s_st2, okm2, s_st1, okm1, s_st3);
+                body.template operator()<VC, SH>(si + 2, s_st2, okm2, s_st1, okm1, s_st3);
                 if (si + 3 >= steps) break;
-                body.template operator()<VC>(si + 3, s_st3, okm3, s_st2, okm2, s_st0);
+                body.template operator()<VC, SH>(si + 3, s_st3, okm3, s_st2, okm2, s_st0);
             }
         }
         wait_vm<0>();  // no load may still be writing this workgroup's LDS when it ends
     };
 
-    if constexpr (VCONV)
+    auto acc_finite = [&]() -> bool  // every accumulator of the wave is finite
     {
-        pipeline.template operator()<true>();
         float t = 0.0f;  // 0 if every accumulator is finite, else NaN
 #pragma unroll
         for (int gi = 0; gi < RG; ++gi)
@@ -1111,15 +1116,34 @@ void paged_prefill_dma(PrefillArgs a)
             for (int n = 0; n < NT; ++n)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) t = __builtin_fmaf(acc[gi][n][i], 0.0f, t);
-        if (__any(!(t == 0.0f))) s_vover = 1;
+        return !__any(!(t == 0.0f));
+    };
+    if constexpr (VCONV)
+    {
+        pipeline.template operator()<true, false>();
+        if (!acc_finite()) s_vover = 1;
         wait_lgkm0();
         __builtin_amdgcn_s_barrier();  // flags written; every wave is past its last reads of the stages
         if (s_vover != 0)              // uniform: some V value of the workgroup's keys does not fit f16
-            pipeline.template operator()<false>();
+            pipeline.template operator()<false, false>();
+    }
+    else if constexpr (CT == I8)
+    {
+        // int8 pages: P carries the keys' V scales into the f16 PV products and p < 2^8, so a V scale of 256 or
+        // more (a dequantized |V| from about 32,500) can overflow f16 and make the accumulators infinite or NaN.
+        // The workgroup then runs the pipeline again with every p scaled by 2^-12, which takes V scales up to 2^20
+        // (|V| up to about 1.3e8); products that the scaling takes below f16's normal range keep an absolute error
+        // of at most 2^-13 of the unscaled p times the V scale.
+        pipeline.template operator()<false, false>();
+        if (!acc_finite()) s_vover = 1;
+        wait_lgkm0();
+        __builtin_amdgcn_s_barrier();  // flags written; every wave is past its last reads of the stages
+        if (s_vover != 0)              // uniform
+            pipeline.template operator()<false, true>();
     }
     else
     {
-        pipeline.template operator()<false>();
+        pipeline.template operator()<false, false>();
     }
 
 #pragma unroll
@@ -1139,7 +1163,9 @@ void paged_prefill_dma(PrefillArgs a)
                     *reinterpret_cast<f32x4*>(dst + 16 * n + 4 * g) = acc[gi][n] * v_head_scale;
                 if (g == 0)
                 {
-                    a.ws_ml[(slot * Hq + hq[gi]) * 2] = m_run[gi] == kNegInf ? kNegInf : m_run[gi] * c_log2;
+                    // (an int8 rerun scaled p by 2^kRerunShift, which the partial's max carries)
+                    const float shift = CT == I8 && s_vover != 0 ? kRerunShift : 0.0f;
+                    a.ws_ml[(slot * Hq + hq[gi]) * 2] = m_run[gi] == kNegInf ? kNegInf : m_run[gi] * c_log2 - shift;
                     a.ws_ml[(slot * Hq + hq[gi]) * 2 + 1] = l_tot;
                 }
             }

@@ -82,6 +82,20 @@ FFKV_API int ffkv_append(const void* k_src, const void* v_src, int src_dtype, vo
                 void* stream);
 
 /*
+ * Bytes one pool block (16 tokens of one layer, K and V) takes in a cache of cache_dtype, its scales included:
+ * what an engine divides its memory budget by to size the pools.  Replaces the 16-bit element size in the
+ * reference's `max_num_blocks = 0.9 * free / (num_layers * 16 * Hkv * D * 2 * 2)` (src/engine.cc:90-96, pools
+ * allocated at :104-113):
+ *   F32        16 * Hkv * D * 4 * 2
+ *   F16, BF16  16 * Hkv * D * 2 * 2
+ *   I8         16 * Hkv * (D + 4) * 2   codes and the per-token-per-head fp32 scales [num_blocks, 16, Hkv]
+ *   FP8_E4M3   16 * Hkv * D * 2         codes; the per-head scales (2 * Hkv * 4 bytes per layer) do not grow
+ *                                       with the pool
+ * Returns 0 for another dtype or a non-positive size.  No counterpart in the reference (fp16 pools only).
+ */
+FFKV_API size_t ffkv_kv_block_bytes(int cache_dtype, int num_kv_heads, int head_dim);
+
+/*
  * Bytes of scratch ffkv_paged_decode needs for split-K partial results at these sizes.  max_context_len is
  * an upper bound on context_lens[b] + 1 (<= 0 means max_blocks * 16).  No counterpart in the reference, whose
  * decode kernel has no split-K (src/kernels/attention.cu:475-485).
@@ -189,9 +203,10 @@ FFKV_API int ffkv_paged_decode_shared_prefix(const void* q, void* out, int qo_dt
  * head_dim] tensors and positions start at 0: the reference's causal prefill.  seq_len = 1 is decode attention.
  * cache_dtype F16, BF16, I8 or FP8_E4M3 (scales as for ffkv_paged_decode); any GQA group; scale <= 0 selects
  * 1/sqrt(head_dim).  No workspace; pointers 16-byte aligned.  fp8 per-head K scales may be any finite value (0
- * weighs the keys uniformly, a negative one negates the scores, as in decode).  Range limit of int8 caches: the
- * attention weights meet their V scales in f16, so per-token V scales must stay below 256 (|V| below 32,512).
- * bf16 caches: V enters the products in f16 (a workgroup that meets |V| >= 65520 reruns in bf16), so V values
+ * weighs the keys uniformly, a negative one negates the scores, as in decode).  int8 caches: the attention
+ * weights (below 2^8) meet their V scales in f16, so a per-token V scale of 256 or more can overflow; a workgroup
+ * whose results overflow reruns with its weights scaled by 2^-12, which takes V scales up to 2^20 (|V| up to about
+ * 1.3e8).  bf16 caches: V enters the products in f16 (a workgroup that meets |V| >= 65520 reruns in bf16), so V values
  * below 2^-14 carry an absolute error of at most 2^-25.  16-bit caches: an infinite V value also makes NaN, in
  * its dim, the outputs of the queries whose causal limit masks its key (it meets them with weight 0 in the tile
  * products).

@@ -104,7 +104,7 @@ def test_head_dim_256_dtypes(ff, gpu, act, kv):
 
 @pytest.mark.parametrize("D", [8, 40, 96, 112])
 @pytest.mark.parametrize("act,kv", [("bf16", "bf16"), ("f16", "f16"), ("f32", "f32"), ("bf16", "i8"),
-                                    ("bf16", "fp8"), ("f32", "fp8")])
+                                    ("bf16", "fp8"), ("f32", "fp8"), ("f16", "i8"), ("f16", "fp8")])
 def test_head_dims_multiple_of_8(ff, gpu, D, act, kv):
     """Any head_dim that is a multiple of 8 up to 128, as the reference's decode takes (one 8-element vector per
     lane of a 16-lane group, src/kernels/attention.cu:307-316) and its append (any head_dim up to 128,
@@ -127,7 +127,9 @@ def test_head_dim_96_multi_token_append(ff, gpu, kv):
 @pytest.mark.parametrize("G,Hkv,D,act,kv", [(17, 2, 128, "bf16", "bf16"), (32, 1, 128, "bf16", "bf16"),
                                              (48, 2, 128, "f16", "f16"), (24, 2, 64, "bf16", "fp8"),
                                              (32, 2, 128, "bf16", "i8"), (20, 1, 256, "f32", "bf16"),
-                                             (20, 2, 96, "bf16", "bf16"), (40, 1, 96, "f16", "f16")])
+                                             (20, 2, 96, "bf16", "bf16"), (40, 1, 96, "f16", "f16"),
+                                             (20, 2, 96, "bf16", "i8"), (20, 2, 96, "bf16", "fp8"),
+                                             (24, 1, 96, "f16", "i8")])
 def test_groups_over_16(ff, gpu, G, Hkv, D, act, kv):
     """GQA groups above 16 query heads per KV head (MQA-style): one wave per block of 16 heads of the group."""
     rng = np.random.default_rng(G * 10 + Hkv)

@@ -308,3 +308,41 @@ def test_prefill_bf16_large_v(ff, gpu, D, big):
         # kv head 3's heads (12..15) hold the infinities; the other heads keep the ordinary bar
         assert gf[:, :12].all() and rf[:, :12].all()
         _check(got[1][:, :12], ref[1][:, :12], c.act, 2e-3)
+
+
+def _jump_scores(c, qn, D, b, kvh, positions, v_big, cached_len):
+    """Arrange int8 pools so that the keys at `positions` of row b, kv head kvh score far above the keys before
+    them, and carry V scales of v_big / 127: every K code is 1, q is 1, K scales are 0 except at those keys, whose
+    scale puts the score at 7.9 / (scale * log2 e) above the others.  The online softmax's reference maximum is set
+    by the first step's keys (score 0) and only moves when a score passes it by 8 in log2 units, so those keys
+    enter the PV products with p = 2^7.9 and p times the V scale exceeds f16's range once v_big / 127 > 65504 /
+    2^7.9 (v_big above about 3.1e4).  The chunk's own keys score 0 (zero K)."""
+    c.k_pool[...] = 1
+    c.k_scale[...] = 0.0
+    kscale = np.float32(7.9 * math.log(2.0) / math.sqrt(D))  # s * scale = 7.9 ln 2 with s = D * kscale
+    for t in positions:
+        assert t >= 64 and t < cached_len  # after the first step of 64 keys, inside the cached part
+        page, slot = c.block_table[b, t // 16], t % 16
+        c.k_scale[page, slot, kvh] = kscale
+        c.v_scale[page, slot, kvh] = np.float32(v_big / 127.0)
+    c.k_new[...] = cases.encode(np.zeros(c.k_new.shape, np.float32), c.act)
+    return cases.encode(np.ones(qn.shape, np.float32), c.act)
+
+
+@pytest.mark.parametrize("big", [4.0e4, 1.0e6])
+@pytest.mark.parametrize("D", [64, 128, 256])
+def test_prefill_int8_v_scale_overflow(ff, gpu, D, big):
+    """int8 pages whose P times V scale overflows f16 in the PV products (keys that enter with p = 2^7.9 and V
+    scales of big / 127): the workgroup must run again with p scaled down.  Row 0, kv head 1 holds the keys; its
+    heads match the float64 closed form relative to the largest |v|, and every other (row, head) keeps the
+    quantized bar."""
+    c, qn = _case(180 + D, 2, 8, 2, D, [300, 300], 37, kv="i8")
+    qn = _jump_scores(c, qn, D, 0, 1, [100, 130, 131, 200, 250], big, 300)
+    got, ref = _run(ff, gpu, c, qn)
+    _check(got[1:], ref[1:], c.act, 2e-2)
+    _check(got[0][:, :4], ref[0][:, :4], c.act, 2e-2)
+    g, r = got[0][:, 4:].astype(np.float64), ref[0][:, 4:]
+    err = float(np.abs(g - r).max())
+    print(f"  row 0 kv head 1: max |out| {float(np.abs(r).max()):.3e}, max-abs err {err:.3e}", flush=True)
+    assert float(np.abs(r).max()) > 0.1 * big  # the jump keys dominate these outputs
+    assert np.isfinite(g).all() and err <= 2e-2 * big

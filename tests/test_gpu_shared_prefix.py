@@ -69,6 +69,39 @@ def test_shared_prefix_bf16(ff, gpu, shared, suffix):
     _both(ff, gpu, c, shared)
 
 
+@pytest.mark.parametrize("big", [4.0e4, 1.0e6])
+def test_shared_prefix_int8_v_scale_overflow(ff, gpu, big):
+    """int8 prefix pages whose keys enter the prefix kernel's f16 PV products with p = 2^7.9 and V scales of
+    big / 127 (p times the scale beyond f16's range): its workgroups run again with p scaled down, and the
+    partials they leave carry that scale in their maxima, so the merge with the rows' own pages is unchanged.
+    Every K code is 1 and q is 1; K scales are 0 except at the jump keys (positions 200-203 and 230, in the
+    second step of the second 8-page chunk of the 16-page prefix), of kv head 1.  Outputs match the checker
+    relative to the largest |v| in kv head 1's heads, the quantized bar elsewhere; the plain decode (p <= 1,
+    no overflow) too."""
+    import math
+
+    rng = np.random.default_rng(48)
+    shared, B = 16, 12
+    ctx = shared * 16 + rng.integers(1, 100, size=B) - 1
+    c = cases.make_case(48, B, 8, 2, 128, ctx, act="bf16", kv="i8", shared_prefix_blocks=shared)
+    c.k_pool[...] = 1
+    c.k_scale[...] = 0.0
+    for t in (200, 201, 202, 203, 230):
+        page, slot = c.block_table[0, t // 16], t % 16
+        c.k_scale[page, slot, 1] = np.float32(7.9 * math.log(2.0) / math.sqrt(128))
+        c.v_scale[page, slot, 1] = np.float32(big / 127.0)
+    c.k_new[...] = cases.encode(np.zeros(c.k_new.shape, np.float32), c.act)
+    c.q = cases.encode(np.ones(c.q.shape, np.float32), c.act)
+    got, plain, ref = _run(ff, gpu, c, shared)
+    for out, what in ((got, "shared-prefix decode"), (plain, "plain decode")):
+        _check(out[:, :4], ref[:, :4], c.act, 2e-2, what + ", kv head 0")
+        err = float(np.abs(out[:, 4:].astype(np.float64) - ref[:, 4:]).max())
+        print(f"  {what}, kv head 1: max |out| {float(np.abs(ref[:, 4:]).max()):.3e}, max-abs err {err:.3e}",
+              flush=True)
+        assert np.isfinite(out).all() and err <= 2e-2 * big
+    assert float(np.abs(ref[:, 4:]).max()) > 0.1 * big
+
+
 @pytest.mark.parametrize("big", [7.0e4, float("inf")])
 def test_shared_prefix_large_v(ff, gpu, big):
     """bf16 V values beyond f16's range in the shared pages: the prefix kernel's f16 PV products overflow, and
