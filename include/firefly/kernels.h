@@ -8,6 +8,12 @@
 // :138-143), exported here, a fused rope + append, and quantized-cache overloads.  Each forwards to the C ABI
 // in ffkv.h.
 //
+// The reference's other operators (the model math, off this path) keep their declarations below unchanged, so
+// that src/model/qwen_model.cu and src/engine.cc compile against this header; their definitions stay in the
+// caller's own kernel files (src/kernels/{embedding,norm,activation,add,linear,sampling}.cu), which this
+// library does not provide.  The caller drops the stream setter/getter its src/kernels/embedding.cu:41-45 defines
+// (cudaStream_t): this library's set_default_stream / get_default_stream (hipStream_t) replace them.
+//
 // Like the reference, the functions return void and report failures on std::cerr
 // (src/kernels/attention.cu:487-491); last_error() additionally returns the message of the calling thread's
 // last failure ("" if none).  Everything is asynchronous on the default stream and may be captured in a hipGraph.
@@ -25,6 +31,18 @@ namespace firefly::kernels
 FIREFLY_API void        set_default_stream(hipStream_t stream);
 FIREFLY_API hipStream_t get_default_stream();
 FIREFLY_API std::string last_error();
+
+// The decode operators keep one split-K workspace per (thread, device, stream), held for the life of the thread
+// (a graph captured on the stream has its address).  release_workspace(stream) synchronizes `stream` and frees
+// the calling thread's workspace for it on the current device; call it when a stream is retired and no graph
+// captured on it will be replayed again (the next call on that stream allocates a new one).  No counterpart in the
+// reference, whose temporaries are stream-ordered allocations.
+FIREFLY_API void release_workspace(hipStream_t stream);
+
+// Bytes one pool block (16 tokens of one layer, K and V, scales included) takes for a cache dtype (F32, F16, BF16,
+// I8, FP8_E4M3; 0 otherwise): the divisor of the engine's pool sizing (src/engine.cc:90-96), which assumes 2-byte
+// elements.  fp8 caches add 2 * num_kv_heads * 4 bytes of per-head scales per layer.  ffkv_kv_block_bytes.
+FIREFLY_API size_t kv_block_bytes(DType cache_dtype, int num_kv_heads, int head_dim);
 
 /**
  * @brief Scaled dot-product attention (reference include/firefly/kernels.h:83-84).
@@ -108,5 +126,25 @@ FIREFLY_API void rope_append_kv_cache(Tensor& q, Tensor& k, const Tensor& v, Ten
 FIREFLY_API void rope_append_kv_cache(Tensor& q, Tensor& k, const Tensor& v, Tensor& k_cache, Tensor& v_cache,
                                       Tensor& k_scale, Tensor& v_scale, const int* block_table,
                                       const int* context_lens, int max_blocks, float theta);
+
+// ---- the reference's off-path operators: declared as in its include/firefly/kernels.h, defined by the caller --
+
+// Embedding lookup (reference include/firefly/kernels.h:18).
+void embedding_lookup(const Tensor& input_ids, const Tensor& embedding_table, Tensor& output);
+
+// RMS normalization (reference include/firefly/kernels.h:28).
+void rms_norm(const Tensor& input, const Tensor& weight, Tensor& output, double epsilon);
+
+// SwiGLU: silu(gate) * up (reference include/firefly/kernels.h:39).
+void swiglu(const Tensor& gate, const Tensor& up, Tensor& output);
+
+// x += y (reference include/firefly/kernels.h:47).
+void add_inplace(Tensor& x, const Tensor& y);
+
+// output = input * weight (reference include/firefly/kernels.h:56).
+void matmul(const Tensor& input, const Tensor& weight, Tensor& output);
+
+// Greedy sampling (reference include/firefly/kernels.h:92).
+void argmax(const Tensor& logits, Tensor& output_token);
 
 }  // namespace firefly::kernels

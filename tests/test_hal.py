@@ -50,3 +50,14 @@ def test_engine_call_shapes_capture_and_replay_on_gpu(gpu):
     res = subprocess.run([str(PREBUILT)], capture_output=True, text=True, timeout=120)
     assert res.returncode == 0, res.stdout + res.stderr
     assert "OK (gpu)" in res.stdout
+
+
+def test_model_and_engine_kernel_call_shapes_compile():
+    """Every firefly::kernels call of the reference's QwenModel::forward (src/model/qwen_model.cu:98-191) and
+    engine (src/engine.cc:136-148, :267), the off-path operators included, compiles against include/firefly
+    (tests/cpp/model_calls.cpp: compiled, not linked; those operators are defined by the caller's kernel files)."""
+    src = ROOT / "tests" / "cpp" / "model_calls.cpp"
+    cmd = ["/opt/rocm/bin/hipcc", "-std=c++20", "-Wall", "-Werror", "-Wno-unused-command-line-argument",
+           "-fsyntax-only", f"-I{ROOT / 'include'}", str(src)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    assert res.returncode == 0, f"model / engine call shapes do not compile against include/firefly:\n{res.stderr}"
