@@ -163,6 +163,27 @@ int RadixTree::evict(int num_blocks_needed)
     return freed;
 }
 
+std::pair<int, bool> RadixTree::count_evictable(const TreeNode& node) const
+{
+    int  blocks = 0;
+    bool whole = node.ref_count == 0;
+    for (const auto& kv : node.children)
+    {
+        const auto [b, w] = count_evictable(*kv.second);
+        blocks += b;
+        whole = whole && w;
+    }
+    // evict() removes unreferenced leaves until none is left: a node goes once its whole subtree is unreferenced
+    if (whole && &node != root_.get()) blocks += static_cast<int>(node.block_indices.size());
+    return {blocks, whole};
+}
+
+int RadixTree::evictable_blocks() const
+{
+    std::lock_guard<std::mutex> lock(mutex_);
+    return count_evictable(*root_).first;
+}
+
 void RadixTree::print_stats() const
 {
     std::lock_guard<std::mutex> lock(mutex_);

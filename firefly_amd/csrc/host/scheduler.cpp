@@ -55,6 +55,11 @@ int BlockAllocator::get_free_blocks() const { return static_cast<int>(free_list_
 
 Scheduler::Scheduler() = default;
 
+void Scheduler::init(int max_context_blocks, int max_batch_size_limit, int max_prefill_chunk_size)
+{
+    init(max_context_blocks, max_batch_size_limit, max_prefill_chunk_size, PrefillBlocks::PerChunk);
+}
+
 void Scheduler::init(int max_context_blocks, int max_batch_size_limit, int max_prefill_chunk_size,
                      PrefillBlocks prefill_blocks)
 {
@@ -108,6 +113,14 @@ int Scheduler::blocks_to_run(const GenerationRequest& r) const
     return r.get_total_len() >= have * block_size_ ? 1 : 0;
 }
 
+// Blocks a request part-way through its prompt still needs to hold the whole prompt (0 once decoding).
+int Scheduler::prompt_blocks_left(const GenerationRequest& r) const
+{
+    if (!r.generated_tokens.empty()) return 0;
+    const int want = (static_cast<int>(r.prompt_tokens.size()) + block_size_ - 1) / block_size_;
+    return std::max(0, want - static_cast<int>(r.block_table.size()));
+}
+
 // Appends `blocks` new blocks to r's table (evicting from the prefix cache if the allocator must); false, and no
 // change, if they cannot be had.
 bool Scheduler::reserve(GenerationRequest& r, int blocks)
@@ -128,12 +141,26 @@ void Scheduler::uncache_last_node(GenerationRequest& r)
 }
 
 // Admission of a pending request: a free batch slot and the blocks of its first chunk, both available now.
+// Under PerChunk the whole prompt must fit beside what the admitted prompts still need (reserved_), counting
+// blocks the prefix cache can give back; the reference (OnePerStep) counts free blocks against the first chunk
+// only, so two long prompts admitted together can each wait forever for the blocks of their next chunk.
 bool Scheduler::admit(GenerationRequest& r)
 {
     if (r.context_len == static_cast<int>(r.prompt_tokens.size()) && !r.radix_nodes.empty()) uncache_last_node(r);
     const int need = (step_tokens(r) + block_size_ - 1) / block_size_ - static_cast<int>(r.block_table.size());
-    if (static_cast<int>(active_.size()) >= max_batch_ || need > allocator_.get_free_blocks()) return false;
-    if (!reserve(r, need)) return false;
+    if (static_cast<int>(active_.size()) >= max_batch_) return false;
+    if (prefill_blocks_ == PrefillBlocks::PerChunk)
+    {
+        const int whole = prompt_blocks_left(r);
+        if (whole + reserved_ > allocator_.get_free_blocks() + tree_->evictable_blocks()) return false;
+        if (!reserve(r, need)) return false;
+        reserved_ += whole - need;
+    }
+    else
+    {
+        if (need > allocator_.get_free_blocks()) return false;
+        if (!reserve(r, need)) return false;
+    }
     r.status = RequestStatus::ACTIVE;
     return true;
 }
@@ -153,6 +180,8 @@ SchedulerBatch Scheduler::step()
     }
 
     // Then waiting requests, longest cached prefix first (a stable order among equals), until one does not fit.
+    reserved_ = 0;
+    for (const RequestPtr& r : active_) reserved_ += prompt_blocks_left(*r);
     pending_.sort([](const RequestPtr& x, const RequestPtr& y) { return x->context_len > y->context_len; });
     while (!pending_.empty() && admit(*pending_.front()))
     {

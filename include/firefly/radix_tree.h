@@ -60,6 +60,10 @@ public:
     // evictable); returns the number of blocks freed.
     int evict(int num_blocks_needed);
 
+    // Blocks evict() could free now: those of every node whose subtree holds no referenced node.  Not in the
+    // reference; the scheduler's PrefillBlocks::PerChunk admission counts them.
+    int evictable_blocks() const;
+
     void print_stats() const;
 
 private:
@@ -67,6 +71,8 @@ private:
 
     void find_evictable(const std::shared_ptr<TreeNode>& node, const std::shared_ptr<TreeNode>& parent,
                         std::vector<LeafRef>& out) const;
+    // (blocks evictable within node's subtree, whether the whole subtree is unreferenced)
+    std::pair<int, bool> count_evictable(const TreeNode& node) const;
 
     std::shared_ptr<TreeNode> root_;
     BlockAllocator*           allocator_;

@@ -49,7 +49,9 @@ struct SchedulerBatch
 // How a request that is part-way through its prompt gets the blocks of its next prefill chunk.
 enum class PrefillBlocks : uint8_t
 {
-    // Before each chunk runs, the request holds a block for every position the chunk writes.  Default.
+    // Before each chunk runs, the request holds a block for every position the chunk writes, and a prompt is
+    // admitted only when the free and evictable blocks cover the rest of it on top of what the running prompts
+    // still need, so prompts part-way through prefill never wait on each other for blocks.  Default.
     PerChunk,
     // The reference's rule (src/scheduler.cc:88-99,137-149): only the admitting chunk is sized; afterwards a
     // running request gains at most one block per step, so with chunk C a prompt longer than C + 16 tokens runs
@@ -63,9 +65,11 @@ class FIREFLY_API Scheduler
 public:
     Scheduler();
     // max_context_blocks: pool size in blocks; max_batch_size_limit: cap on active requests;
-    // max_prefill_chunk_size: tokens a request may prefill in one step.
+    // max_prefill_chunk_size: tokens a request may prefill in one step.  The three-argument form is the
+    // reference's (same symbol) and selects PrefillBlocks::PerChunk.
+    void init(int max_context_blocks, int max_batch_size_limit, int max_prefill_chunk_size);
     void init(int max_context_blocks, int max_batch_size_limit, int max_prefill_chunk_size,
-              PrefillBlocks prefill_blocks = PrefillBlocks::PerChunk);
+              PrefillBlocks prefill_blocks);
 
     void add_request(RequestPtr req);
     SchedulerBatch step();
@@ -78,6 +82,7 @@ public:
 private:
     int  step_tokens(const GenerationRequest& r) const;
     int  blocks_to_run(const GenerationRequest& r) const;
+    int  prompt_blocks_left(const GenerationRequest& r) const;
     bool reserve(GenerationRequest& r, int blocks);
     void uncache_last_node(GenerationRequest& r);
     bool admit(GenerationRequest& r);
@@ -92,6 +97,7 @@ private:
     int                        max_batch_ = 64;
     int                        max_chunk_ = 256;
     PrefillBlocks              prefill_blocks_ = PrefillBlocks::PerChunk;
+    int                        reserved_ = 0;  // PerChunk: blocks the admitted prompts still need (this step)
 };
 
 }  // namespace firefly

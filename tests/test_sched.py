@@ -186,3 +186,36 @@ def test_per_chunk_policy_covers_every_step(mine, seed):
         # prefix blocks are shared between requests; a request's own blocks never repeat within its table
         for _, _, _, blocks in batch:
             assert len(set(blocks)) == len(blocks)
+
+
+def test_per_chunk_long_prompts_do_not_wait_on_each_other(mine):
+    """Two 600-token prompts (38 blocks each) over a 40-block pool with chunks of 256 tokens.  If both were
+    admitted on their first chunk (16 blocks each), each would then wait forever for the 16 blocks of its second
+    chunk (8 free, nothing to evict).  Under PerChunk a prompt is admitted only when the free and evictable
+    blocks cover all of it beside what the running prompts still need: the second waits until the first has
+    finished and its blocks can be evicted, and both complete, every step holding blocks for what it writes."""
+    rng = np.random.default_rng(11)
+    prompts = {rid: [int(t) for t in rng.integers(1, 50000, size=600)] for rid in (0, 1)}
+    arrivals = {0: [(0, prompts[0], 4), (1, prompts[1], 4)]}
+    trace = su.run_serving(mine, 40, 4, 256, arrivals, max_steps=100, per_chunk=True)
+    assert len(trace) < 100, "the scheduler stopped making progress"
+    done = {rid: max(gen for batch in trace for r, _, gen, _ in batch if r == rid) for rid in (0, 1)}
+    assert done == {0: 3, 1: 3}  # the last scheduled step of each decodes its 4th token
+    rows = _positions_covered(trace, prompts, 256)
+    assert all(end <= have for _, _, end, have in rows)
+    first_of_1 = next(i for i, batch in enumerate(trace) if any(r == 1 for r, *_ in batch))
+    last_of_0 = max(i for i, batch in enumerate(trace) if any(r == 0 for r, *_ in batch))
+    assert first_of_1 > last_of_0
+
+
+def test_per_chunk_admits_beside_a_running_long_prompt(mine):
+    """The reservation counts what a running prompt still needs, not more: a short prompt that fits beside it is
+    admitted while the long one is still prefilling."""
+    rng = np.random.default_rng(12)
+    prompts = {0: [int(t) for t in rng.integers(1, 50000, size=600)],
+               1: [int(t) for t in rng.integers(1, 50000, size=40)]}
+    arrivals = {0: [(0, prompts[0], 2)], 1: [(1, prompts[1], 2)]}
+    trace = su.run_serving(mine, 44, 4, 256, arrivals, max_steps=100, per_chunk=True)
+    assert len(trace) < 100
+    # step 1: request 0 runs its second chunk and request 1 (3 blocks) is admitted beside it (38 + 3 <= 44)
+    assert sorted(r for r, *_ in trace[1]) == [0, 1]
