@@ -53,6 +53,8 @@ def _load() -> ctypes.CDLL:
     vp, i32, f32, sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_size_t
     lib.ffkv_append.restype = i32
     lib.ffkv_append.argtypes = [vp, vp, i32, vp, vp, i32, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, vp]
+    lib.ffkv_kv_block_bytes.restype = sz
+    lib.ffkv_kv_block_bytes.argtypes = [i32, i32, i32]
     lib.ffkv_decode_workspace_bytes.restype = sz
     lib.ffkv_decode_workspace_bytes.argtypes = [i32, i32, i32, i32, i32]
     lib.ffkv_paged_decode.restype = i32
@@ -179,6 +181,11 @@ def rope_append_kv_cache(q, k, v, k_cache, v_cache, block_table, context_lens=No
                                torch_dtype_code(k_cache), _ptr(k_scale), _ptr(v_scale), _ptr(block_table),
                                _ptr(context_lens), B, S, Hq, Hkv, D, BLOCK_SIZE, max_blocks, N, float(theta),
                                _stream(stream)))
+
+
+def kv_block_bytes(cache_dtype: int, num_kv_heads: int, head_dim: int) -> int:
+    """Bytes of one pool block (16 tokens of one layer, K and V, scales included) for a cache dtype."""
+    return int(lib.ffkv_kv_block_bytes(cache_dtype, num_kv_heads, head_dim))
 
 
 def decode_workspace_bytes(batch: int, num_heads: int, head_dim: int, max_blocks: int,

@@ -366,6 +366,27 @@ int ffkv_rope_append(void* q, void* k, const void* v, int src_dtype, void* k_cac
     return ok();
 }
 
+size_t ffkv_kv_block_bytes(int cache_dtype, int num_kv_heads, int head_dim)
+{
+    if (num_kv_heads <= 0 || head_dim <= 0) return 0;
+    const size_t rows = static_cast<size_t>(FFKV_BLOCK_SIZE) * static_cast<size_t>(num_kv_heads);  // token x head
+    const size_t d = static_cast<size_t>(head_dim);
+    switch (cache_dtype)
+    {
+        case FFKV_DTYPE_F32:
+            return rows * d * 4 * 2;
+        case FFKV_DTYPE_F16:
+        case FFKV_DTYPE_BF16:
+            return rows * d * 2 * 2;
+        case FFKV_DTYPE_I8:
+            return rows * (d + 4) * 2;  // codes + one fp32 scale per (token, head), K and V
+        case FFKV_DTYPE_FP8_E4M3:
+            return rows * d * 2;
+        default:
+            return 0;
+    }
+}
+
 size_t ffkv_decode_workspace_bytes(int batch, int num_heads, int head_dim, int max_blocks, int max_context_len)
 {
     if (batch <= 0 || num_heads <= 0 || head_dim <= 0) return 0;

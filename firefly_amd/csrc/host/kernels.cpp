@@ -48,17 +48,30 @@ void fail(const std::string& msg)
 // one, so a graph replayed on one stream does not race with eager calls on another.  A workspace that must grow is
 // replaced by a larger one (at least twice the size) and the old buffer is retired, never freed: a graph captured
 // while it was current has its address baked in and may still be replayed.  Retired buffers are therefore held
-// until the process ends; the geometric growth keeps them smaller in total than the live one.  Nothing here
-// synchronizes the device.
+// until the process ends; the geometric growth keeps them smaller in total than the live one.  A thread that ends
+// retires its live workspaces the same way.  release_workspace() frees a stream's workspace when the caller
+// retires the stream (a host that makes a stream per request would otherwise hold one workspace per stream it
+// ever used).  Nothing here synchronizes the device except release_workspace().
 struct Workspace
 {
     void*  ptr = nullptr;
     size_t bytes = 0;
 };
-thread_local std::map<std::pair<int, hipStream_t>, Workspace> t_ws;
 
 std::mutex         g_retired_mu;
 std::vector<void*> g_retired;  // never freed (see above)
+
+struct WorkspaceCache
+{
+    std::map<std::pair<int, hipStream_t>, Workspace> by_stream;
+    ~WorkspaceCache()  // thread exit: graphs captured by this thread may still hold these addresses
+    {
+        std::lock_guard<std::mutex> lock(g_retired_mu);
+        for (const auto& kv : by_stream)
+            if (kv.second.ptr != nullptr) g_retired.push_back(kv.second.ptr);
+    }
+};
+thread_local WorkspaceCache t_ws;
 
 // A workspace of at least `bytes` for the current device and the default stream, or nullptr while that stream is
 // being captured and its workspace is too small (the library then allocates stream-ordered memory inside the
@@ -67,7 +80,7 @@ void* workspace(size_t bytes, size_t& have)
 {
     int dev = 0;
     (void)hipGetDevice(&dev);
-    Workspace& ws = t_ws[{dev, t_stream}];
+    Workspace& ws = t_ws.by_stream[{dev, t_stream}];
     if (ws.ptr != nullptr && ws.bytes >= bytes)
     {
         have = ws.bytes;
@@ -97,6 +110,35 @@ void* workspace(size_t bytes, size_t& have)
 }
 
 bool is_gpu(const Tensor& t) { return t.device() == Device::GPU; }
+
+}  // namespace
+
+size_t kv_block_bytes(DType cache_dtype, int num_kv_heads, int head_dim)
+{
+    return ffkv_kv_block_bytes(static_cast<int>(cache_dtype), num_kv_heads, head_dim);
+}
+
+void release_workspace(hipStream_t stream)
+{
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    const auto it = t_ws.by_stream.find({dev, stream});
+    if (it == t_ws.by_stream.end()) return;
+    if (it->second.ptr != nullptr)
+    {
+        // the stream's queued work may still use it
+        if (hipStreamSynchronize(stream) != hipSuccess || hipFree(it->second.ptr) != hipSuccess)
+        {
+            std::lock_guard<std::mutex> lock(g_retired_mu);  // keep it rather than free memory still in use
+            g_retired.push_back(it->second.ptr);
+            fail("release_workspace: could not synchronize the stream; the workspace is kept");
+        }
+    }
+    t_ws.by_stream.erase(it);
+}
+
+namespace
+{
 
 int code(DType d) { return static_cast<int>(d); }
 

@@ -18,6 +18,14 @@ static thread_local std::string g_err;
 
 const char* kas_last_error() { return g_err.c_str(); }
 
+// kernels::release_workspace on the calling thread's workspace for `stream`.
+int kas_release_workspace(void* stream)
+{
+    kernels::release_workspace(static_cast<hipStream_t>(stream));
+    if (!kernels::last_error().empty()) return g_err = kernels::last_error(), -1;
+    return 0;
+}
+
 // q [B,1,Hq,D], k_new/v_new [B,S,Hkv,D] in dtype qd; caches [N,16,Hkv,D] in dtype cd; out [B,1,Hq*D] in dtype qd.
 int kas_append_then_decode(void* q, void* k_new, void* v_new, void* k_cache, void* v_cache, void* k_scale,
                            void* v_scale, int scale_rows, void* out, const int* block_table, const int* context_lens,

@@ -209,3 +209,29 @@ def test_prefill_empty_and_contiguous_args_ok(ff):
     assert _prefill(ff, batch=0, q=None) == 0
     assert _prefill(ff, seq_len=0) == 0
     assert ff.lib.ffkv_last_error().decode() == ""
+
+
+@pytest.mark.parametrize("Hkv,D", [(8, 128), (4, 128), (8, 64), (2, 256), (8, 96)])
+def test_kv_block_bytes_matches_the_pool_tensors(ff, Hkv, D):
+    """ffkv_kv_block_bytes x num_blocks = the bytes of the tensors kernels::append_kv_cache takes for a pool of
+    that many blocks: K and V pages [N, 16, Hkv, D] of the cache type, plus int8's per-token-per-head fp32 scales
+    [N, 16, Hkv] for K and V (fp8's per-head scales [Hkv] do not grow with N).  16-bit caches give the reference's
+    divisor 16 * Hkv * D * 2 * 2 (src/engine.cc:90-96)."""
+    import numpy as np
+
+    N = 7
+    elem = {ff.DTYPE_F32: 4, ff.DTYPE_F16: 2, ff.DTYPE_BF16: 2, ff.DTYPE_I8: 1, ff.DTYPE_FP8_E4M3: 1}
+    for dt, es in elem.items():
+        pages = 2 * np.empty((N, 16, Hkv, D), dtype=f"u{es}").nbytes
+        scales = 2 * np.empty((N, 16, Hkv), dtype=np.float32).nbytes if dt == ff.DTYPE_I8 else 0
+        assert ff.kv_block_bytes(dt, Hkv, D) * N == pages + scales, dt
+    assert ff.kv_block_bytes(ff.DTYPE_BF16, Hkv, D) == 16 * Hkv * D * 2 * 2
+    # an 8-bit pool holds about twice the blocks of a 16-bit one in the same memory
+    assert ff.kv_block_bytes(ff.DTYPE_FP8_E4M3, Hkv, D) * 2 == ff.kv_block_bytes(ff.DTYPE_BF16, Hkv, D)
+    assert ff.kv_block_bytes(ff.DTYPE_I8, Hkv, D) < ff.kv_block_bytes(ff.DTYPE_BF16, Hkv, D)
+
+
+def test_kv_block_bytes_rejects(ff):
+    assert ff.kv_block_bytes(7, 8, 128) == 0  # UNKNOWN
+    assert ff.kv_block_bytes(ff.DTYPE_BF16, 0, 128) == 0
+    assert ff.kv_block_bytes(ff.DTYPE_BF16, 8, -1) == 0

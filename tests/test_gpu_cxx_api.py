@@ -43,6 +43,8 @@ def shim(ff):
     lib.kas_decode_shared_prefix.argtypes = [vp] * 6 + [i] * 9 + [vp]
     lib.kas_append_attention.restype = i
     lib.kas_append_attention.argtypes = [vp, vp, i] + [vp] * 6 + [i] * 8 + [vp]
+    lib.kas_release_workspace.restype = i
+    lib.kas_release_workspace.argtypes = [vp]
     return lib
 
 
@@ -81,6 +83,38 @@ def test_cxx_api_append_then_decode(shim, gpu, act, kv, tol):
         assert np.array_equal(dks.cpu().numpy().view(np.uint32), ks.view(np.uint32))
     got = out.float().cpu().numpy().reshape(out32.shape)
     assert np.abs(got - out32).max() <= tol + (0 if c.act == O.DTYPE_F32 else 2.0 ** -9)
+
+
+@pytest.mark.gpu
+def test_cxx_api_release_workspace_between_calls(shim, gpu):
+    """kernels::release_workspace frees a stream's decode workspace: decodes on a fresh stream before and after a
+    release (which allocates a new one) and on a stream never used (a no-op release) give the same bytes."""
+    import torch
+
+    import gpu_util as gu
+
+    c = cases.make_case(33, 8, 32, 8, 128, [900, 20, 4000, 1, 77, 300, 2500, 64])
+    outs = []
+    side = torch.cuda.Stream(device=gpu)
+    for release in (False, True, True):
+        dk, dv = gu.to_dev(c.k_pool, c.kv, gpu), gu.to_dev(c.v_pool, c.kv, gpu)
+        q, kn, vn = gu.to_dev(c.q, c.act, gpu), gu.to_dev(c.k_new, c.act, gpu), gu.to_dev(c.v_new, c.act, gpu)
+        bt, ctx = torch.from_numpy(c.block_table).to(gpu), torch.from_numpy(c.ctx).to(gpu)
+        out = torch.empty((c.B, 1, c.Hq * c.D), dtype=q.dtype, device=gpu)
+        torch.cuda.synchronize()
+        rc = shim.kas_append_then_decode(q.data_ptr(), kn.data_ptr(), vn.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+                                         None, None, 0, out.data_ptr(), bt.data_ptr(), ctx.data_ptr(), c.B, c.S,
+                                         c.Hq, c.Hkv, c.D, c.num_blocks, c.max_blocks, c.act, c.kv, side.cuda_stream)
+        assert rc == 0, shim.kas_last_error()
+        if release:
+            assert shim.kas_release_workspace(side.cuda_stream) == 0, shim.kas_last_error()
+            assert shim.kas_release_workspace(side.cuda_stream) == 0  # nothing left to release
+        torch.cuda.synchronize()
+        outs.append(gu.to_host(out, np.uint16))
+    assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[0], outs[2])
+    _, _, _, _, _, out32 = cases.oracle_step(c)
+    got = gu.out_to_f32(outs[0], c.act).reshape(out32.shape)
+    assert _excess_bf16(got, out32) <= 2e-3
 
 
 @pytest.mark.gpu
