@@ -17,6 +17,8 @@ Printed JSON line (rank 0, N = 1):
                  inputs, same algorithmic-bytes formula, threaded over every core this process may run on
   parity         max-abs error of the layer-0 GPU output against that CPU result (fp32, before rounding)
   device_copy    a 1 GiB torch device copy timed the same way: the streaming rate a plain kernel reaches here
+  read_stream    a read-only 2 GiB stream (firefly_amd/libffkv_bench.so) over a few launch shapes: the practical
+                 read ceiling for the read-dominated decode; decode_kernel_vs_read_stream = roofline.achieved over it
   other_configs  C3, C4 and C5 (int8 and fp8 pools filled by the quantizing append, whose bulk throughput is
                  reported as quantized_append), the C4 prefill on every cache type and head_dim, a head_dim 256
                  decode, the fused rope + append, and the decode step's host upload
@@ -96,6 +98,36 @@ def device_copy_rate(torch, dev, stream, nbytes: int = 1 << 30) -> dict:
     torch.cuda.empty_cache()
     return {"bytes_moved": 2 * nbytes, "us_per_copy": us, "TB_per_s": 2 * nbytes / (us * 1e-6) / 1e12,
             "pct_of_peak": 2 * nbytes / (us * 1e-6) / 1e12 / HBM_PEAK_TBS * 100}
+
+
+def read_stream_rate(torch, dev, stream, nbytes: int = 2 << 30) -> dict | None:
+    """A read-only stream over 2 GiB (firefly_amd/libffkv_bench.so: 16-byte loads, 4 or 8 in flight per lane, one
+    word written per workgroup), timed with HIP events for a few launch shapes: the practical read ceiling of this
+    GPU for a read-dominated kernel such as the decode.  The best shape is `TB_per_s`; every shape is listed."""
+    import ctypes
+
+    path = ROOT / "firefly_amd" / "libffkv_bench.so"
+    if not path.exists():
+        return None
+    lib = ctypes.CDLL(str(path))
+    lib.ffkv_bench_stream_read.restype = ctypes.c_int
+    lib.ffkv_bench_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_int,
+                                           ctypes.c_int, ctypes.c_void_p]
+    src = torch.ones(nbytes, dtype=torch.uint8, device=dev)
+    sink = torch.empty(1 << 16, dtype=torch.int32, device=dev)
+    shapes = {}
+    for blocks in (2048, 4096, 8192, 16384):  # powers of two: 2 GiB splits evenly over every lane
+        for unroll in (4, 8):
+            def call(i, b=blocks, u=unroll):
+                rc = lib.ffkv_bench_stream_read(src.data_ptr(), nbytes, sink.data_ptr(), b, u, stream.cuda_stream)
+                assert rc == 0
+            us = _events_us(call, 20, stream)
+            shapes[f"{blocks}x256_unroll{unroll}"] = {"us": us, "TB_per_s": nbytes / (us * 1e-6) / 1e12}
+    del src, sink
+    torch.cuda.empty_cache()
+    best = max(shapes, key=lambda k: shapes[k]["TB_per_s"])
+    return {"bytes_read": nbytes, "best_shape": best, "TB_per_s": shapes[best]["TB_per_s"],
+            "pct_of_peak": shapes[best]["TB_per_s"] / HBM_PEAK_TBS * 100, "shapes": shapes}
 
 
 BF16_MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense bf16
@@ -438,6 +470,44 @@ def rope_append_config(ff, torch, dev, stream, calls=50, seed=5):
     return res
 
 
+def decode_batch_upload(torch, stream, ctx_np, table_np, calls=50) -> dict | None:
+    """firefly::DecodeBatch::upload itself (through tests/cpp/libdecode_step_shim.so, the C++ API's test shim):
+    the C2 rows packed with DecodeBatch::pack, then one upload per step on the launch stream, timed with HIP
+    events (best of three runs)."""
+    import ctypes
+
+    import numpy as np
+
+    path = ROOT / "tests" / "cpp" / "libdecode_step_shim.so"
+    if not path.exists():
+        return None
+    lib = ctypes.CDLL(str(path))
+    vp, i, ip = ctypes.c_void_p, ctypes.c_int, ctypes.POINTER(ctypes.c_int)
+    for name, res, args in [("dss_create", vp, [i, i]), ("dss_destroy", None, [vp]),
+                            ("dss_pack", i, [vp, i, ip, ip, ip]), ("dss_upload", i, [vp, vp]),
+                            ("dss_last_upload_bytes", ctypes.c_longlong, [vp])]:
+        fn = getattr(lib, name)
+        fn.restype, fn.argtypes = res, args
+    Bn, stride = len(ctx_np), table_np.shape[1]
+    nblk = [int((table_np[b] >= 0).sum()) for b in range(Bn)]
+    blocks = [int(x) for b in range(Bn) for x in table_np[b, :nblk[b]]]
+    arr = lambda xs: (ctypes.c_int * max(1, len(xs)))(*xs)  # noqa: E731
+    h = lib.dss_create(Bn, stride)
+    assert h
+    try:
+        width = lib.dss_pack(h, Bn, arr([int(c) for c in ctx_np]), arr(nblk), arr(blocks))
+        assert width > 0
+
+        def up(k):
+            assert lib.dss_upload(h, stream.cuda_stream) == 0
+
+        us = min(_events_us(up, calls, stream) for _ in range(3))
+        nbytes = int(lib.dss_last_upload_bytes(h))
+    finally:
+        lib.dss_destroy(h)
+    return {"row_stride_blocks": stride, "live_width": width, "bytes": nbytes, "copies": 1, "us_per_step": us}
+
+
 def decode_step_config(ff, torch, dev, stream, ctx_np, table_np, N, pools, q, k_new, v_new, out, ws, max_ctx,
                        calls=50):
     """The engine's per-step host -> device upload of context lengths and block tables (src/engine.cc:296-322):
@@ -461,8 +531,9 @@ def decode_step_config(ff, torch, dev, stream, ctx_np, table_np, N, pools, q, k_
 
         # best of three runs: a small pinned upload's time varies with the host-side copy path from run to run
         us = min(_events_us(up, calls, stream) for _ in range(3))
-        res[label] = {"row_stride_blocks": stride, "bytes": Bn * stride * 4 + Bn * 4, "us_per_step": us}
+        res[label] = {"row_stride_blocks": stride, "bytes": Bn * stride * 4 + Bn * 4, "copies": 2, "us_per_step": us}
         del h, d
+    res["decode_batch"] = decode_batch_upload(torch, stream, ctx_np, table_np, calls)
     table = torch.from_numpy(table_np).to(dev)
     cx = torch.from_numpy(ctx_np.astype(np.int32)).to(dev)
     L = len(pools)
@@ -708,6 +779,7 @@ def main(argv=None) -> int:
         configs = {name: makers[name]() for name in want}
 
     copy_rate = None if args.skip_c2 else device_copy_rate(torch, dev, stream)
+    read_rate = None if args.skip_c2 else read_stream_rate(torch, dev, stream)
 
     # Layer-0 output for the parity figure and the CPU baseline on the same inputs.
     kp0, vp0 = pools[0]
@@ -752,6 +824,9 @@ def main(argv=None) -> int:
                      "traffic": traffic, "traffic_measured_at_commit": traffic_commit,
                      "algorithmic_bytes": dbytes},
         "device_copy": copy_rate,
+        "read_stream": read_rate,
+        "decode_kernel_vs_read_stream": (None if read_rate is None or achieved is None else
+                                         achieved / read_rate["TB_per_s"]),
         "other_configs": configs,
         "cpu_baseline": cpu,
         "parity_max_abs_err_vs_cpu": err,

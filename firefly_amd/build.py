@@ -96,6 +96,18 @@ def build_test_shims() -> None:
         raise RuntimeError(f"test executable build failed: {' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
 
 
+def build_bench_helpers() -> Path:
+    """bench.py's measurement helpers (csrc/bench/*.hip, e.g. the read-only stream) into libffkv_bench.so, apart
+    from the product library."""
+    out = PKG / "libffkv_bench.so"
+    srcs = sorted((CSRC / "bench").glob("*.hip"))
+    cmd = [HIPCC, "-x", "hip", *COMMON, *DEVICE, "-shared", *map(str, srcs), "-o", str(out)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"bench helper build failed: {' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
+    return out
+
+
 def build_oracle() -> None:
     """Build the CPU checker (and, where the reference sources exist, the compiled reference host code)."""
     make = shutil.which("make") or "make"
@@ -111,6 +123,7 @@ def main(argv: list[str] | None = None) -> int:
     args = ap.parse_args(argv)
     lib = build_library(args.jobs)
     build_test_shims()
+    build_bench_helpers()
     print(f"built {lib}")
     if not args.no_oracle:
         build_oracle()

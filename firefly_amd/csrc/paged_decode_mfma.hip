@@ -115,6 +115,28 @@ constexpr int kMfmaWaves =
 #define FFKV_DECODE_TRV 1  // V^T operands through transposed LDS reads (ds_read_b64_tr_b16)
 #endif
 
+// Page loads.  V is staged through LDS, so its loads can take any lane layout: each load instruction reads 64
+// consecutive 16-byte chunks of the wave's slice of the page (whole 128-byte lines of 4 token rows at head_dim
+// 128), non-temporal.  K feeds the matrix products straight from its registers, so its lanes keep the operand
+// layout (64 bytes of each of 16 token rows per instruction).  A read-only stream measured 6.3 TB/s with plain
+// loads in either layout and 7.0-7.2 TB/s once the whole-line half of the traffic is non-temporal: pages are read
+// once per call, and plain loads also allocate them in the caches on the way.
+#ifndef FFKV_DECODE_NT_V
+#define FFKV_DECODE_NT_V 1
+#endif
+#ifndef FFKV_DECODE_NT_K
+#define FFKV_DECODE_NT_K 0  // K (the operand-layout half) non-temporal too
+#endif
+
+template <bool NT>
+__device__ __forceinline__ u32x4 load16(const char* p)
+{
+    if constexpr (NT)
+        return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+    else
+        return *reinterpret_cast<const u32x4*>(p);
+}
+
 // Position of element (token t, dim d) of a wave's V tile: 16-byte chunks XOR-swizzled by row so that the four
 // rows of one transposed read (two chunks each) sit on distinct banks.
 template <int D>
@@ -269,6 +291,14 @@ void paged_decode_mfma(DecodeArgs a)
         v_head_scale = a.v_scale[kvh];
     }
 
+    // V chunks of this lane: chunk i = 64 j + lane of the wave's page slice is token row i / VCPR, 16 bytes at
+    // (i % VCPR) * 16 of it (VCPR 16-byte chunks a row; rows past the page's 16 are not loaded: 8-bit head_dim 96)
+    // (recomputed where used from the lane and the constant j: cheaper than holding them in registers)
+    constexpr int VCPR = D * kElemBytes<CT> / 16;
+    const int     v_row_bytes = a.num_kv_heads * D * kElemBytes<CT>;  // token stride of the pages
+    auto          v_tok = [&](int j) { return (64 * j + lane) / VCPR; };
+    auto          v_chk = [&](int j) { return (64 * j + lane) % VCPR; };
+
     // ---- load cursor: the next page to load and its row -----------------------------------------------------
     // The row's block-table entries come 64 at a time (lane l: entry tb + l); the next row with pages, and its
     // first 64 entries, are fetched as soon as the cursor enters a row, so crossing into it costs no round trip.
@@ -357,43 +387,41 @@ void paged_decode_mfma(DecodeArgs a)
             r.ks = a.k_scale[row_c];
             r.vs = a.v_scale[row_c];
         }
+        // V: whole 16-byte chunks of the slice, rows v_tok (non-temporal)
+        const char* vpage = static_cast<const char*>(a.v_cache) +
+                            (static_cast<size_t>(phys) * kBlockSize * a.num_kv_heads + kvh) * D * kElemBytes<CT>;
         if constexpr (kElemBytes<CT> == 2)
         {
             const char* kp = static_cast<const char*>(a.k_cache) + row_c * D * 2;
-            const char* vp = static_cast<const char*>(a.v_cache) + row_c * D * 2;
             if (c == r.ns)  // fused append: the new token comes from the step's k / v (same dtype as the cache)
-            {
-                const size_t src = (static_cast<size_t>(lrow.b) * a.num_kv_heads + kvh) * D * 2;
-                kp = static_cast<const char*>(a.k_new) + src;
-                vp = static_cast<const char*>(a.v_new) + src;
-            }
+                kp = static_cast<const char*>(a.k_new) + (static_cast<size_t>(lrow.b) * a.num_kv_heads + kvh) * D * 2;
+            const char* vnew = static_cast<const char*>(a.v_new) + (static_cast<size_t>(lrow.b) * a.num_kv_heads + kvh) * D * 2;
 #pragma unroll
             for (int j = 0; j < KSTEPS; ++j)
             {
-                r.k[j] = *reinterpret_cast<const u32x4*>(kp + dim_of<CT>(j, g) * 2);
-                r.v[j] = *reinterpret_cast<const u32x4*>(vp + dim_of<CT>(j, g) * 2);
+                r.k[j] = load16<FFKV_DECODE_NT_K>(kp + dim_of<CT>(j, g) * 2);
+                r.v[j] = load16<FFKV_DECODE_NT_V>(v_tok(j) == r.ns ? vnew + 16 * v_chk(j) : vpage + static_cast<uint32_t>(v_tok(j) * v_row_bytes + 16 * v_chk(j)));
             }
         }
         else
         {
             const char* kp = static_cast<const char*>(a.k_cache) + row_c * D;
-            const char* vp = static_cast<const char*>(a.v_cache) + row_c * D;
 #pragma unroll
             for (int j = 0; j < KSTEPS; j += 2)
             {
                 if (j + 1 < KSTEPS)
                 {
-                    r.k[j / 2] = *reinterpret_cast<const u32x4*>(kp + dimof(j, g));
-                    r.v[j / 2] = *reinterpret_cast<const u32x4*>(vp + dimof(j, g));
+                    r.k[j / 2] = load16<FFKV_DECODE_NT_K>(kp + dimof(j, g));
                 }
                 else  // an odd last k-step: its 8 codes alone
                 {
                     const u32x2 tk = *reinterpret_cast<const u32x2*>(kp + dimof(j, g));
-                    const u32x2 tv = *reinterpret_cast<const u32x2*>(vp + dimof(j, g));
                     r.k[j / 2] = u32x4{tk[0], tk[1], 0u, 0u};
-                    r.v[j / 2] = u32x4{tv[0], tv[1], 0u, 0u};
                 }
             }
+#pragma unroll
+            for (int j = 0; j < NW; ++j)
+                r.v[j] = v_tok(j) < kBlockSize ? load16<FFKV_DECODE_NT_V>(vpage + static_cast<uint32_t>(v_tok(j) * v_row_bytes + 16 * v_chk(j))) : u32x4{0u, 0u, 0u, 0u};
         }
     };
 
@@ -459,29 +487,47 @@ void paged_decode_mfma(DecodeArgs a)
     {
         if constexpr (kElemBytes<CT> == 2)
         {
-            if (c == r.ns && h0 == 0)  // fused append: write the new token's row into its page slot (as ffkv_append)
+            // fused append: write the new token's row into its page slot (as ffkv_append)
+            if (r.ns >= 0 && h0 == 0)
             {
-                const size_t row_c = (static_cast<size_t>(r.phys) * kBlockSize + c) * a.num_kv_heads + kvh;
-                char*        kp = static_cast<char*>(const_cast<void*>(a.k_cache)) + row_c * D * 2;
-                char*        vp = static_cast<char*>(const_cast<void*>(a.v_cache)) + row_c * D * 2;
+                const size_t row_n = (static_cast<size_t>(r.phys) * kBlockSize + r.ns) * a.num_kv_heads + kvh;
+                char*        kp = static_cast<char*>(const_cast<void*>(a.k_cache)) + row_n * D * 2;
+                char*        vp = static_cast<char*>(const_cast<void*>(a.v_cache)) + row_n * D * 2;
+                if (c == r.ns)
 #pragma unroll
-                for (int j = 0; j < KSTEPS; ++j)
-                {
-                    *reinterpret_cast<u32x4*>(kp + dim_of<CT>(j, g) * 2) = r.k[j];
-                    *reinterpret_cast<u32x4*>(vp + dim_of<CT>(j, g) * 2) = r.v[j];
-                }
+                    for (int j = 0; j < KSTEPS; ++j) *reinterpret_cast<u32x4*>(kp + dim_of<CT>(j, g) * 2) = r.k[j];
+#pragma unroll
+                for (int j = 0; j < NW; ++j)
+                    if (v_tok(j) == r.ns) *reinterpret_cast<u32x4*>(vp + 16 * v_chk(j)) = r.v[j];
             }
         }
-        const bool tok_ok = c < n_tok;  // V[t = c], zero for slots past the row's last token
+        // V rows into the LDS tile, zero for slots past the row's last token
 #pragma unroll
-        for (int j = 0; j < KSTEPS; ++j)
+        for (int j = 0; j < NW; ++j)
         {
-            const u32x4 w = tok_ok ? mword.template operator()<VBF>(r.v, j) : u32x4{0u, 0u, 0u, 0u};
+            const int  t = v_tok(j);
+            const bool tok_ok = t < n_tok;
+            if constexpr (kElemBytes<CT> == 2)
+            {
+                const u32x4 w = tok_ok ? r.v[j] : u32x4{0u, 0u, 0u, 0u};
 #if FFKV_DECODE_TRV
-            *reinterpret_cast<u32x4*>(sv + vt_pos<D>(c, dimof(j, g))) = w;
+                *reinterpret_cast<u32x4*>(sv + vt_pos<D>(t, 8 * v_chk(j))) = w;
 #else
-            *reinterpret_cast<u32x4*>(sv + lds_pos<D>(c, dimof(j, g))) = w;
+                *reinterpret_cast<u32x4*>(sv + lds_pos<D>(t, 8 * v_chk(j))) = w;
 #endif
+            }
+            else if (t < kBlockSize)  // 16 codes: dims 16 ch .. 16 ch + 15 as two 8-value words
+            {
+                const u32x4 lo = tok_ok ? codes_to_m<CT, VBF>(r.v[j][0], r.v[j][1]) : u32x4{0u, 0u, 0u, 0u};
+                const u32x4 hi = tok_ok ? codes_to_m<CT, VBF>(r.v[j][2], r.v[j][3]) : u32x4{0u, 0u, 0u, 0u};
+#if FFKV_DECODE_TRV
+                *reinterpret_cast<u32x4*>(sv + vt_pos<D>(t, 16 * v_chk(j))) = lo;
+                *reinterpret_cast<u32x4*>(sv + vt_pos<D>(t, 16 * v_chk(j) + 8)) = hi;
+#else
+                *reinterpret_cast<u32x4*>(sv + lds_pos<D>(t, 16 * v_chk(j))) = lo;
+                *reinterpret_cast<u32x4*>(sv + lds_pos<D>(t, 16 * v_chk(j) + 8)) = hi;
+#endif
+            }
         }
         s = f32x4{0.0f, 0.0f, 0.0f, 0.0f};  // lane (c, g) gets tokens 4g + i of head c
 #pragma unroll
