@@ -21,32 +21,32 @@ DecodeBatch::DecodeBatch(int batch_capacity, int max_context_blocks)
     : capacity_(batch_capacity > 0 ? batch_capacity : 0), stride_(max_context_blocks > 0 ? max_context_blocks : 0)
 {
     if (capacity_ == 0 || stride_ == 0) return;
-    const size_t table = static_cast<size_t>(capacity_) * stride_ * sizeof(int32_t);
-    const size_t lens = static_cast<size_t>(capacity_) * sizeof(int32_t);
-    if (hipHostMalloc(reinterpret_cast<void**>(&h_context_lens_), lens, hipHostMallocDefault) != hipSuccess ||
-        hipHostMalloc(reinterpret_cast<void**>(&h_block_table_), table, hipHostMallocDefault) != hipSuccess ||
-        hipMalloc(reinterpret_cast<void**>(&d_context_lens_), lens) != hipSuccess ||
-        hipMalloc(reinterpret_cast<void**>(&d_block_table_), table) != hipSuccess)
+    lens_rows_ = (capacity_ + stride_ - 1) / stride_;
+    const size_t lens = static_cast<size_t>(lens_rows_) * stride_;
+    const size_t all = (lens + static_cast<size_t>(capacity_) * stride_) * sizeof(int32_t);
+    if (hipHostMalloc(reinterpret_cast<void**>(&h_all_), all, hipHostMallocDefault) != hipSuccess ||
+        hipMalloc(reinterpret_cast<void**>(&d_all_), all) != hipSuccess)
     {
         release();
         return;
     }
+    h_context_lens_ = h_all_;
+    h_block_table_ = h_all_ + lens;
+    d_context_lens_ = d_all_;
+    d_block_table_ = d_all_ + lens;
     // A padded table everywhere before the first upload, and device buffers that hold it from the start.
-    std::fill(h_context_lens_, h_context_lens_ + capacity_, 0);
+    std::fill(h_all_, h_all_ + lens, 0);
     std::fill(h_block_table_, h_block_table_ + static_cast<size_t>(capacity_) * stride_, -1);
-    (void)hipMemcpy(d_context_lens_, h_context_lens_, lens, hipMemcpyHostToDevice);
-    (void)hipMemcpy(d_block_table_, h_block_table_, table, hipMemcpyHostToDevice);
+    (void)hipMemcpy(d_all_, h_all_, all, hipMemcpyHostToDevice);
 }
 
 DecodeBatch::~DecodeBatch() { release(); }
 
 void DecodeBatch::release()
 {
-    if (d_block_table_) (void)hipFree(d_block_table_);
-    if (d_context_lens_) (void)hipFree(d_context_lens_);
-    if (h_block_table_) (void)hipHostFree(h_block_table_);
-    if (h_context_lens_) (void)hipHostFree(h_context_lens_);
-    d_block_table_ = d_context_lens_ = h_block_table_ = h_context_lens_ = nullptr;
+    if (d_all_) (void)hipFree(d_all_);
+    if (h_all_) (void)hipHostFree(h_all_);
+    d_all_ = h_all_ = d_block_table_ = d_context_lens_ = h_block_table_ = h_context_lens_ = nullptr;
 }
 
 int DecodeBatch::pack(const std::vector<const GenerationRequest*>& requests)
@@ -83,15 +83,19 @@ int DecodeBatch::pack(const std::vector<const GenerationRequest*>& requests)
 bool DecodeBatch::upload(hipStream_t stream)
 {
     if (!ok()) return false;
+    // one copy over rows [0, lens_rows + capacity) of the combined buffer: every row's first w ints, w covering
+    // the context lengths (capacity ints in row 0, or whole rows when they take several) and the live width
+    const size_t rows = static_cast<size_t>(lens_rows_) + static_cast<size_t>(capacity_);
+    const int    w = std::max(width_, lens_rows_ == 1 ? capacity_ : stride_);
     const size_t pitch = static_cast<size_t>(stride_) * sizeof(int32_t);
-    if (hipMemcpyAsync(d_context_lens_, h_context_lens_, static_cast<size_t>(capacity_) * sizeof(int32_t),
-                       hipMemcpyHostToDevice, stream) != hipSuccess)
-        return false;
-    if (hipMemcpy2DAsync(d_block_table_, pitch, h_block_table_, pitch, static_cast<size_t>(width_) * sizeof(int32_t),
-                         static_cast<size_t>(capacity_), hipMemcpyHostToDevice, stream) != hipSuccess)
-        return false;
-    last_bytes_ = static_cast<size_t>(capacity_) * sizeof(int32_t) +
-                  static_cast<size_t>(capacity_) * width_ * sizeof(int32_t);
+    hipError_t   e;
+    if (w >= stride_)
+        e = hipMemcpyAsync(d_all_, h_all_, rows * pitch, hipMemcpyHostToDevice, stream);
+    else
+        e = hipMemcpy2DAsync(d_all_, pitch, h_all_, pitch, static_cast<size_t>(w) * sizeof(int32_t), rows,
+                             hipMemcpyHostToDevice, stream);
+    if (e != hipSuccess) return false;
+    last_bytes_ = rows * static_cast<size_t>(std::min(w, stride_)) * sizeof(int32_t);
     return true;
 }
 

@@ -3,11 +3,14 @@
 // Replaces the per-step packing of the reference engine (src/engine.cc:296-323 with GraphData,
 // include/firefly/engine.h:56-68): pinned host staging filled from the scheduled requests, then copied to the
 // fixed device buffers a captured decode graph reads.  The reference fills a [bs, max_context_blocks] table whose
-// row stride is the POOL size (src/engine.cc:96,126,310) and copies all of it every step (25.6 MB at 64 x 100k
-// blocks); here the device table keeps a fixed row stride (so a graph captured once stays valid) but each upload
-// copies only the live width of the rows (the longest row's block count) with one 2D copy, plus the context
-// lengths.  Entries beyond a row's live blocks are never read by the path's kernels (they read blocks
-// 0 .. ceil((context_len + new tokens) / 16) - 1 of a row), so stale device entries there are harmless.
+// row stride is the POOL size (src/engine.cc:96,126,310) and copies all of it, and the context lengths, in
+// separate copies every step (25.6 MB at 64 x 100k blocks); here the device table keeps a fixed row stride (so a
+// graph captured once stays valid) and each upload is ONE copy: the context lengths sit in the rows just before
+// the table in one buffer of that row stride (host and device alike), and the copy takes only the live width of
+// every row (the longest row's block count, at least the lengths' width) - a plain copy when that is the whole
+// stride, a 2D copy otherwise.  Entries beyond a row's live blocks are never read by the path's kernels (they
+// read blocks 0 .. ceil((context_len + new tokens) / 16) - 1 of a row), so stale device entries there are
+// harmless.
 //
 // Padding rows (batch slots past the live requests) get context_len 0 and block -1, as in the reference
 // (src/engine.cc:298-300): append skips them and decode gives them zeros.
@@ -42,8 +45,8 @@ public:
     /// than slots, or a block table longer than max_context_blocks).
     int pack(const std::vector<const GenerationRequest*>& requests);
 
-    /// Copy the packed context lengths and the live width of every table row to the device, on `stream`.
-    /// Asynchronous; the staging must not be re-packed until the copy has completed on the stream.
+    /// Copy the packed context lengths and the live width of every table row to the device, on `stream`, as one
+    /// copy.  Asynchronous; the staging must not be re-packed until the copy has completed on the stream.
     bool upload(hipStream_t stream);
 
     const int32_t* device_context_lens() const { return d_context_lens_; }
@@ -65,8 +68,11 @@ private:
     int      rows_ = 0;
     int      width_ = 1;
     size_t   last_bytes_ = 0;
-    int32_t* h_context_lens_ = nullptr;  // pinned
-    int32_t* h_block_table_ = nullptr;   // pinned, [capacity, stride]
+    int      lens_rows_ = 1;             // rows of `stride` ints holding the context lengths
+    int32_t* h_all_ = nullptr;           // pinned [lens_rows + capacity, stride]: context lengths, then the table
+    int32_t* d_all_ = nullptr;           // the same on the device
+    int32_t* h_context_lens_ = nullptr;  // = h_all_
+    int32_t* h_block_table_ = nullptr;   // = h_all_ + lens_rows * stride, [capacity, stride]
     int32_t* d_context_lens_ = nullptr;
     int32_t* d_block_table_ = nullptr;
 };

@@ -1,5 +1,6 @@
 """The engine's decode step with this library (src/engine.cc:279-351): DecodeBatch packs the scheduled requests'
-context lengths and block tables into pinned staging and uploads only the live table width; one hal::Graph,
+context lengths and block tables into pinned staging and uploads them, the table at its live width only, in one
+copy; one hal::Graph,
 captured once, replays append + PagedAttention for every layer on those device buffers while the batch changes
 (contexts grow, rows cross into new blocks, a request leaves, another joins).  Every step's pages are compared
 bit-exact and its outputs within tolerance with the CPU checker run on the same tables
@@ -92,7 +93,9 @@ def test_graph_replayed_decode_steps_match_checker(shim, gpu):
             assert list(ctxs[:len(reqs)]) == ctx and not ctxs[len(reqs):].any()
             assert (table[len(reqs):, :width] == -1).all()
             assert shim.dss_upload(h, stream) == 0
-            assert shim.dss_last_upload_bytes(h) == CAP * 4 + CAP * width * 4 < CAP * 4 + CAP * STRIDE * 4
+            # one copy: the context lengths' row and the table rows, each as wide as the live width (at least the
+            # CAP lengths), against the lengths plus the whole stride in the reference's two copies
+            assert shim.dss_last_upload_bytes(h) == (1 + CAP) * max(width, CAP) * 4 < CAP * 4 + CAP * STRIDE * 4
             # this step's inputs
             qs, kns, vns = [], [], []
             for l in range(L):
