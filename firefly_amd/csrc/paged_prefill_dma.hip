@@ -149,10 +149,19 @@ __device__ __forceinline__ int v_swizzle(int t)
     return D == 64 ? 2 * ((t >> 1) & 3) : 2 * (t & 7);
 }
 
-// K swizzle: the same row permutation as lds_pos<D>.
+// K swizzle: 16-byte chunk c of key row t sits at chunk c ^ k_swizzle<D>(t).  A K operand read takes the same
+// chunk of 16 key rows, and 16 lanes of a 16-byte read are served per LDS cycle (256 bytes), so the 16 rows must
+// land on distinct 16-byte slots of a 256-byte window: at head_dim 128 and 256 a row is a multiple of 256 bytes
+// and the swizzle permutes all 16 chunk slots (with the 8 slots of the earlier 3-bit swizzle, every such read
+// cost a 2-way conflict: LDS bank-conflict cycles equal to the product count); 128-byte rows (head_dim 64)
+// alternate the window's halves by themselves.
+template <int D>
 __device__ __forceinline__ int k_swizzle(int t)
 {
-    return (t & 7) ^ ((t >> 3) << 1);
+    if constexpr (D == 64)
+        return (t & 7) ^ ((t >> 3) << 1);
+    else
+        return t & 15;
 }
 
 // 8-bit K rows (D bytes): the 16 rows of one 8-byte operand read (same chunk) on distinct banks.
@@ -548,7 +557,7 @@ void paged_prefill_dma(PrefillArgs a)
         else if constexpr (Q8)
             sw = is_v ? v8_swizzle<D>(tok, u) : k8_swizzle<D>(tok);
         else
-            sw = is_v ? v_swizzle<D>(tok) : k_swizzle(tok);
+            sw = is_v ? v_swizzle<D>(tok) : k_swizzle<D>(tok);
         const int ch = (p % LC::CPT) ^ sw;
         vtok[k] = tok;
         voff[k] = static_cast<uint32_t>(tok * Hkv * LC::RB + 16 * ch);
@@ -582,7 +591,7 @@ void paged_prefill_dma(PrefillArgs a)
             const int p = run_lr(k) * 64 % LC::CHUNKS + lane;
             const int tok = p / LC::CPT;
             const int ch = p % LC::CPT;
-            const int sw = run_is_v(k) ? v_swizzle<D>(tok) : k_swizzle(tok);
+            const int sw = run_is_v(k) ? v_swizzle<D>(tok) : k_swizzle<D>(tok);
 #pragma unroll
             for (int h = 0; h < 2; ++h) c16_dst[k][h] = 32 * (lane - ch) - 1024 + 16 * ((2 * ch + h) ^ sw);
         }
@@ -736,11 +745,12 @@ void paged_prefill_dma(PrefillArgs a)
     for (int off = 1; off < 16; off <<= 1) kmin = min(kmin, __shfl_xor(kmin, off, 64));
     kmin = __builtin_amdgcn_readfirstlane(kmin);
 
-    // 16-bit K operand of k-step j: key c, dims 32j + 8g .. +8 at element lds_pos<D>(c, 32j + 8g) =
-    // c*D + 8*(g ^ s01) + 32*(j ^ s2) with the row swizzle sw = 4*s2 + s01: an even and an odd base plus 32j.
-    const int ksw = k_swizzle(c);
-    const int kb_even = 2 * (c * D + 8 * (g ^ (ksw & 3)) + 32 * (ksw >> 2));  // bytes
-    const int kb_odd = 2 * (c * D + 8 * (g ^ (ksw & 3)) - 32 * (ksw >> 2));
+    // 16-bit K operand of k-step j: key c, dims 32j + 8g .. +8, chunk (4 j + g) ^ ksw of the key's row, at bytes
+    // kb4[j % 4] + 64 (j - j % 4) (the swizzle's upper bits XOR j % 4)
+    const int ksw = k_swizzle<D>(c);
+    int       kb4[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) kb4[m] = 2 * (c * D + 8 * (g ^ (ksw & 3)) + 32 * (m ^ (ksw >> 2)));
     // 16-bit V^T operand via transposed reads: this lane supplies dims 16n + 4q .. +3 of key row 4g + rr of a page
     const int vrow = 4 * g + (c >> 2);
     const int vsw = v_swizzle<D>(vrow) >> 1;
@@ -772,7 +782,7 @@ void paged_prefill_dma(PrefillArgs a)
             }
             else
             {
-                const int ka = ((j & 1) ? kb_odd : kb_even) + 64 * j;
+                const int ka = kb4[j & 3] + 64 * (j & ~3);
                 return __builtin_bit_cast(X8, *reinterpret_cast<const u32x4*>(stage + u * kBlockSize * C::RB + ka));
             }
         };
