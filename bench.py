@@ -609,7 +609,7 @@ def main(argv=None) -> int:
                     help="skip the other BASELINE configurations (C3, C4, C5 int8/fp8) and the rope+append figures")
     ap.add_argument("--configs", default="all",
                     help="comma-separated subset of C3,C5_int8,C5_fp8,C4,prefill_variants,decode_d256,decode_d96,"
-                         "decode_d112,rope_append,C2_decode_step_host (default all)")
+                         "decode_d112,decode_d80,rope_append,C2_decode_step_host (default all)")
     ap.add_argument("--skip-c2", action="store_true",
                     help="skip the C2 steps, the device copy and the CPU baseline (profiling other configurations "
                          "alone); the headline fields are then null")
@@ -760,9 +760,12 @@ def main(argv=None) -> int:
             "decode_d96": lambda: decode_config(ff, torch, dev, stream, "head_dim 96 decode (matrix cores): "
                                                 "Hq32/Hkv8/D96 bf16, B=64, ctx U[512,4096]", 64, 32, 8, 96, d96_ctx,
                                                 seed=9),
-            "decode_d112": lambda: decode_config(ff, torch, dev, stream, "head_dim 112 decode (the vector kernel): "
-                                                 "Hq32/Hkv8/D112 bf16, B=64, ctx U[512,4096]", 64, 32, 8, 112,
-                                                 d112_ctx, seed=10),
+            "decode_d112": lambda: decode_config(ff, torch, dev, stream, "head_dim 112 decode (matrix cores, a last "
+                                                 "k-step of 16 dims): Hq32/Hkv8/D112 bf16, B=64, ctx U[512,4096]",
+                                                 64, 32, 8, 112, d112_ctx, seed=10),
+            "decode_d80": lambda: decode_config(ff, torch, dev, stream, "head_dim 80 decode (matrix cores, a last "
+                                                "k-step of 16 dims): Hq32/Hkv8/D80 bf16, B=64, ctx U[512,4096]",
+                                                64, 32, 8, 80, d80_ctx, seed=11),
             "rope_append": lambda: rope_append_config(ff, torch, dev, stream),
             "C2_decode_step_host": lambda: decode_step_config(ff, torch, dev, stream, ctx_np, table_np, N, pools, q,
                                                               k_new, v_new, out, ws, max_ctx),
@@ -771,6 +774,7 @@ def main(argv=None) -> int:
         d256_ctx = rng.integers(512, 4097, size=64)
         d96_ctx = rng.integers(512, 4097, size=64)
         d112_ctx = rng.integers(512, 4097, size=64)
+        d80_ctx = rng.integers(512, 4097, size=64)
         want = list(makers) if args.configs == "all" else [x for x in args.configs.split(",") if x]
         unknown = [x for x in want if x not in makers]
         if unknown:

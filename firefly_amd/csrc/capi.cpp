@@ -89,8 +89,10 @@ namespace ffkv
 
 bool decode_use_mfma(int cache_dtype, int /*group*/, int head_dim)
 {
-    // head_dim 96 on the matrix cores too (three k-steps of 32 dims)
-    return !env_force_generic() && cache_dtype != FFKV_DTYPE_F32 && (head_dim_mfma(head_dim) || head_dim == 96);
+    // head_dim 96 on the matrix cores too (three k-steps of 32 dims), and 80 and 112 (k-steps of 32 dims and a last
+    // one of 16)
+    return !env_force_generic() && cache_dtype != FFKV_DTYPE_F32 &&
+           (head_dim_mfma(head_dim) || head_dim == 80 || head_dim == 96 || head_dim == 112);
 }
 
 // MFMA workspace layout: [row meta: batch x 2 int32 | (m, l): slots x num_heads x 2 fp32 | acc: slots x num_heads

@@ -51,14 +51,15 @@ namespace ffkv
 namespace
 {
 
-// One page in flight: NW 16-byte words of K and of V per lane as loaded (one k-step each for 16-bit caches, two
-// for 8-bit codes, which convert when the page is staged so the loads stay in flight until then), the physical
-// block, and the row the page belongs to.
-template <int NW>
+// One page in flight: NW 16-byte words of K per lane as loaded (one k-step each for 16-bit caches, two for 8-bit
+// codes, which convert when the page is staged so the loads stay in flight until then), the K words of a last
+// 16-dim k-step (head_dim 80, 112), NWV 16-byte words of V, the physical block, and the row the page belongs to.
+template <int NW, int NWV>
 struct PageRegs
 {
-    u32x4 k[NW];
-    u32x4 v[NW];
+    u32x4 k[NW > 0 ? NW : 1];
+    u32x2 kt;  // last 16-dim k-step: 4 values (8 bytes) of 16-bit K, or 4 codes (first word)
+    u32x4 v[NWV];
     int   phys;
     bool  ok;
     int   b;   // row
@@ -108,8 +109,8 @@ constexpr int kMfmaDepth =
 // Waves per SIMD the register budget is sized for (168 registers at 3, 128 at 4, 256 at 2).
 template <int CT, int QT, int D>
 constexpr int kMfmaWaves =
-    D == 256 ? 2
-    : D == 96 ? (QT == CT ? 3 : 2)  // a q of another type needs its lo part: three waves' registers would spill
+    D == 256 || D == 112 ? 2
+    : D == 96 || D == 80 ? (QT == CT ? 3 : 2)  // a q of another type needs its lo part: three waves' registers would spill
              : (D == 128 ? (kElemBytes<CT> == 2 ? FFKV_MFMA_WAVES128_16
                                                 : (CT == FP8 ? FFKV_MFMA_WAVES128_FP8 : FFKV_MFMA_WAVES128_I8))
                          : (kMfmaDepth<CT, D> > 1 ? 3 : 4));
@@ -146,7 +147,9 @@ template <int D>
 __device__ __forceinline__ int vt_pos(int t, int d)
 {
     // head_dim 96 (12 chunks a row, whose 192-byte stride already spreads a read's four rows over the banks): the
-    // swizzle stays within aligned groups of four chunks, so it never leaves the row
+    // swizzle stays within aligned groups of four chunks, so it never leaves the row; head_dim 80 and 112 (160- and
+    // 224-byte rows) put the 8 rows of two transposed reads on distinct banks unswizzled
+    if constexpr (D == 80 || D == 112) return t * D + d;
     const int sw = D == 64 ? 2 * ((t >> 1) & 3) : (D == 96 ? 2 * ((t >> 2) & 1) : 2 * (t & 7));
     return t * D + (((d >> 3) ^ sw) << 3) + (d & 7);
 }
@@ -156,7 +159,8 @@ __device__ __forceinline__ int vt_pos(int t, int d)
 // head_dim 96 98.6 -> 88.8 us, fp8 C5 395 -> 390 us; bf16 at 128 unchanged, int8 slower (417 -> 439 us).
 template <int CT, int D>
 constexpr int kMfmaMaxWaves =
-    (D == 96 && kElemBytes<CT> == 2) || (CT == FP8 && D == 128) ? FFKV_MFMA_MAX_WAVES_WIDE : FFKV_MFMA_MAX_WAVES;
+    ((D == 80 || D == 96 || D == 112) && kElemBytes<CT> == 2) || (CT == FP8 && D == 128) ? FFKV_MFMA_MAX_WAVES_WIDE
+                                                                                          : FFKV_MFMA_MAX_WAVES;
 
 // Work item i (blockIdx.x) of W (gridDim.x); KV heads blockIdx.y*NW .. +NW, one per wave.
 template <int CT, int QT, int D>
@@ -172,12 +176,17 @@ void paged_decode_mfma(DecodeArgs a)
     using M = MType<BF>;
     using MV = MType<VBF>;
     using X8 = typename M::x8;
-    constexpr int  KSTEPS = D / 32;
+    using X4 = typename M::x4;
+    constexpr int  KSTEPS = D / 32;            // k-steps of 32 dims (16x16x32 products)
+    constexpr bool KT = D % 32 == 16;          // and a last one of 16 dims (16x16x16): head_dim 80, 112
+    constexpr int  DT = 32 * KSTEPS;           // its first dim
     constexpr int  NT = D / 16;  // output tiles of 16 dims
     constexpr bool NEED_LO = !((QT == BF16 && BF) || (QT == F16 && !BF));
     constexpr bool P_LO = VBF;  // bf16 P: hi + lo parts
     constexpr int  DEPTH = kMfmaDepth<CT, D>;
     constexpr int  NW = kElemBytes<CT> == 2 ? KSTEPS : (KSTEPS + 1) / 2;
+    constexpr int  VCPR = D * kElemBytes<CT> / 16;  // 16-byte chunks of a token's V row
+    constexpr int  NWV = (kBlockSize * VCPR + 63) / 64;  // V load instructions per page
     // First dim of k-step j's 8 values in lane group g.  8-bit codes pair k-steps in one 16-byte read; an odd last
     // k-step (head_dim 96) reads its 8 codes alone, at dims 32j + 8g.
     auto dimof = [](int j, int g)
@@ -304,7 +313,6 @@ void paged_decode_mfma(DecodeArgs a)
     // V chunks of this lane: chunk i = 64 j + lane of the wave's page slice is token row i / VCPR, 16 bytes at
     // (i % VCPR) * 16 of it (VCPR 16-byte chunks a row; rows past the page's 16 are not loaded: 8-bit head_dim 96)
     // (recomputed where used from the lane and the constant j: cheaper than holding them in registers)
-    constexpr int VCPR = D * kElemBytes<CT> / 16;
     const int     v_row_bytes = a.num_kv_heads * D * kElemBytes<CT>;  // token stride of the pages
     auto          v_tok = [&](int j) { return (64 * j + lane) / VCPR; };
     auto          v_chk = [&](int j) { return (64 * j + lane) % VCPR; };
@@ -365,7 +373,7 @@ void paged_decode_mfma(DecodeArgs a)
     int lp = start;  // next page to load
 
     // Issue the K and V loads of page lp into r and advance the cursor.
-    auto load_next = [&](PageRegs<NW>& r)
+    auto load_next = [&](PageRegs<NW, NWV>& r)
     {
         if (lp == lrow.pb + lrow.nb)
         {
@@ -407,11 +415,16 @@ void paged_decode_mfma(DecodeArgs a)
                 kp = static_cast<const char*>(a.k_new) + (static_cast<size_t>(lrow.b) * a.num_kv_heads + kvh) * D * 2;
             const char* vnew = static_cast<const char*>(a.v_new) + (static_cast<size_t>(lrow.b) * a.num_kv_heads + kvh) * D * 2;
 #pragma unroll
-            for (int j = 0; j < KSTEPS; ++j)
-            {
-                r.k[j] = load16<FFKV_DECODE_NT_K>(kp + dim_of<CT>(j, g) * 2);
-                r.v[j] = load16<FFKV_DECODE_NT_V>(v_tok(j) == r.ns ? vnew + 16 * v_chk(j) : vpage + static_cast<uint32_t>(v_tok(j) * v_row_bytes + 16 * v_chk(j)));
-            }
+            for (int j = 0; j < KSTEPS; ++j) r.k[j] = load16<FFKV_DECODE_NT_K>(kp + dim_of<CT>(j, g) * 2);
+            if constexpr (KT) r.kt = *reinterpret_cast<const u32x2*>(kp + (DT + 4 * g) * 2);
+#pragma unroll
+            for (int j = 0; j < NWV; ++j)
+                r.v[j] = v_tok(j) < kBlockSize
+                             ? load16<FFKV_DECODE_NT_V>(v_tok(j) == r.ns
+                                                            ? vnew + 16 * v_chk(j)
+                                                            : vpage + static_cast<uint32_t>(v_tok(j) * v_row_bytes +
+                                                                                            16 * v_chk(j)))
+                             : u32x4{0u, 0u, 0u, 0u};
         }
         else
         {
@@ -429,15 +442,50 @@ void paged_decode_mfma(DecodeArgs a)
                     r.k[j / 2] = u32x4{tk[0], tk[1], 0u, 0u};
                 }
             }
+            if constexpr (KT) r.kt = u32x2{*reinterpret_cast<const uint32_t*>(kp + DT + 4 * g), 0u};
 #pragma unroll
-            for (int j = 0; j < NW; ++j)
+            for (int j = 0; j < NWV; ++j)
                 r.v[j] = v_tok(j) < kBlockSize ? load16<FFKV_DECODE_NT_V>(vpage + static_cast<uint32_t>(v_tok(j) * v_row_bytes + 16 * v_chk(j))) : u32x4{0u, 0u, 0u, 0u};
         }
     };
 
-    X8   qhi[KSTEPS], qlo[KSTEPS];
+    X8   qhi[KSTEPS > 0 ? KSTEPS : 1], qlo[KSTEPS > 0 ? KSTEPS : 1];
+    X4   qthi, qtlo;  // last 16-dim k-step (KT): dims DT + 4g .. + 3
     auto load_q = [&](int b)  // Q of row b's group as MFMA B operands (column c = head, zero beyond the group)
     {
+        if constexpr (KT)
+        {
+            const size_t e = (static_cast<size_t>(b) * a.num_heads + kvh * G + h0 + c) * D + DT + 4 * g;
+            float        x[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            if (c < gc)
+            {
+                if constexpr (QT == F32)
+                {
+                    const f32x4 v = *reinterpret_cast<const f32x4*>(static_cast<const float*>(a.q) + e);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) x[i] = v[i];
+                }
+                else
+                {
+                    const u32x2 w = *reinterpret_cast<const u32x2*>(static_cast<const uint16_t*>(a.q) + e);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                    {
+                        const uint32_t h = (w[i >> 1] >> (16 * (i & 1))) & 0xffffu;
+                        x[i] = QT == BF16 ? bf16_to_f32(h) : f16_to_f32(h);
+                    }
+                }
+            }
+            uint32_t hi[4], lo[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+            {
+                hi[i] = M::bits(x[i]);
+                lo[i] = NEED_LO ? M::bits(x[i] - M::value(hi[i])) : 0u;
+            }
+            qthi = __builtin_bit_cast(X4, u32x2{hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16)});
+            qtlo = __builtin_bit_cast(X4, u32x2{lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16)});
+        }
 #pragma unroll
         for (int j = 0; j < KSTEPS; ++j)
         {
@@ -493,7 +541,7 @@ void paged_decode_mfma(DecodeArgs a)
 
     // Stage a loaded page: V rows into the wave's LDS tile, scores S^T = K Q^T into s.  Consumes r.k and r.v,
     // so the next page can be loaded into r right after.
-    auto stage_page = [&](int n_tok, const PageRegs<NW>& r, f32x4& s)
+    auto stage_page = [&](int n_tok, const PageRegs<NW, NWV>& r, f32x4& s)
     {
         if constexpr (kElemBytes<CT> == 2)
         {
@@ -504,19 +552,24 @@ void paged_decode_mfma(DecodeArgs a)
                 char*        kp = static_cast<char*>(const_cast<void*>(a.k_cache)) + row_n * D * 2;
                 char*        vp = static_cast<char*>(const_cast<void*>(a.v_cache)) + row_n * D * 2;
                 if (c == r.ns)
+                {
 #pragma unroll
                     for (int j = 0; j < KSTEPS; ++j) *reinterpret_cast<u32x4*>(kp + dim_of<CT>(j, g) * 2) = r.k[j];
+                    if constexpr (KT) *reinterpret_cast<u32x2*>(kp + (DT + 4 * g) * 2) = r.kt;
+                }
 #pragma unroll
-                for (int j = 0; j < NW; ++j)
+                for (int j = 0; j < NWV; ++j)
                     if (v_tok(j) == r.ns) *reinterpret_cast<u32x4*>(vp + 16 * v_chk(j)) = r.v[j];
             }
         }
-        // V rows into the LDS tile, zero for slots past the row's last token
+        // V rows into the LDS tile, zero for slots past the row's last token (chunks past the page's 16 rows:
+        // head_dim 80 and 112, and 8-bit 96, whose pages fill the last load instruction in part)
 #pragma unroll
-        for (int j = 0; j < NW; ++j)
+        for (int j = 0; j < NWV; ++j)
         {
             const int  t = v_tok(j);
             const bool tok_ok = t < n_tok;
+            if (t >= kBlockSize) continue;
             if constexpr (kElemBytes<CT> == 2)
             {
                 const u32x4 w = tok_ok ? r.v[j] : u32x4{0u, 0u, 0u, 0u};
@@ -526,7 +579,7 @@ void paged_decode_mfma(DecodeArgs a)
                 *reinterpret_cast<u32x4*>(sv + lds_pos<D>(t, 8 * v_chk(j))) = w;
 #endif
             }
-            else if (t < kBlockSize)  // 16 codes: dims 16 ch .. 16 ch + 15 as two 8-value words
+            else  // 16 codes: dims 16 ch .. 16 ch + 15 as two 8-value words
             {
                 const u32x4 lo = tok_ok ? codes_to_m<CT, VBF>(r.v[j][0], r.v[j][1]) : u32x4{0u, 0u, 0u, 0u};
                 const u32x4 hi = tok_ok ? codes_to_m<CT, VBF>(r.v[j][2], r.v[j][3]) : u32x4{0u, 0u, 0u, 0u};
@@ -546,6 +599,23 @@ void paged_decode_mfma(DecodeArgs a)
             const X8 kj = __builtin_bit_cast(X8, mword.template operator()<BF>(r.k, j));
             s = M::mma32(kj, qhi[j], s);
             if constexpr (NEED_LO) s = M::mma32(kj, qlo[j], s);
+        }
+        if constexpr (KT)  // the last 16 dims: 4 per lane
+        {
+            u32x2 w = r.kt;
+            if constexpr (kElemBytes<CT> == 1)
+            {
+                const u32x4 m = codes_to_m<CT, BF>(r.kt[0], 0u);
+                w = u32x2{m[0], m[1]};
+            }
+            // Its products accumulate apart and join the scores by vector adds: a 16x16x16 product that takes the
+            // 16x16x32 chain's result as its accumulator input got no wait states between them from this compiler
+            // (gfx950), and read the accumulator before the chain had written it (the scores of head_dim 80 and 112
+            // lost their first 64 or 96 dims on the GPU).
+            const X4 kt = __builtin_bit_cast(X4, w);
+            f32x4    st = M::mma16(kt, qthi, f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+            if constexpr (NEED_LO) st = M::mma16(kt, qtlo, st);
+            s += st;
         }
     };
 
@@ -689,14 +759,14 @@ void paged_decode_mfma(DecodeArgs a)
     int seg_start = start;
 #pragma unroll
     for (int n = 0; n < NT; ++n) acc[n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    PageRegs<NW> r[DEPTH];
+    PageRegs<NW, NWV> r[DEPTH];
 #pragma unroll
     for (int sl = 0; sl < DEPTH; ++sl)
         if (start + sl < end) load_next(r[sl]);
 
     auto step = [&]<int S>(int p)
     {
-        PageRegs<NW>& cur = r[S];
+        PageRegs<NW, NWV>& cur = r[S];
         const int     b = cur.b, pb = cur.pb, nb = cur.nb;
         const float   tks = cur.ks, tvs = cur.vs;
         const bool    ok = cur.ok;
@@ -944,8 +1014,12 @@ int items_m2(const DecodeArgs& a)
     {
         case 64:
             return items_m3<CT, QT, 64>(a);
+        case 80:
+            return items_m3<CT, QT, 80>(a);
         case 96:
             return items_m3<CT, QT, 96>(a);
+        case 112:
+            return items_m3<CT, QT, 112>(a);
         case 128:
             return items_m3<CT, QT, 128>(a);
         default:
@@ -974,8 +1048,12 @@ hipError_t launch_m2(const DecodeArgs& a, hipStream_t stream)
     {
         case 64:
             return launch_m3<CT, QT, 64>(a, stream);
+        case 80:
+            return launch_m3<CT, QT, 80>(a, stream);
         case 96:
             return launch_m3<CT, QT, 96>(a, stream);
+        case 112:
+            return launch_m3<CT, QT, 112>(a, stream);
         case 128:
             return launch_m3<CT, QT, 128>(a, stream);
         default:

@@ -92,7 +92,7 @@ def test_invalid_page_under_new_token(ff, gpu):
 
 
 @pytest.mark.parametrize("D,G", [(64, 1), (64, 8), (256, 4), (128, 16), (128, 7), (128, 32), (64, 20), (96, 4),
-                                 (40, 8)])
+                                 (40, 8), (80, 4), (112, 7), (112, 20)])
 def test_head_shapes(ff, gpu, D, G):
     rng = np.random.default_rng(74 + D + G)
     c = cases.make_case(74 + D + G, 9, 2 * G, 2, D, rng.integers(0, 700, size=9), act="bf16")

@@ -102,15 +102,16 @@ def test_head_dim_256_dtypes(ff, gpu, act, kv):
     _check(ff, gpu, c, 2e-3 if kv in ("f16", "bf16") else 2e-2)
 
 
-@pytest.mark.parametrize("D", [8, 40, 96, 112])
+@pytest.mark.parametrize("D", [8, 40, 80, 96, 112])
 @pytest.mark.parametrize("act,kv", [("bf16", "bf16"), ("f16", "f16"), ("f32", "f32"), ("bf16", "i8"),
                                     ("bf16", "fp8"), ("f32", "fp8"), ("f16", "i8"), ("f16", "fp8")])
 def test_head_dims_multiple_of_8(ff, gpu, D, act, kv):
     """Any head_dim that is a multiple of 8 up to 128, as the reference's decode takes (one 8-element vector per
     lane of a 16-lane group, src/kernels/attention.cu:307-316) and its append (any head_dim up to 128,
     src/model/qwen_model.cu:21-47): pages and int8 scales bit-exact, outputs within the bar.  head_dim 96 runs on
-    the matrix cores (three k-steps of 32 dims; 8-bit codes read the odd last k-step's 8 codes alone), the others
-    on the vector kernel with 16 lanes per token, those past head_dim / 8 idle."""
+    the matrix cores (three k-steps of 32 dims; 8-bit codes read the odd last k-step's 8 codes alone), and so do
+    80 and 112 (k-steps of 32 dims and a last one of 16, 4 dims per lane), the others on the vector kernel with 16
+    lanes per token, those past head_dim / 8 idle."""
     rng = np.random.default_rng(D * 7 + len(act) + len(kv))
     ctx = rng.integers(0, 600, size=5)
     c = cases.make_case(80 + D, 5, 16, 4, D, ctx, act=act, kv=kv, input_scale=1 / math.sqrt(D))
@@ -129,7 +130,8 @@ def test_head_dim_96_multi_token_append(ff, gpu, kv):
                                              (32, 2, 128, "bf16", "i8"), (20, 1, 256, "f32", "bf16"),
                                              (20, 2, 96, "bf16", "bf16"), (40, 1, 96, "f16", "f16"),
                                              (20, 2, 96, "bf16", "i8"), (20, 2, 96, "bf16", "fp8"),
-                                             (24, 1, 96, "f16", "i8")])
+                                             (24, 1, 96, "f16", "i8"), (20, 2, 112, "bf16", "bf16"),
+                                             (24, 1, 80, "f16", "i8"), (18, 2, 112, "f32", "fp8")])
 def test_groups_over_16(ff, gpu, G, Hkv, D, act, kv):
     """GQA groups above 16 query heads per KV head (MQA-style): one wave per block of 16 heads of the group."""
     rng = np.random.default_rng(G * 10 + Hkv)

@@ -216,11 +216,13 @@ def test_workspace_with_garbage_reused(ff, gpu):
         _check(got, ref, c.act, 2e-3, f"call {i}")
 
 
-def test_head_dim_96_takes_the_plain_decode(ff, gpu):
-    """head_dim 96 has no matrix-core kernels: the shared-prefix entry point runs the plain decode, same results."""
-    rng = np.random.default_rng(96)
+@pytest.mark.parametrize("D", [80, 96, 112])
+def test_head_dims_without_prefix_kernel_take_the_plain_decode(ff, gpu, D):
+    """head_dim 80, 96 and 112 have no prefix-partial (prefill) kernel: the shared-prefix entry point runs the
+    plain decode, same results."""
+    rng = np.random.default_rng(D)
     ctx = 8 * 16 + rng.integers(1, 200, size=10) - 1
-    c = cases.make_case(96, 10, 16, 4, 96, ctx, act="bf16", shared_prefix_blocks=8)
+    c = cases.make_case(D, 10, 16, 4, D, ctx, act="bf16", shared_prefix_blocks=8)
     _both(ff, gpu, c, 8)
 
 
