@@ -111,9 +111,9 @@ FFKV_API size_t ffkv_decode_workspace_bytes(int batch, int num_heads, int head_d
  *
  * qo_dtype (q and out) is F32, F16 or BF16; cache_dtype as for ffkv_append.  scale <= 0 selects
  * 1/sqrt(head_dim) (src/kernels/attention.cu:458).  num_heads must be a multiple of num_kv_heads (any group
- * size for 16- and 8-bit caches at head_dim 64, 96, 128 and 256, at most 16 otherwise)
+ * size for 16- and 8-bit caches at head_dim 64, 80, 96, 112, 128 and 256, at most 16 otherwise)
  * and at most 65535; head_dim a multiple of 8 up to 128 (as the reference's decode,
- * src/kernels/attention.cu:307-316), or 256: 64, 96, 128 and 256 run the matrix-core kernels, the others a
+ * src/kernels/attention.cu:307-316), or 256: 64, 80, 96, 112, 128 and 256 run the matrix-core kernels, the others a
  * vector kernel; q, out, cache and workspace pointers 16-byte aligned.  Rows are
  * split over the context and the pieces merged; the partials live in `workspace` (ffkv_decode_workspace_bytes;
  * any initial contents), or, when workspace is NULL, in stream-ordered memory the library allocates and frees on
