@@ -491,7 +491,17 @@ int decode_impl(const void* q, void* out, int qo_dtype, const void* k_cache, con
     a.num_kv_heads = num_kv_heads;
     a.group = group;
     a.head_dim = head_dim;
-    a.items = mfma ? ffkv::decode_mfma_launch_items(a) : 0;
+    // shared prefix on 16-bit pages at head_dim 128: the prefix partials run inside the decode's grid
+    ffkv::DecodePfxPlan plan{};
+    const bool          fused_pfx = skip > 0 && ffkv::decode_pfx_plan(a, skip, pfx_chunks, plan);
+    if (fused_pfx)
+    {
+        pfx_chunks = plan.chunks;
+        pfx_chunk_pages = plan.chunk_pages;
+        a.pfx_items = plan.pfx_items;
+        a.pfx_share = plan.pfx_share;
+    }
+    a.items = fused_pfx ? plan.items : (mfma ? ffkv::decode_mfma_launch_items(a) : 0);
 
     // workspace layout: MFMA kernel see mfma_layout, generic kernel [ml | acc] (none for single-chunk rows)
     ffkv::MfmaLayout lay{};
@@ -560,13 +570,13 @@ int decode_impl(const void* q, void* out, int qo_dtype, const void* k_cache, con
     a.chunk = chunk;
     a.max_chunks = max_chunks;
     a.scale_log2 = sm_scale * 1.4426950408889634f;
-    hipError_t e = hipSuccess;
+    hipError_t        e = hipSuccess;
+    ffkv::PrefillArgs p{};
     if (skip > 0)
     {
         a.skip_blocks = skip;
         a.pfx_chunks = pfx_chunks;
         a.pfx_slot0 = a.items + batch;
-        ffkv::PrefillArgs p{};
         p.q = q;
         p.k_cache = k_cache;
         p.v_cache = v_cache;
@@ -593,7 +603,7 @@ int decode_impl(const void* q, void* out, int qo_dtype, const void* k_cache, con
         p.pfx_slot0 = a.pfx_slot0;
         p.ws_ml = a.ws_ml;
         p.ws_acc = a.ws_acc;
-        e = ffkv::launch_prefix_partials(p, s);
+        if (!fused_pfx) e = ffkv::launch_prefix_partials(p, s);
     }
     if (k_new != nullptr && e == hipSuccess)
     {
@@ -611,7 +621,9 @@ int decode_impl(const void* q, void* out, int qo_dtype, const void* k_cache, con
             e = ffkv::launch_append(ap, s);
         }
     }
-    if (e == hipSuccess) e = mfma ? ffkv::launch_decode_mfma(a, s) : ffkv::launch_decode(a, s);
+    if (e == hipSuccess)
+        e = fused_pfx ? ffkv::launch_decode_pfx(a, p, plan.gy, s)
+                      : (mfma ? ffkv::launch_decode_mfma(a, s) : ffkv::launch_decode(a, s));
     if (owned)
     {
         hipError_t fe = hipFreeAsync(ws, s);

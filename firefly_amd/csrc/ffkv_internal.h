@@ -122,6 +122,10 @@ struct DecodeArgs
     int            skip_blocks;
     int            pfx_chunks;
     int            pfx_slot0;
+    // Fused shared-prefix launch (launch_decode_pfx): work items 0 .. pfx_items - 1 compute prefix partials first,
+    // and their share of the rows' own pages is pfx_share / 1024 of another item's.  0 elsewhere.
+    int            pfx_items;
+    int            pfx_share;
     // Fused append (16-bit caches, k/v in the cache dtype): [batch, 1, num_kv_heads, head_dim]; the item holding a
     // row's last page takes the new token from here and writes it to its page slot (the first wave copies the
     // tokens of rows cut short by cap_tokens).
@@ -144,6 +148,23 @@ int decode_mfma_items(const void* kernel, int threads, int grid_y);
 // decode_mfma_items for the kernel instance launch_decode_mfma selects for `a` (its dtypes, head_dim and heads).
 int decode_mfma_launch_items(const DecodeArgs& a);
 bool decode_use_mfma(int cache_dtype, int group, int head_dim);
+
+// Fused shared-prefix decode (paged_decode_pfx.hip): the prefix partials and the decode of the rows' own pages in
+// one grid, then the merge.  decode_pfx_plan sizes it for `a` (dtypes, batch, heads, head_dim set) over
+// `shared_pages` shared pages in at most `max_chunks` chunks, or returns false when the fused kernel does not take
+// these dtypes / head_dim / heads (then the prefix kernel and the decode launch one after the other).
+struct DecodePfxPlan
+{
+    int items;        // decode work items (grid x)
+    int gy;           // head groups (grid y)
+    int chunks;       // prefix chunks
+    int chunk_pages;  // pages per prefix chunk
+    int pfx_items;    // items that compute a prefix task first
+    int pfx_share;    // their page share, per 1024 of another item's
+};
+constexpr int kPfxDefaultShare = 512;
+bool       decode_pfx_plan(const DecodeArgs& a, int shared_pages, int max_chunks, DecodePfxPlan& plan);
+hipError_t launch_decode_pfx(const DecodeArgs& a, const PrefillArgs& p, int gy, hipStream_t stream);
 size_t decode_mfma_workspace_bytes(int batch, int num_heads, int head_dim);  // upper bound (kMfmaMaxItems items)
 
 // Split-K geometry shared by the workspace query and the launcher.

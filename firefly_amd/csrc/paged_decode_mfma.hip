@@ -93,7 +93,7 @@ struct PageRegs
 #define FFKV_MFMA_WAVES128_FP8 (FFKV_MFMA_DEPTH_FP8 > 1 ? 2 : 3)
 #endif
 #ifndef FFKV_MFMA_WAVES128_I8
-#define FFKV_MFMA_WAVES128_I8 2
+#define FFKV_MFMA_WAVES128_I8 3
 #endif
 
 #ifndef FFKV_MFMA_DEPTH256
@@ -162,11 +162,16 @@ constexpr int kMfmaMaxWaves =
     ((D == 80 || D == 96 || D == 112) && kElemBytes<CT> == 2) || (CT == FP8 && D == 128) ? FFKV_MFMA_MAX_WAVES_WIDE
                                                                                           : FFKV_MFMA_MAX_WAVES;
 
-// Work item i (blockIdx.x) of W (gridDim.x); KV heads blockIdx.y*NW .. +NW, one per wave.
-template <int CT, int QT, int D>
-__global__ __launch_bounds__((64 * kMfmaMaxWaves<CT, D>)) __attribute__((amdgpu_waves_per_eu(kMfmaWaves<CT, QT, D>, 8)))
-void paged_decode_mfma(DecodeArgs a)
+// One workgroup of a decode launch: work item `item` of `n_items`, KV heads y*nw .. +nw (one per wave; nw waves
+// in the workgroup).  s_v: the workgroup's V tiles in LDS, [nw][16 * D] 16-bit elements.  PW: the page split may
+// weigh the first pfx_items items less (the fused shared-prefix launch); the plain decode's split otherwise.
+template <int CT, int QT, int D, bool PW = false>
+__device__ __forceinline__ void decode_wg(const DecodeArgs& a, int item_, int y_, int n_items_, int nw_, uint16_t* s_v)
 {
+    // (the plain decode reads its indices where it uses them: held in registers from the start, they cost the
+    // kernel scalar registers it spills)
+    auto item_of = [&]() { return PW ? item_ : static_cast<int>(blockIdx.x); };
+    auto y_of = [&]() { return PW ? y_ : static_cast<int>(blockIdx.y); };
     // Score products in M (BF: bf16, else f16); PV products in MV.  8-bit codes are exact in both types, so their
     // PV products take f16, where P fits one product (11 bits) instead of a bf16 hi + lo pair; bf16 caches keep
     // bf16 P as hi + lo.  (int8 scores stay f16 with q split in two: bf16 scores, q whole, measured 20 % slower
@@ -196,14 +201,12 @@ void paged_decode_mfma(DecodeArgs a)
         return dim_of<CT>(j, g);
     };
 
-    __shared__ uint16_t s_v[kMfmaMaxWaves<CT, D>][kBlockSize * D];
-
     const int  lane = threadIdx.x & 63;
     const int  wave = threadIdx.x >> 6;
     const int  c = lane & 15;  // MFMA column / row-in-tile index
     const int  g = lane >> 4;  // lane group
     const int  B = a.batch;
-    const bool first_wg = blockIdx.x == 0 && blockIdx.y == 0 && wave == 0;
+    const bool first_wg = item_of() == 0 && y_of() == 0 && wave == 0;
 
     // ---- rows in windows of 64, one row per lane --------------------------------------------------------------
     // A window holds rows w0 .. w0 + 63: lane l has row w0 + l's attended tokens, pages and first page (relative to
@@ -286,21 +289,39 @@ void paged_decode_mfma(DecodeArgs a)
         if (w.w0 + 64 >= B) break;
         w = load_win(w.w0 + 64, P);
     }
-    const int W = min(static_cast<int>(gridDim.x), P);
-    const int item = blockIdx.x;
+    // Work item i of W takes pages [i * P / W, (i + 1) * P / W), W = min(items, P) so that every item has a page.
+    // PW (fused shared-prefix launch): the first pfx_items items also compute prefix partials, so each of them
+    // weighs pfx_share / 1024 of another item: pages [P * cum(i) / T, P * cum(i + 1) / T) with cum(i) = 1024 i -
+    // min(i, pfx_items) (1024 - pfx_share) and T = cum(items), as long as that still leaves every item a page.
+    const int     item = item_of();
+    const int     n_items = PW ? n_items_ : static_cast<int>(gridDim.x);
+    const int64_t uh = a.pfx_share, up = 1024, H = a.pfx_items;
+    const int64_t T_w = H * uh + (n_items - H) * up;
+    const bool    weighted = PW && H > 0 && static_cast<int64_t>(P) * min(uh, up) >= T_w;
+    const int     W = weighted ? n_items : min(n_items, P);
     if (item >= W) return;
-    const int start = static_cast<int>(static_cast<int64_t>(item) * P / W);
-    const int end = static_cast<int>(static_cast<int64_t>(item + 1) * P / W);
+    auto cum = [&](int64_t i) { return i * up - min(i, H) * (up - uh); };
+    const int start = weighted ? static_cast<int>(static_cast<int64_t>(P) * cum(item) / T_w)
+                               : static_cast<int>(static_cast<int64_t>(item) * P / W);
+    const int end = weighted ? static_cast<int>(static_cast<int64_t>(P) * cum(item + 1) / T_w)
+                             : static_cast<int>(static_cast<int64_t>(item + 1) * P / W);
+    // largest item i with start(i) <= x
+    auto last_item = [&](int64_t x) -> int
+    {
+        if (!weighted) return static_cast<int>(((x + 1) * W + P - 1) / P - 1);  // largest i with i*P/W <= x
+        const int64_t K = ((x + 1) * T_w + P - 1) / P - 1;                      // cum(i) <= K
+        return static_cast<int>(K < H * uh ? K / uh : H + (K - H * uh) / up);
+    };
 
     // wave -> (KV head, block of 16 of its query heads): heads kvh * G + h0 + c for c < gc
     const int G = a.group;
     const int HB = (G + 15) >> 4;
-    const int vh = blockIdx.y * (static_cast<int>(blockDim.x) >> 6) + wave;
+    const int vh = y_of() * (PW ? nw_ : static_cast<int>(blockDim.x) >> 6) + wave;
     if (vh >= a.num_kv_heads * HB) return;
     const int kvh = vh / HB;
     const int h0 = (vh - kvh * HB) * 16;
     const int gc = min(16, G - h0);  // heads of this block
-    uint16_t* sv = s_v[wave];
+    uint16_t* sv = s_v + wave * (kBlockSize * D);
 
     float kv_scale_log2 = a.scale_log2;
     float v_head_scale = 1.0f;
@@ -743,12 +764,10 @@ void paged_decode_mfma(DecodeArgs a)
             }
         }
         // the item holding a row's first page records which items cover the row
-        if (seg_start == pb && blockIdx.y == 0 && wave == 0 && lane == 0)
+        if (seg_start == pb && y_of() == 0 && wave == 0 && lane == 0)
         {
-            const int64_t last = pb + nb - 1;
-            const int64_t i_hi = ((last + 1) * W + P - 1) / P - 1;  // largest i with i*P/W <= last
             a.ws_meta[2 * b] = item;
-            a.ws_meta[2 * b + 1] = static_cast<int32_t>(i_hi);
+            a.ws_meta[2 * b + 1] = last_item(pb + nb - 1);
         }
     };
 
@@ -800,6 +819,16 @@ void paged_decode_mfma(DecodeArgs a)
         if constexpr (DEPTH > 2)
             if (p + 2 < end) step.template operator()<2 % DEPTH>(p + 2);
     }
+}
+
+// Work item blockIdx.x of gridDim.x; KV heads blockIdx.y * NW .. +NW, one per wave (NW = blockDim.x / 64).
+template <int CT, int QT, int D>
+__global__ __launch_bounds__((64 * kMfmaMaxWaves<CT, D>)) __attribute__((amdgpu_waves_per_eu(kMfmaWaves<CT, QT, D>, 8)))
+void paged_decode_mfma(DecodeArgs a)
+{
+    __shared__ uint16_t s_v[kMfmaMaxWaves<CT, D> * kBlockSize * D];
+    decode_wg<CT, QT, D>(a, static_cast<int>(blockIdx.x), static_cast<int>(blockIdx.y), static_cast<int>(gridDim.x),
+                         static_cast<int>(blockDim.x) >> 6, s_v);
 }
 
 // Combine the partials of rows split over several work items.
@@ -983,17 +1012,10 @@ int items_m3(const DecodeArgs& a)
     return decode_mfma_items(reinterpret_cast<const void*>(paged_decode_mfma<CT, QT, D>), 64 * sh.nw, sh.gy);
 }
 
-template <int CT, int QT, int D>
-hipError_t launch_m3(const DecodeArgs& a, hipStream_t stream)
+// The merge after a decode launch (rows split over several items, or shared-prefix partials).
+template <int QT, int D>
+hipError_t launch_merge(const DecodeArgs& a, hipStream_t stream)
 {
-    const MfmaShape sh = mfma_shape<CT, D>(a);
-    const int       nw = sh.nw, gy = sh.gy;
-    const auto      kern = paged_decode_mfma<CT, QT, D>;
-    // the workspace holds items + batch partial slots
-    const int items = a.items > 0 ? a.items : items_m3<CT, QT, D>(a);
-    hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(items), static_cast<unsigned>(gy)), dim3(64 * nw), 0, stream, a);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
     if (a.batch <= FFKV_MERGE_ROWS_MIN_BATCH)  // few rows over the same items: tens of pieces per row
     {
         const dim3 mgrid(static_cast<unsigned>(a.batch), static_cast<unsigned>(a.num_heads));
@@ -1005,6 +1027,20 @@ hipError_t launch_m3(const DecodeArgs& a, hipStream_t stream)
         hipLaunchKernelGGL((paged_decode_mfma_merge_rows<QT, D>), mgrid, dim3(256), 0, stream, a);
     }
     return hipGetLastError();
+}
+
+template <int CT, int QT, int D>
+hipError_t launch_m3(const DecodeArgs& a, hipStream_t stream)
+{
+    const MfmaShape sh = mfma_shape<CT, D>(a);
+    const int       nw = sh.nw, gy = sh.gy;
+    const auto      kern = paged_decode_mfma<CT, QT, D>;
+    // the workspace holds items + batch partial slots
+    const int items = a.items > 0 ? a.items : items_m3<CT, QT, D>(a);
+    hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(items), static_cast<unsigned>(gy)), dim3(64 * nw), 0, stream, a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    return launch_merge<QT, D>(a, stream);
 }
 
 template <int CT, int QT>
@@ -1077,6 +1113,8 @@ hipError_t launch_m1(const DecodeArgs& a, hipStream_t stream)
 
 }  // namespace
 
+#ifndef FFKV_DEVICE_BODIES_ONLY
+
 int decode_mfma_launch_items(const DecodeArgs& a)
 {
     switch (a.cache_dtype)
@@ -1106,5 +1144,7 @@ hipError_t launch_decode_mfma(const DecodeArgs& a, hipStream_t stream)
             return launch_m1<FP8>(a, stream);
     }
 }
+
+#endif  // FFKV_DEVICE_BODIES_ONLY
 
 }  // namespace ffkv

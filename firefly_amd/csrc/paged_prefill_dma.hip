@@ -258,10 +258,27 @@ __device__ __forceinline__ void wait_vm()
 // instead of 8 waves of 16, two waves per SIMD).
 // Register budget: 256 at two row groups (two waves per SIMD); one row group at head_dim <= 128 takes 128 (four waves
 // per SIMD), or 168 for int8 codes, whose scales and conversions would spill at 128.
+// LDS of one workgroup: kDmaStages<D> stages, each [K tile | V tile | int8 scales] of KP pages, key-major, swizzled
+// chunks (stages past kDmaStages<D> take 16 bytes).
 template <int QT, int D, int CT, bool PFX, int RG>
-__global__ __launch_bounds__(512 / RG)
-__attribute__((amdgpu_waves_per_eu(RG == 2 ? 2 : (D <= 128 ? (CT == I8 ? 3 : 4) : 1))))
-void paged_prefill_dma(PrefillArgs a)
+struct PrefillLds
+{
+    static constexpr bool C16 = FFKV_PREFILL_C16 && CT == I8 && !(FFKV_PREFILL_I8_BF && QT != F16) && D <= 128;
+    using C = DmaCfg<D, C16 ? 2 : kElemBytes<CT>, CT == I8, 8 / RG, PFX>;
+    static constexpr int STAGE = 2 * C::TILEB + C::SCB;
+    static constexpr int S2 = kDmaStages<D> >= 3 ? STAGE : 16;
+    static constexpr int S3 = kDmaStages<D> == 4 ? STAGE : 16;
+    static constexpr int BYTES = 2 * STAGE + S2 + S3;  // the four in a row
+};
+
+// One workgroup's share of a prefill (or of the shared-prefix partials): `wg_index` is its index in the launch grid
+// (blockIdx.x for paged_prefill_dma), s_st0 .. s_st3 its LDS stages (16-byte aligned, PrefillLds<...>::STAGE, S2 and
+// S3 bytes) and `s_vover` an int in LDS.  Every wave of the workgroup calls it; it leaves no load in flight into
+// the stages.  (paged_prefill_dma gives each stage an LDS array of its own, which tells the compiler that they
+// do not overlap.)
+template <int QT, int D, int CT, bool PFX, int RG>
+__device__ __forceinline__ void prefill_wg(PrefillArgs a, int wg_index, uint8_t* s_st0, uint8_t* s_st1,
+                                           uint8_t* s_st2, uint8_t* s_st3, int& s_vover)
 {
     constexpr int  W = 8 / RG;  // waves per workgroup
     constexpr int  EB = kElemBytes<CT>;
@@ -303,13 +320,8 @@ void paged_prefill_dma(PrefillArgs a)
     // per p.  int8's P carries the keys' V scales, so its denominator sums p itself, as do bf16's hi + lo pairs.
     constexpr bool L_DOT = !(BF && !V16) && CT != I8;
 
-    // kDmaStages<D> stages, each [K tile | V tile | int8 scales] of KP pages, key-major, swizzled chunks
-    __shared__ __align__(16) uint8_t s_st0[2 * C::TILEB + C::SCB];
-    __shared__ __align__(16) uint8_t s_st1[2 * C::TILEB + C::SCB];
-    __shared__ __align__(16) uint8_t s_st2[kDmaStages<D> >= 3 ? 2 * C::TILEB + C::SCB : 16];
-    __shared__ __align__(16) uint8_t s_st3[kDmaStages<D> == 4 ? 2 * C::TILEB + C::SCB : 16];
-
-    __shared__ int s_vover;  // some accumulator is not finite after the f16 PV products (bf16 and int8 pages)
+    static_assert(PrefillLds<QT, D, CT, PFX, RG>::STAGE == 2 * C::TILEB + C::SCB, "stage layout");
+    // s_vover: some accumulator is not finite after the f16 PV products (bf16 and int8 pages)
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -330,7 +342,7 @@ void paged_prefill_dma(PrefillArgs a)
     const int nrb = (R + kDmaRows - 1) / kDmaRows;
     const int groups = PFX ? Hkv * a.pfx_chunks : a.batch * Hkv;
 #if FFKV_PREFILL_XCD
-    const int wg = blockIdx.x;
+    const int wg = wg_index;
     const int xcd = wg % kXcds;
     const int k_in_xcd = wg / kXcds;
     const int rb = nrb - 1 - k_in_xcd % nrb;
@@ -353,8 +365,8 @@ void paged_prefill_dma(PrefillArgs a)
     }
     if (grp >= groups) return;  // padding of the grid to whole rounds of XCDs
 #else
-    const int grp = blockIdx.x / nrb;
-    const int rb = blockIdx.x % nrb;
+    const int grp = wg_index / nrb;
+    const int rb = wg_index % nrb;
 #endif
     const int b = PFX ? 0 : grp / Hkv;                 // prefill: the workgroup's row
     const int kvh = PFX ? grp / a.pfx_chunks : grp % Hkv;
@@ -1190,6 +1202,22 @@ void paged_prefill_dma(PrefillArgs a)
     }
 }
 
+template <int QT, int D, int CT, bool PFX, int RG>
+__global__ __launch_bounds__(512 / RG)
+__attribute__((amdgpu_waves_per_eu(RG == 2 ? 2 : (D <= 128 ? (CT == I8 ? 3 : 4) : 1))))
+void paged_prefill_dma(PrefillArgs a)
+{
+    using L = PrefillLds<QT, D, CT, PFX, RG>;
+    __shared__ __align__(16) uint8_t s_st0[L::STAGE];
+    __shared__ __align__(16) uint8_t s_st1[L::STAGE];
+    __shared__ __align__(16) uint8_t s_st2[L::S2];
+    __shared__ __align__(16) uint8_t s_st3[L::S3];
+    __shared__ int s_vover;
+    prefill_wg<QT, D, CT, PFX, RG>(a, static_cast<int>(blockIdx.x), s_st0, s_st1, s_st2, s_st3, s_vover);
+}
+
+#ifndef FFKV_DEVICE_BODIES_ONLY
+
 namespace
 {
 
@@ -1264,5 +1292,7 @@ hipError_t launch_pfd(const PrefillArgs& a, hipStream_t stream)
 hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream) { return launch_pfd<false>(a, stream); }
 
 hipError_t launch_prefix_partials(const PrefillArgs& a, hipStream_t stream) { return launch_pfd<true>(a, stream); }
+
+#endif  // FFKV_DEVICE_BODIES_ONLY
 
 }  // namespace ffkv

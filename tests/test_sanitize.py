@@ -44,8 +44,8 @@ def test_scheduler_radix_allocator_under_asan_ubsan(tmp_path):
 def test_c_abi_validation_under_asan_ubsan(tmp_path):
     gxx, hipcc = shutil.which("g++"), "/opt/rocm/bin/hipcc"
     build = ROOT / "firefly_amd" / "_build"
-    kernels = [build / f"{n}.hip.o" for n in ("kv_append", "paged_decode", "paged_decode_mfma", "paged_prefill_dma",
-                                               "rope_append")]
+    kernels = [build / f"{n}.hip.o" for n in ("kv_append", "paged_decode", "paged_decode_mfma", "paged_decode_pfx",
+                                               "paged_prefill_dma", "rope_append")]
     if gxx is None or not Path(hipcc).exists() or not all(k.exists() for k in kernels):
         pytest.skip("needs g++, hipcc and the library's objects (python firefly_amd/build.py)")
     inc = [f"-I{ROOT / 'include'}", f"-I{ROOT / 'firefly_amd' / 'csrc'}"]
