@@ -106,11 +106,16 @@ constexpr int kMfmaDepth =
     D == 256 ? FFKV_MFMA_DEPTH256
              : (kElemBytes<CT> == 2 ? FFKV_MFMA_DEPTH16 : (CT == FP8 ? FFKV_MFMA_DEPTH_FP8 : FFKV_MFMA_DEPTH_I8));
 
+#ifndef FFKV_MFMA_WAVES80
+#define FFKV_MFMA_WAVES80 2  // head_dim 80 with q in the cache's type (three waves' 168 registers spill)
+#endif
+
 // Waves per SIMD the register budget is sized for (168 registers at 3, 128 at 4, 256 at 2).
 template <int CT, int QT, int D>
 constexpr int kMfmaWaves =
     D == 256 || D == 112 ? 2
-    : D == 96 || D == 80 ? (QT == CT ? 3 : 2)  // a q of another type needs its lo part: three waves' registers would spill
+    : D == 96 ? (QT == CT ? 3 : 2)  // a q of another type needs its lo part: three waves' registers would spill
+    : D == 80 ? (QT == CT ? FFKV_MFMA_WAVES80 : 2)
              : (D == 128 ? (kElemBytes<CT> == 2 ? FFKV_MFMA_WAVES128_16
                                                 : (CT == FP8 ? FFKV_MFMA_WAVES128_FP8 : FFKV_MFMA_WAVES128_I8))
                          : (kMfmaDepth<CT, D> > 1 ? 3 : 4));
