@@ -93,7 +93,11 @@ constexpr int kXcds = 8;  // MI355X: workgroups are dealt to 8 XCDs (separate L2
 #endif
 
 #ifndef FFKV_PREFILL_RG
-#define FFKV_PREFILL_RG 2  // row groups of 16 query rows per wave at head_dim <= 128 (head_dim 256 takes 1)
+#define FFKV_PREFILL_RG 2  // row groups of 16 query rows per wave at head_dim <= 128
+#endif
+
+#ifndef FFKV_PREFILL_RG256
+#define FFKV_PREFILL_RG256 1  // the same at head_dim 256 (two take 512 registers, one wave per SIMD: 287 -> 908 us)
 #endif
 
 #ifndef FFKV_PREFILL_DMA_KP64
@@ -1204,7 +1208,7 @@ __device__ __forceinline__ void prefill_wg(PrefillArgs a, int wg_index, uint8_t*
 
 template <int QT, int D, int CT, bool PFX, int RG>
 __global__ __launch_bounds__(512 / RG)
-__attribute__((amdgpu_waves_per_eu(RG == 2 ? 2 : (D <= 128 ? (CT == I8 ? 3 : 4) : 1))))
+__attribute__((amdgpu_waves_per_eu(RG == 2 ? (D == 256 ? 1 : 2) : (D <= 128 ? (CT == I8 ? 3 : 4) : 1))))
 void paged_prefill_dma(PrefillArgs a)
 {
     using L = PrefillLds<QT, D, CT, PFX, RG>;
@@ -1248,8 +1252,11 @@ hipError_t launch_pfd_d(const PrefillArgs& a, hipStream_t stream)
             hipLaunchKernelGGL((paged_prefill_dma<QT, 128, CT, PFX, RG>), grid, dim3(512 / RG), 0, stream, a);
             break;
         default:
-            hipLaunchKernelGGL((paged_prefill_dma<QT, 256, CT, PFX, 1>), grid, dim3(512), 0, stream, a);
+        {
+            constexpr int RG256 = PFX ? 1 : FFKV_PREFILL_RG256;
+            hipLaunchKernelGGL((paged_prefill_dma<QT, 256, CT, PFX, RG256>), grid, dim3(512 / RG256), 0, stream, a);
             break;
+        }
     }
     return hipGetLastError();
 }
