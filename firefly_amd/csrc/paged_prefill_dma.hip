@@ -793,7 +793,10 @@ __device__ __forceinline__ void prefill_wg(PrefillArgs a, int wg_index, uint8_t*
             if constexpr (R8)
             {
                 const int   ka = u * kBlockSize * C::RB + k8base + (((2 * j + (g >> 1)) ^ k8sw) << 4);
-                const u32x2 w = *reinterpret_cast<const u32x2*>(stage + ka);
+                // volatile: the compiler would pair the reads of pages u and u + 1 (2 KiB apart) into one
+                // ds_read2st64_b64, whose two halves land on the same banks (one LDS conflict cycle per product,
+                // measured; separate reads count none)
+                const u32x2 w = *(const volatile FFKV_LDS u32x2*)(stage + ka);
                 return __builtin_bit_cast(X8, codes_to_m<CT, BF>(w[0], w[1]));
             }
             else
