@@ -18,7 +18,9 @@ Printed JSON line (rank 0, N = 1):
   parity         max-abs error of the layer-0 GPU output against that CPU result (fp32, before rounding)
   device_copy    a 1 GiB torch device copy timed the same way: the streaming rate a plain kernel reaches here
   read_stream    a read-only 2 GiB stream (firefly_amd/libffkv_bench.so) over a few launch shapes: the practical
-                 read ceiling for the read-dominated decode; decode_kernel_vs_read_stream = roofline.achieved over it
+                 read ceiling for the read-dominated decode; decode_call_vs_read_stream = roofline.achieved over it;
+                 at_call_size: the best shape over buffers of one decode call's bytes (start and tail included),
+                 decode_call_vs_read_at_call_size = roofline.achieved over that
   other_configs  C3, C4 and C5 (int8 and fp8 pools filled by the quantizing append, whose bulk throughput is
                  reported as quantized_append), the C4 prefill on every cache type and head_dim, a head_dim 256
                  decode, the fused rope + append, and the decode step's host upload
@@ -100,10 +102,13 @@ def device_copy_rate(torch, dev, stream, nbytes: int = 1 << 30) -> dict:
             "pct_of_peak": 2 * nbytes / (us * 1e-6) / 1e12 / HBM_PEAK_TBS * 100}
 
 
-def read_stream_rate(torch, dev, stream, nbytes: int = 2 << 30) -> dict | None:
+def read_stream_rate(torch, dev, stream, nbytes: int = 2 << 30, call_bytes: int | None = None) -> dict | None:
     """A read-only stream over 2 GiB (firefly_amd/libffkv_bench.so: 16-byte loads, 4 or 8 in flight per lane, one
     word written per workgroup), timed with HIP events for a few launch shapes: the practical read ceiling of this
-    GPU for a read-dominated kernel such as the decode.  The best shape is `TB_per_s`; every shape is listed."""
+    GPU for a read-dominated kernel such as the decode.  The best shape is `TB_per_s`; every shape is listed.
+    With call_bytes, the best shape also reads buffers of that size (four, in turn, so that the 256 MB on-chip
+    cache cannot hold them, as the decode rotates its layer pools): `at_call_size`, the ceiling for a launch that
+    reads as much as one decode call, start and tail included."""
     import ctypes
 
     path = ROOT / "firefly_amd" / "libffkv_bench.so"
@@ -123,11 +128,28 @@ def read_stream_rate(torch, dev, stream, nbytes: int = 2 << 30) -> dict | None:
                 assert rc == 0
             us = _events_us(call, 20, stream)
             shapes[f"{blocks}x256_unroll{unroll}"] = {"us": us, "TB_per_s": nbytes / (us * 1e-6) / 1e12}
-    del src, sink
+    del src
     torch.cuda.empty_cache()
     best = max(shapes, key=lambda k: shapes[k]["TB_per_s"])
+    at_call = None
+    if call_bytes is not None and call_bytes >= 16:
+        nb = call_bytes // 16 * 16
+        blocks = int(best.split("x")[0])
+        unroll = int(best.rsplit("unroll", 1)[1])
+        bufs = [torch.ones(nb, dtype=torch.uint8, device=dev) for _ in range(4)]
+
+        def call(i):
+            rc = lib.ffkv_bench_stream_read(bufs[i % 4].data_ptr(), nb, sink.data_ptr(), blocks, unroll,
+                                            stream.cuda_stream)
+            assert rc == 0
+        us = _events_us(call, 20, stream)
+        at_call = {"bytes_read": nb, "buffers": 4, "shape": best, "us": us, "TB_per_s": nb / (us * 1e-6) / 1e12}
+        del bufs
+    del sink
+    torch.cuda.empty_cache()
     return {"bytes_read": nbytes, "best_shape": best, "TB_per_s": shapes[best]["TB_per_s"],
-            "pct_of_peak": shapes[best]["TB_per_s"] / HBM_PEAK_TBS * 100, "shapes": shapes}
+            "pct_of_peak": shapes[best]["TB_per_s"] / HBM_PEAK_TBS * 100, "shapes": shapes,
+            "at_call_size": at_call}
 
 
 BF16_MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense bf16
@@ -783,7 +805,7 @@ def main(argv=None) -> int:
         configs = {name: makers[name]() for name in want}
 
     copy_rate = None if args.skip_c2 else device_copy_rate(torch, dev, stream)
-    read_rate = None if args.skip_c2 else read_stream_rate(torch, dev, stream)
+    read_rate = None if args.skip_c2 else read_stream_rate(torch, dev, stream, call_bytes=dbytes)
 
     # Layer-0 output for the parity figure and the CPU baseline on the same inputs.
     kp0, vp0 = pools[0]
@@ -829,8 +851,11 @@ def main(argv=None) -> int:
                      "algorithmic_bytes": dbytes},
         "device_copy": copy_rate,
         "read_stream": read_rate,
-        "decode_kernel_vs_read_stream": (None if read_rate is None or achieved is None else
+        "decode_call_vs_read_stream": (None if read_rate is None or achieved is None else
                                          achieved / read_rate["TB_per_s"]),
+        "decode_call_vs_read_at_call_size": (None if read_rate is None or achieved is None
+                                             or read_rate["at_call_size"] is None else
+                                             achieved / read_rate["at_call_size"]["TB_per_s"]),
         "other_configs": configs,
         "cpu_baseline": cpu,
         "parity_max_abs_err_vs_cpu": err,
