@@ -494,8 +494,8 @@ def rope_append_config(ff, torch, dev, stream, calls=50, seed=5):
 
 def decode_batch_upload(torch, stream, ctx_np, table_np, calls=50) -> dict | None:
     """firefly::DecodeBatch::upload itself (through tests/cpp/libdecode_step_shim.so, the C++ API's test shim):
-    the C2 rows packed with DecodeBatch::pack, then one upload per step on the launch stream, timed with HIP
-    events (best of three runs)."""
+    the C2 rows packed with DecodeBatch::pack, then one upload per step on the launch stream (a kernel that reads
+    the pinned staging through its device mapping), timed with HIP events (best of three runs)."""
     import ctypes
 
     import numpy as np
@@ -527,7 +527,8 @@ def decode_batch_upload(torch, stream, ctx_np, table_np, calls=50) -> dict | Non
         nbytes = int(lib.dss_last_upload_bytes(h))
     finally:
         lib.dss_destroy(h)
-    return {"row_stride_blocks": stride, "live_width": width, "bytes": nbytes, "copies": 1, "us_per_step": us}
+    return {"row_stride_blocks": stride, "live_width": width, "bytes": nbytes, "copies": 1,
+            "how": "one kernel reading the pinned staging through its device mapping", "us_per_step": us}
 
 
 def decode_step_config(ff, torch, dev, stream, ctx_np, table_np, N, pools, q, k_new, v_new, out, ws, max_ctx,

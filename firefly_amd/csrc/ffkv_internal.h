@@ -139,6 +139,9 @@ hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream);  // matrix-
 hipError_t launch_prefix_partials(const PrefillArgs& a, hipStream_t stream);  // shared-prefix decode partials
 hipError_t launch_decode(const DecodeArgs& a, hipStream_t stream);       // generic kernel (any cache dtype)
 hipError_t launch_decode_mfma(const DecodeArgs& a, hipStream_t stream);  // matrix-core kernel (16-bit/8-bit caches)
+// Copies the first `width` ints of `rows` rows of `pitch` ints from src (pinned host memory mapped into the device's
+// address space: its device pointer) to dst (device memory) with a kernel on `stream`.
+hipError_t launch_staging_copy(int32_t* dst, const int32_t* src, int pitch, int width, int rows, hipStream_t stream);
 
 // Upper bound on the MFMA kernel's work items (sizes its partial-result slots).
 constexpr int kMfmaMaxItems = 2048;

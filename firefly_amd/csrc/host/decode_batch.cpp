@@ -12,6 +12,7 @@
 #include <string>
 #include <utility>
 
+#include "ffkv_internal.h"
 #include "firefly/hal/graph.h"
 
 namespace firefly
@@ -24,12 +25,14 @@ DecodeBatch::DecodeBatch(int batch_capacity, int max_context_blocks)
     lens_rows_ = (capacity_ + stride_ - 1) / stride_;
     const size_t lens = static_cast<size_t>(lens_rows_) * stride_;
     const size_t all = (lens + static_cast<size_t>(capacity_) * stride_) * sizeof(int32_t);
-    if (hipHostMalloc(reinterpret_cast<void**>(&h_all_), all, hipHostMallocDefault) != hipSuccess ||
+    if (hipHostMalloc(reinterpret_cast<void**>(&h_all_), all, hipHostMallocMapped) != hipSuccess ||
         hipMalloc(reinterpret_cast<void**>(&d_all_), all) != hipSuccess)
     {
         release();
         return;
     }
+    // the staging's address on the device, which upload's copy kernel reads; without it upload copies by DMA
+    if (hipHostGetDevicePointer(reinterpret_cast<void**>(&h_dev_), h_all_, 0) != hipSuccess) h_dev_ = nullptr;
     h_context_lens_ = h_all_;
     h_block_table_ = h_all_ + lens;
     d_context_lens_ = d_all_;
@@ -46,7 +49,7 @@ void DecodeBatch::release()
 {
     if (d_all_) (void)hipFree(d_all_);
     if (h_all_) (void)hipHostFree(h_all_);
-    d_all_ = h_all_ = d_block_table_ = d_context_lens_ = h_block_table_ = h_context_lens_ = nullptr;
+    d_all_ = h_all_ = h_dev_ = d_block_table_ = d_context_lens_ = h_block_table_ = h_context_lens_ = nullptr;
 }
 
 int DecodeBatch::pack(const std::vector<const GenerationRequest*>& requests)
@@ -89,7 +92,9 @@ bool DecodeBatch::upload(hipStream_t stream)
     const int    w = std::max(width_, lens_rows_ == 1 ? capacity_ : stride_);
     const size_t pitch = static_cast<size_t>(stride_) * sizeof(int32_t);
     hipError_t   e;
-    if (w >= stride_)
+    if (h_dev_ != nullptr)  // one kernel reads the mapped staging: a launch instead of a DMA transfer's start-up
+        e = ffkv::launch_staging_copy(d_all_, h_dev_, stride_, std::min(w, stride_), static_cast<int>(rows), stream);
+    else if (w >= stride_)
         e = hipMemcpyAsync(d_all_, h_all_, rows * pitch, hipMemcpyHostToDevice, stream);
     else
         e = hipMemcpy2DAsync(d_all_, pitch, h_all_, pitch, static_cast<size_t>(w) * sizeof(int32_t), rows,

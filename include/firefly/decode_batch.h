@@ -7,8 +7,10 @@
 // separate copies every step (25.6 MB at 64 x 100k blocks); here the device table keeps a fixed row stride (so a
 // graph captured once stays valid) and each upload is ONE copy: the context lengths sit in the rows just before
 // the table in one buffer of that row stride (host and device alike), and the copy takes only the live width of
-// every row (the longest row's block count, at least the lengths' width) - a plain copy when that is the whole
-// stride, a 2D copy otherwise.  Entries beyond a row's live blocks are never read by the path's kernels (they
+// every row (the longest row's block count, at least the lengths' width): one small kernel that reads the pinned
+// staging through its device mapping (a launch, where a DMA copy costs about 10 us of start-up), or, where the
+// staging has no device mapping, a plain copy when that width is the whole stride and a 2D copy otherwise.
+// Entries beyond a row's live blocks are never read by the path's kernels (they
 // read blocks 0 .. ceil((context_len + new tokens) / 16) - 1 of a row), so stale device entries there are
 // harmless.
 //
@@ -46,7 +48,8 @@ public:
     int pack(const std::vector<const GenerationRequest*>& requests);
 
     /// Copy the packed context lengths and the live width of every table row to the device, on `stream`, as one
-    /// copy.  Asynchronous; the staging must not be re-packed until the copy has completed on the stream.
+    /// copy (a kernel reading the mapped staging).  Asynchronous; the staging must not be re-packed until the copy
+    /// has completed on the stream.
     bool upload(hipStream_t stream);
 
     const int32_t* device_context_lens() const { return d_context_lens_; }
@@ -71,6 +74,7 @@ private:
     int      lens_rows_ = 1;             // rows of `stride` ints holding the context lengths
     int32_t* h_all_ = nullptr;           // pinned [lens_rows + capacity, stride]: context lengths, then the table
     int32_t* d_all_ = nullptr;           // the same on the device
+    int32_t* h_dev_ = nullptr;           // h_all_'s address on the device (mapped), read by the upload kernel
     int32_t* h_context_lens_ = nullptr;  // = h_all_
     int32_t* h_block_table_ = nullptr;   // = h_all_ + lens_rows * stride, [capacity, stride]
     int32_t* d_context_lens_ = nullptr;
