@@ -22,8 +22,9 @@ Printed JSON line (rank 0, N = 1):
                  at_call_size: the best shape over buffers of one decode call's bytes (start and tail included),
                  decode_call_vs_read_at_call_size = roofline.achieved over that
   other_configs  C3, C4 and C5 (int8 and fp8 pools filled by the quantizing append, whose bulk throughput is
-                 reported as quantized_append), the C4 prefill on every cache type and head_dim, a head_dim 256
-                 decode, the fused rope + append, and the decode step's host upload
+                 reported as quantized_append), the C4 prefill on every cache type and head_dim, decodes at head_dim
+                 256, 96, 112 and 80 and over fp32 pages (the vector kernel), the fused rope + append, and the decode
+                 step's host upload
 
 Algorithmic bytes per decode call (L'_b = context_lens[b] + 1):
   sum_b L'_b*Hkv*D*2*2 (K and V) + B*Hq*D*2*2 (q in, out) + sum_b ceil(L'_b/16)*4 (block table) + 4*B
@@ -202,11 +203,12 @@ def _tables(rng, need, shared_blocks=0):
 
 
 def _pools(torch, gen, dev, N, Hkv, D, kv, layers):
-    """Random bf16 pools (kv must be "bf16"; quantized pools come from _appended_pools)."""
-    assert kv == "bf16"
+    """Random bf16 or fp32 pools (quantized pools come from _appended_pools)."""
+    assert kv in ("bf16", "f32")
     shape = (N, BLOCK, Hkv, D)
-    return [(torch.randn(shape, generator=gen, device=dev, dtype=torch.bfloat16),
-             torch.randn(shape, generator=gen, device=dev, dtype=torch.bfloat16), None, None) for _ in range(layers)]
+    dt = torch.bfloat16 if kv == "bf16" else torch.float32
+    return [(torch.randn(shape, generator=gen, device=dev, dtype=dt),
+             torch.randn(shape, generator=gen, device=dev, dtype=dt), None, None) for _ in range(layers)]
 
 
 def _appended_pools(ff, torch, gen, dev, stream, N, Hkv, D, kv, layers, table, ctx, chunk=1024):
@@ -266,7 +268,7 @@ def decode_config(ff, torch, dev, stream, name, B, Hq, Hkv, D, ctx, kv="bf16", l
     table_np, N = _tables(rng, need, shared_blocks)
     bt = torch.from_numpy(table_np).to(dev)
     append_fig = None
-    if kv == "bf16":
+    if kv in ("bf16", "f32"):
         pools = _pools(torch, gen, dev, N, Hkv, D, kv, layers)
     else:
         pools, append_fig = _appended_pools(ff, torch, gen, dev, stream, N, Hkv, D, kv, layers, bt, Lp)
@@ -281,7 +283,7 @@ def decode_config(ff, torch, dev, stream, name, B, Hq, Hkv, D, ctx, kv="bf16", l
                            workspace=ws, stream=stream)
 
     us = _events_us(call, calls, stream)
-    es = 2 if kv == "bf16" else 1
+    es = {"bf16": 2, "f32": 4}.get(kv, 1)
     tok = sum(Lp)
     kv_bytes = tok * Hkv * D * es * 2 + (tok * Hkv * 4 * 2 if kv == "i8" else 0)
     other = B * Hq * D * 2 * 2 + sum(need) * 4 + 4 * B
@@ -632,7 +634,7 @@ def main(argv=None) -> int:
                     help="skip the other BASELINE configurations (C3, C4, C5 int8/fp8) and the rope+append figures")
     ap.add_argument("--configs", default="all",
                     help="comma-separated subset of C3,C5_int8,C5_fp8,C4,prefill_variants,decode_d256,decode_d96,"
-                         "decode_d112,decode_d80,rope_append,C2_decode_step_host (default all)")
+                         "decode_d112,decode_d80,decode_f32,rope_append,C2_decode_step_host (default all)")
     ap.add_argument("--skip-c2", action="store_true",
                     help="skip the C2 steps, the device copy and the CPU baseline (profiling other configurations "
                          "alone); the headline fields are then null")
@@ -789,6 +791,9 @@ def main(argv=None) -> int:
             "decode_d80": lambda: decode_config(ff, torch, dev, stream, "head_dim 80 decode (matrix cores, a last "
                                                 "k-step of 16 dims): Hq32/Hkv8/D80 bf16, B=64, ctx U[512,4096]",
                                                 64, 32, 8, 80, d80_ctx, seed=11),
+            "decode_f32": lambda: decode_config(ff, torch, dev, stream, "fp32 pages (the vector kernel): "
+                                                "Hq32/Hkv8/D128, q bf16, B=64, ctx U[512,4096]",
+                                                64, 32, 8, 128, f32_ctx, kv="f32", seed=12),
             "rope_append": lambda: rope_append_config(ff, torch, dev, stream),
             "C2_decode_step_host": lambda: decode_step_config(ff, torch, dev, stream, ctx_np, table_np, N, pools, q,
                                                               k_new, v_new, out, ws, max_ctx),
@@ -798,6 +803,7 @@ def main(argv=None) -> int:
         d96_ctx = rng.integers(512, 4097, size=64)
         d112_ctx = rng.integers(512, 4097, size=64)
         d80_ctx = rng.integers(512, 4097, size=64)
+        f32_ctx = rng.integers(512, 4097, size=64)
         want = list(makers) if args.configs == "all" else [x for x in args.configs.split(",") if x]
         unknown = [x for x in want if x not in makers]
         if unknown:
