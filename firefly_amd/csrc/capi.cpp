@@ -121,7 +121,8 @@ size_t decode_mfma_workspace_bytes(int batch, int num_heads, int head_dim)
 
 // Shared-prefix split: the prefix kernel runs (kv head, chunk) groups of ceil(batch * group / 128) workgroups;
 // about one workgroup per CU (256) without chunks under 8 pages (each chunk's partials cost 4 * (head_dim + 2)
-// bytes per (row, head) written and read back).  FFKV_PREFIX_CHUNKS overrides the count.
+// bytes per (row, head) written and read back).  FFKV_PREFIX_CHUNKS overrides the count.  The workspace's prefix
+// slots are sized for this count; the fused grid (decode_pfx_plan) takes at most as many chunks.
 void prefix_chunking(int batch, int group, int num_kv_heads, int shared_blocks, int& chunks, int& chunk_pages)
 {
     static const int env = []
