@@ -1,8 +1,8 @@
-"""Seeded random shapes for the decode (with its append) and the chunked prefill, against the CPU checker, to the
-same bar as the fixed-shape parity tests: pages bit-exact, outputs within 2e-3 (16-bit caches) / 2e-2 (8-bit
-caches) / 1e-4 (fp32 decode) of the checker beyond the output's own rounding.  Each case draws the batch, the GQA
-group (1 .. 40 query heads per KV head), the KV heads, head_dim, the row lengths (empty rows included), the
-chunk length and the dtype pair from a fixed seed, so a failure names a reproducible case."""
+"""Seeded random shapes for the decode (with its append), the decode over a shared prefix and the chunked prefill,
+against the CPU checker, to the same bar as the fixed-shape parity tests: pages bit-exact, outputs within 2e-3
+(16-bit caches) / 2e-2 (8-bit caches) / 1e-4 (fp32 decode) of the checker beyond the output's own rounding.  Each case
+draws the batch, the GQA group (1 .. 40 query heads per KV head), the KV heads, head_dim, the row lengths (empty
+rows included), the chunk length and the dtype pair from a fixed seed, so a failure names a reproducible case."""
 
 import math
 
@@ -67,3 +67,27 @@ def test_random_decode_head_dims(ff, gpu, seed):
     ctx[rng.random(B) < 0.1] = 0
     c = cases.make_case(9800 + seed, B, G * Hkv, Hkv, D, ctx, act=act, kv=kv, input_scale=1 / math.sqrt(D))
     _decode_check(ff, gpu, c, TOL[(act, kv)])
+
+
+SHARED_PAIRS = [("bf16", "bf16"), ("f16", "f16"), ("f32", "bf16"), ("bf16", "bf16"), ("bf16", "i8"), ("f16", "fp8")]
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_random_shared_prefix(ff, gpu, seed):
+    """ffkv_paged_decode_shared_prefix on seeded shapes, against the checker and the plain decode: mostly 16-bit
+    pages at head_dim 128 with KV-head counts that are multiples of 4 (the prefix partials inside the decode's
+    grid; enough private pages for its weighted page split in most cases), the 8-bit pairs on the two-launch path.
+    Some rows end exactly at the prefix."""
+    from test_gpu_shared_prefix import _both
+
+    rng = np.random.default_rng(9900 + seed)
+    act, kv = SHARED_PAIRS[seed % len(SHARED_PAIRS)]
+    G = int(rng.choice([g for g in GROUPS if g <= 16]))
+    Hkv = int(rng.choice([4, 8, 12]))
+    B = int(rng.integers(4, 49))
+    shared = int(rng.integers(1, 161))
+    ctx = shared * 16 + rng.integers(0, 601, size=B) - 1  # ctx + 1 tokens after the step's append
+    ctx[rng.random(B) < 0.1] = shared * 16 - 1  # the row ends at the prefix's end
+    c = cases.make_case(9900 + seed, B, G * Hkv, Hkv, 128, ctx, act=act, kv=kv, shared_prefix_blocks=shared,
+                        input_scale=1 / math.sqrt(128))
+    _both(ff, gpu, c, shared, tol=2e-3 if kv in ("bf16", "f16") else 2e-2)
