@@ -598,8 +598,14 @@ __device__ __forceinline__ void prefill_wg(PrefillArgs a, int wg_index, uint8_t*
         run_dst[k] = (is_v ? C::TILEB : 0) + (C16 ? lr * 2048 + 1024 : lr * 64 * 16);
     }
     // C16: where this lane's 16 codes go once converted (the 16-bit chunks 2ch and 2ch + 1 of its key row, at
-    // their swizzled places), relative to run_dst[k]
-    int c16_dst[C16 ? LC::RPW : 1][2];
+    // their swizzled places), relative to run_dst[k].  A scattered 16-byte LDS write is served 8 lanes at a time
+    // over 128 bytes, so the 8 lanes of each group must write 8 distinct 16-byte slots modulo 128 bytes: with the
+    // lower half of every lane's codes written first, a group (4 chunks of one or two key rows) fills the slots
+    // of one parity only (two lanes per bank group: 8 conflict cycles per write, one per matrix product).  Lanes
+    // 4..7 of each group therefore write the other parity first: c16_hi1[k] says the lane's first write holds
+    // its upper 8 values.
+    int  c16_dst[C16 ? LC::RPW : 1][2];
+    bool c16_hi1[C16 ? LC::RPW : 1];
     if constexpr (C16)
 #pragma unroll
         for (int k = 0; k < LC::RPW; ++k)
@@ -608,8 +614,10 @@ __device__ __forceinline__ void prefill_wg(PrefillArgs a, int wg_index, uint8_t*
             const int tok = p / LC::CPT;
             const int ch = p % LC::CPT;
             const int sw = run_is_v(k) ? v_swizzle<D>(tok) : k_swizzle<D>(tok);
+            const int hs = ((lane >> 2) ^ sw) & 1;  // the first write's slot has parity (lane >> 2) & 1
+            c16_hi1[k] = hs != 0;
 #pragma unroll
-            for (int h = 0; h < 2; ++h) c16_dst[k][h] = 32 * (lane - ch) - 1024 + 16 * ((2 * ch + h) ^ sw);
+            for (int h = 0; h < 2; ++h) c16_dst[k][h] = 32 * (lane - ch) - 1024 + 16 * ((2 * ch + (h ^ hs)) ^ sw);
         }
     const uint32_t page_bytes = static_cast<uint32_t>(kBlockSize * row_bytes);
     const uint64_t row_base = a.paged ? 0 : static_cast<uint64_t>(b) * S * row_bytes;
@@ -1033,10 +1041,11 @@ __device__ __forceinline__ void prefill_wg(PrefillArgs a, int wg_index, uint8_t*
         for (int k = 0; k < (C16 ? LC::RPW : 0); ++k)
         {
             const u32x4 w = *(FFKV_LDS u32x4*)(stage + run_dst[k] + 16 * lane);
-            const u32x4 lo = codes_to_m<CT, false>(w[0], w[1]);
-            const u32x4 hi = codes_to_m<CT, false>(w[2], w[3]);
-            *(FFKV_LDS u32x4*)(stage + run_dst[k] + c16_dst[k][0]) = lo;
-            *(FFKV_LDS u32x4*)(stage + run_dst[k] + c16_dst[k][1]) = hi;
+            const bool  h1 = c16_hi1[k];
+            const u32x4 first = codes_to_m<CT, false>(h1 ? w[2] : w[0], h1 ? w[3] : w[1]);
+            const u32x4 second = codes_to_m<CT, false>(h1 ? w[0] : w[2], h1 ? w[1] : w[3]);
+            *(FFKV_LDS u32x4*)(stage + run_dst[k] + c16_dst[k][0]) = first;
+            *(FFKV_LDS u32x4*)(stage + run_dst[k] + c16_dst[k][1]) = second;
         }
     };
 
