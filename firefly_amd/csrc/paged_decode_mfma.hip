@@ -120,9 +120,6 @@ constexpr int kMfmaWaves =
                                                 : (CT == FP8 ? FFKV_MFMA_WAVES128_FP8 : FFKV_MFMA_WAVES128_I8))
                          : (kMfmaDepth<CT, D> > 1 ? 3 : 4));
 
-#ifndef FFKV_DECODE_TRV
-#define FFKV_DECODE_TRV 1  // V^T operands through transposed LDS reads (ds_read_b64_tr_b16)
-#endif
 
 // Page loads.  V is staged through LDS, so its loads can take any lane layout: each load instruction reads 64
 // consecutive 16-byte chunks of the wave's slice of the page (whole 128-byte lines of 4 token rows at head_dim
@@ -148,15 +145,21 @@ __device__ __forceinline__ u32x4 load16(const char* p)
 
 // Position of element (token t, dim d) of a wave's V tile: 16-byte chunks XOR-swizzled by row so that the four
 // rows of one transposed read (two chunks each) sit on distinct banks.
+// Bit 0 of the chunk index is also flipped for the chunks written by lanes 4..7 of each group of 8 (flip below):
+// a scattered 16-byte LDS write is served 8 lanes at a time over 128 bytes, and an 8-bit page's lane writes the
+// 8 values of its first half to chunk 2ch and those of its second half to 2ch + 1 (16 codes, dims 16 ch ..
+// 16 ch + 15), so without the flip the 8 lanes of a group would fill chunks of one parity only, two lanes per
+// bank group.  A flip only swaps the two chunks of a 16-dim pair, which a transposed read takes together.
 template <int D>
 __device__ __forceinline__ int vt_pos(int t, int d)
 {
+    // 16 codes per chunk of an 8-bit page: lane group bit of the code chunk (row t, 16-dim pair d / 16)
+    const int flip = ((t * (D / 16) + (d >> 4)) >> 2) & 1;
     // head_dim 96 (12 chunks a row, whose 192-byte stride already spreads a read's four rows over the banks): the
     // swizzle stays within aligned groups of four chunks, so it never leaves the row; head_dim 80 and 112 (160- and
     // 224-byte rows) put the 8 rows of two transposed reads on distinct banks unswizzled
-    if constexpr (D == 80 || D == 112) return t * D + d;
-    const int sw = D == 64 ? 2 * ((t >> 1) & 3) : (D == 96 ? 2 * ((t >> 2) & 1) : 2 * (t & 7));
-    return t * D + (((d >> 3) ^ sw) << 3) + (d & 7);
+    const int sw = D == 80 || D == 112 ? 0 : (D == 64 ? 2 * ((t >> 1) & 3) : (D == 96 ? 2 * ((t >> 2) & 1) : 2 * (t & 7)));
+    return t * D + (((d >> 3) ^ sw ^ flip) << 3) + (d & 7);
 }
 
 // Waves per workgroup (the KV heads, or blocks of 16 query heads, that read the same pages together).  With 8
@@ -599,23 +602,14 @@ __device__ __forceinline__ void decode_wg(const DecodeArgs& a, int item_, int y_
             if constexpr (kElemBytes<CT> == 2)
             {
                 const u32x4 w = tok_ok ? r.v[j] : u32x4{0u, 0u, 0u, 0u};
-#if FFKV_DECODE_TRV
                 *reinterpret_cast<u32x4*>(sv + vt_pos<D>(t, 8 * v_chk(j))) = w;
-#else
-                *reinterpret_cast<u32x4*>(sv + lds_pos<D>(t, 8 * v_chk(j))) = w;
-#endif
             }
             else  // 16 codes: dims 16 ch .. 16 ch + 15 as two 8-value words
             {
                 const u32x4 lo = tok_ok ? codes_to_m<CT, VBF>(r.v[j][0], r.v[j][1]) : u32x4{0u, 0u, 0u, 0u};
                 const u32x4 hi = tok_ok ? codes_to_m<CT, VBF>(r.v[j][2], r.v[j][3]) : u32x4{0u, 0u, 0u, 0u};
-#if FFKV_DECODE_TRV
                 *reinterpret_cast<u32x4*>(sv + vt_pos<D>(t, 16 * v_chk(j))) = lo;
                 *reinterpret_cast<u32x4*>(sv + vt_pos<D>(t, 16 * v_chk(j) + 8)) = hi;
-#else
-                *reinterpret_cast<u32x4*>(sv + lds_pos<D>(t, 16 * v_chk(j))) = lo;
-                *reinterpret_cast<u32x4*>(sv + lds_pos<D>(t, 16 * v_chk(j) + 8)) = hi;
-#endif
             }
         }
         s = f32x4{0.0f, 0.0f, 0.0f, 0.0f};  // lane (c, g) gets tokens 4g + i of head c
@@ -716,19 +710,11 @@ __device__ __forceinline__ void decode_wg(const DecodeArgs& a, int item_, int y_
 #pragma unroll
         for (int n = 0; n < NT; ++n)
         {
-#if FFKV_DECODE_TRV
             // transposed read: lane 4r + q of group g supplies dims 16n + 4q .. +3 of token 4g + r; lane c
             // receives dim 16n + c of tokens 4g .. 4g + 3
             const auto raw = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
                 (__attribute__((address_space(3))) bf16x4*)(sv + vt_pos<D>(4 * g + (c >> 2), 16 * n + 4 * (c & 3))));
             const typename MV::x4 vt = __builtin_bit_cast(typename MV::x4, raw);
-#else
-            const uint32_t v0 = sv[lds_pos<D>(4 * g + 0, 16 * n + c)];
-            const uint32_t v1 = sv[lds_pos<D>(4 * g + 1, 16 * n + c)];
-            const uint32_t v2 = sv[lds_pos<D>(4 * g + 2, 16 * n + c)];
-            const uint32_t v3 = sv[lds_pos<D>(4 * g + 3, 16 * n + c)];
-            const typename MV::x4 vt = __builtin_bit_cast(typename MV::x4, u32x2{v0 | (v1 << 16), v2 | (v3 << 16)});
-#endif
             acc[n] = MV::mma16(vt, phi, acc[n]);
             if constexpr (P_LO) acc[n] = MV::mma16(vt, plo, acc[n]);
         }
