@@ -209,7 +209,8 @@ FFKV_API int ffkv_paged_decode_shared_prefix(const void* q, void* out, int qo_dt
  * 1.3e8).  bf16 caches: V enters the products in f16 (a workgroup that meets |V| >= 65520 reruns in bf16), so V values
  * below 2^-14 carry an absolute error of at most 2^-25.  16-bit caches: an infinite V value also makes NaN, in
  * its dim, the outputs of the queries whose causal limit masks its key (it meets them with weight 0 in the tile
- * products).
+ * products), as in the reference's prefill, whose P.V tile product (src/kernels/attention.cu:232-243) takes every
+ * key of its 16-key tile, the causally masked ones with p = 0 (:173-174).
  */
 FFKV_API int ffkv_paged_prefill(const void* q, void* out, int qo_dtype, const void* k_cache, const void* v_cache,
                                 int cache_dtype, const float* k_scale, const float* v_scale, const int32_t* block_table,

@@ -276,7 +276,9 @@ def test_prefill_bf16_large_v(ff, gpu, D, big):
     1's outputs must match the float64 closed form relative to its largest |v|, and rows 0 and 2 keep the
     ordinary bar.  Infinite V: non-finite wherever the closed form is; a query for which the infinite value's key
     is masked (causal limit) may get NaN in that dim too, as the masked key still meets it in the step's products
-    with p = 0 (0 * inf), but only in kv head 3's heads; the other heads keep the ordinary bar."""
+    with p = 0 (0 * inf), but only in kv head 3's heads; the other heads keep the ordinary bar.  The reference's
+    prefill does the same: its P.V tile product (src/kernels/attention.cu:232-243) takes every key of the 16-key
+    tile, the causally masked ones with p = 0 (:173-174)."""
     Hq, Hkv = (16, 4) if D == 256 else (32, 8)
     c, qn = _case(150 + D, 3, Hq, Hkv, D, [17, 300, 5], 37)
     rng = np.random.default_rng(151)
