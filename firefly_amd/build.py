@@ -43,9 +43,9 @@ def _sources() -> list[Path]:
     return sorted(list(CSRC.glob("*.hip")) + list(CSRC.glob("*.cpp")) + list((CSRC / "host").glob("*.cpp")))
 
 
-def _compile(src: Path) -> Path:
-    obj = BUILD / (src.name + ".o")
-    cmd = [HIPCC, *COMMON, *DEVICE, "-c", str(src), "-o", str(obj)]
+def _compile(src: Path, build_dir: Path = BUILD, defines: tuple[str, ...] = ()) -> Path:
+    obj = build_dir / (src.name + ".o")
+    cmd = [HIPCC, *COMMON, *DEVICE, *(f"-D{d}" for d in defines), "-c", str(src), "-o", str(obj)]
     if src.suffix == ".hip":
         cmd[1:1] = ["-x", "hip"]
     else:
@@ -57,19 +57,28 @@ def _compile(src: Path) -> Path:
     return obj
 
 
-def build_library(jobs: int = 8) -> Path:
-    """Compile every source and link ``libffkv.so``.  Always rebuilds."""
-    BUILD.mkdir(exist_ok=True)
+def build_library(jobs: int = 8, defines: tuple[str, ...] = (), out: Path | None = None) -> Path:
+    """Compile every source and link ``libffkv.so``.  Always rebuilds.
+
+    ``defines`` (``NAME=VALUE`` strings) set the kernels' compile-time switches (``FFKV_*`` macros) for a variant
+    build, which is linked to ``out`` (its objects under ``_build/variant``) and leaves ``libffkv.so`` alone;
+    ``bench.py --lib`` measures such a build beside the shipped one."""
+    if defines and out is None:
+        raise ValueError("a variant build (defines) needs its own output path")
+    build_dir = BUILD / "variant" if defines else BUILD
+    build_dir.mkdir(parents=True, exist_ok=True)
+    target = Path(out) if out is not None else LIB
+    target.parent.mkdir(parents=True, exist_ok=True)
     srcs = _sources()
     with cf.ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
-        objs = list(ex.map(_compile, srcs))
-    tmp = LIB.with_suffix(".so.tmp")
+        objs = list(ex.map(lambda src: _compile(src, build_dir, tuple(defines)), srcs))
+    tmp = target.with_suffix(".so.tmp")
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed: {' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
-    os.replace(tmp, LIB)
-    return LIB
+    os.replace(tmp, target)
+    return target
 
 
 def build_test_shims() -> None:
@@ -120,7 +129,14 @@ def main(argv: list[str] | None = None) -> int:
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--jobs", type=int, default=8)
     ap.add_argument("--no-oracle", action="store_true")
+    ap.add_argument("--define", action="append", default=[], metavar="NAME=VALUE",
+                    help="compile-time switch for a variant build (repeatable; needs --out)")
+    ap.add_argument("--out", default=None, help="output path of a variant build")
     args = ap.parse_args(argv)
+    if args.define:
+        lib = build_library(args.jobs, tuple(args.define), Path(args.out) if args.out else None)
+        print(f"built {lib}")
+        return 0
     lib = build_library(args.jobs)
     build_test_shims()
     build_bench_helpers()
