@@ -273,6 +273,9 @@ struct PrefillLds
     static constexpr int S2 = kDmaStages<D> >= 3 ? STAGE : 16;
     static constexpr int S3 = kDmaStages<D> == 4 ? STAGE : 16;
     static constexpr int BYTES = 2 * STAGE + S2 + S3;  // the four in a row
+    static_assert(BYTES + 16 <= 160 * 1024,
+                  "the stages exceed the 160 KiB of LDS of a CU: fewer stages (FFKV_PREFILL_STAGES) or pages per step "
+                  "(FFKV_PREFILL_DMA_KP*) for this head_dim");
 };
 
 // One workgroup's share of a prefill (or of the shared-prefix partials): `wg_index` is its index in the launch grid
