@@ -102,6 +102,20 @@ def test_head_dim_256_dtypes(ff, gpu, act, kv):
     _check(ff, gpu, c, 2e-3 if kv in ("f16", "bf16") else 2e-2)
 
 
+@pytest.mark.parametrize("D", [64, 256])
+@pytest.mark.parametrize("G", [1, 7, 16])
+@pytest.mark.parametrize("kv", ["i8", "fp8"])
+def test_quantized_head_shapes(ff, gpu, D, G, kv):
+    """8-bit pages at head_dim 64 and 256 on the matrix cores: each lane stages its 16 codes of a V row as two
+    converted 16-byte chunks in the wave's LDS tile, whose chunk order differs by lane group (the pair of a
+    16-dim tile swapped for lanes 4..7 of every 8); outputs within the 8-bit bar."""
+    Hkv = 2
+    rng = np.random.default_rng(D * 1000 + G * 10 + len(kv))
+    ctx = rng.integers(0, 700, size=5)
+    c = cases.make_case(31 + G + D, 5, Hkv * G, Hkv, D, ctx, act="bf16", kv=kv, input_scale=1 / math.sqrt(D))
+    _check(ff, gpu, c, TOL[("bf16", kv)])
+
+
 @pytest.mark.parametrize("D", [8, 40, 80, 96, 112])
 @pytest.mark.parametrize("act,kv", [("bf16", "bf16"), ("f16", "f16"), ("f32", "f32"), ("bf16", "i8"),
                                     ("bf16", "fp8"), ("f32", "fp8"), ("f16", "i8"), ("f16", "fp8")])
