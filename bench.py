@@ -583,6 +583,62 @@ def decode_step_config(ff, torch, dev, stream, ctx_np, table_np, N, pools, q, k_
     return res
 
 
+def decode_timeline(ff, torch, np, stream, call, calls: int = 5, warm: int = 20, out_path=None) -> dict:
+    """Per-wave start and end times of the split-K decode kernel (a timeline build of the library records them on
+    the GPU's 100 MHz clock), over `calls` decode calls after `warm` untimed ones: when the waves start, when they
+    end (relative to the first start), and how far the last end trails the median one."""
+    import ctypes
+
+    fn = getattr(ff.lib, "ffkv_decode_timeline", None)
+    if fn is None:
+        raise SystemExit("--timeline needs --lib pointing at a timeline build: python -m firefly_amd.build "
+                         "--define FFKV_DECODE_TIMELINE=1 --out PATH")
+    fn.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int]
+    fn.restype = ctypes.c_int
+    max_waves = 1 << 16
+    buf = np.zeros(2 * max_waves, dtype=np.uint64)
+    for i in range(warm):
+        call(i)
+    torch.cuda.synchronize()
+    per_call, raw = [], []
+    for i in range(calls):
+        torch.cuda.synchronize()
+        assert fn(None, max_waves, 1) == 0
+        call(i)
+        torch.cuda.synchronize()
+        assert fn(buf.ctypes.data, max_waves, 0) == 0
+        st, en = buf[0::2].copy(), buf[1::2].copy()
+        raw.append((st, en))
+        rec = st > 0
+        t0 = int(st[rec].min())
+        s_us = (st[rec] - t0) / 100.0  # 100 MHz ticks -> us
+        e_us = (en[rec] - t0) / 100.0
+        q = lambda x, p: float(np.percentile(x, p))
+        per_call.append({
+            "waves": int(rec.sum()),
+            "start_us": {"p50": q(s_us, 50), "p90": q(s_us, 90), "max": float(s_us.max())},
+            "end_us": {"p10": q(e_us, 10), "p50": q(e_us, 50), "p90": q(e_us, 90), "p99": q(e_us, 99),
+                       "max": float(e_us.max())},
+            "wave_us": {"p50": q(e_us - s_us, 50), "p90": q(e_us - s_us, 90)},
+            "tail_after_median_end_us": float(e_us.max()) - q(e_us, 50),
+        })
+    if out_path is not None:  # wave w = (blockIdx.y * gridDim.x + blockIdx.x) * waves per workgroup + wave
+        np.savez(out_path, start=np.stack([r[0] for r in raw]), end=np.stack([r[1] for r in raw]))
+    med = lambda key, sub: float(np.median([c[key][sub] for c in per_call]))
+    return {
+        "timeline": "paged_decode_mfma, C2 decode call (bench.py workload), wave start/end on the 100 MHz clock",
+        "calls": calls,
+        "waves": per_call[0]["waves"],
+        "median_over_calls": {
+            "start_us": {k: med("start_us", k) for k in ("p50", "p90", "max")},
+            "end_us": {k: med("end_us", k) for k in ("p10", "p50", "p90", "p99", "max")},
+            "wave_us": {k: med("wave_us", k) for k in ("p50", "p90")},
+            "tail_after_median_end_us": float(np.median([c["tail_after_median_end_us"] for c in per_call])),
+        },
+        "per_call": per_call,
+    }
+
+
 def cpu_baseline(ctx, table, N, k_pool, v_pool, q, gpu_out, seconds: float = 10.0):
     """Time the CPU restatement (oracle/) of the decode call on the host cores, on the same inputs as layer 0,
     and return (baseline dict, max-abs error of the GPU output against it)."""
@@ -641,6 +697,12 @@ def main(argv=None) -> int:
     ap.add_argument("--lib", default=None,
                     help="time another build of libffkv.so (for example one made from an earlier commit in a git "
                          "worktree) instead of firefly_amd/libffkv.so")
+    ap.add_argument("--timeline", action="store_true",
+                    help="with --lib pointing at a timeline build (python -m firefly_amd.build --define "
+                         "FFKV_DECODE_TIMELINE=1 --out PATH): report when the split-K decode kernel's waves start and "
+                         "end over a few C2 decode calls, then exit")
+    ap.add_argument("--timeline-out", default=None,
+                    help="with --timeline: also save every call's per-wave start and end ticks to this .npz file")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run one 1 GiB device-to-device copy (a kernel of known read/write bytes, used to "
                          "scale rocprofv3 FETCH_SIZE/WRITE_SIZE counters)")
@@ -691,6 +753,12 @@ def main(argv=None) -> int:
         kp, vp = pools[i % args.layers]
         ff.append_kv_cache(k_new, v_new, kp, vp, table, ctx, stream=stream)
         ff.paged_attention(q, kp, vp, table, ctx, out=out, max_context_len=max_ctx, workspace=ws, stream=stream)
+
+    if args.timeline:
+        print(json.dumps(decode_timeline(ff, torch, np, stream, lambda i: ff.paged_attention(
+            q, pools[i % args.layers][0], pools[i % args.layers][1], table, ctx, out=out, max_context_len=max_ctx,
+            workspace=ws, stream=stream), out_path=args.timeline_out)))
+        return 0
 
     if args.calibrate_copy:
         src = torch.ones(1 << 30, dtype=torch.uint8, device=dev)

@@ -130,6 +130,9 @@ constexpr int kMfmaWaves =
 #ifndef FFKV_DECODE_NT_V
 #define FFKV_DECODE_NT_V 1
 #endif
+#ifndef FFKV_DECODE_TIMELINE
+#define FFKV_DECODE_TIMELINE 0  // 1: each wave of the split-K kernel records its start and end (timeline builds)
+#endif
 #ifndef FFKV_DECODE_NT_K
 #define FFKV_DECODE_NT_K 0  // K (the operand-layout half) non-temporal too
 #endif
@@ -812,14 +815,32 @@ __device__ __forceinline__ void decode_wg(const DecodeArgs& a, int item_, int y_
     }
 }
 
+#if FFKV_DECODE_TIMELINE
+// Timeline builds: wave w of a launch (w = (blockIdx.y * gridDim.x + blockIdx.x) * NW + wave) records its start
+// and end on the GPU's constant 100 MHz clock in entries 2w and 2w + 1; ffkv_decode_timeline reads them back.
+constexpr int kTimelineWaves = 1 << 16;
+static __device__ uint64_t g_decode_timeline[2 * kTimelineWaves];
+#endif
+
 // Work item blockIdx.x of gridDim.x; KV heads blockIdx.y * NW .. +NW, one per wave (NW = blockDim.x / 64).
 template <int CT, int QT, int D>
 __global__ __launch_bounds__((64 * kMfmaMaxWaves<CT, D>)) __attribute__((amdgpu_waves_per_eu(kMfmaWaves<CT, QT, D>, 8)))
 void paged_decode_mfma(DecodeArgs a)
 {
     __shared__ uint16_t s_v[kMfmaMaxWaves<CT, D> * kBlockSize * D];
+#if FFKV_DECODE_TIMELINE
+    const uint64_t t_start = __builtin_amdgcn_s_memrealtime();
+#endif
     decode_wg<CT, QT, D>(a, static_cast<int>(blockIdx.x), static_cast<int>(blockIdx.y), static_cast<int>(gridDim.x),
                          static_cast<int>(blockDim.x) >> 6, s_v);
+#if FFKV_DECODE_TIMELINE
+    const uint64_t t_end = __builtin_amdgcn_s_memrealtime();
+    const int      lane = static_cast<int>(threadIdx.x) & 63;
+    const int      w = (static_cast<int>(blockIdx.y * gridDim.x + blockIdx.x) * static_cast<int>(blockDim.x >> 6)) +
+                  (static_cast<int>(threadIdx.x) >> 6);
+    if (lane < 2 && w < kTimelineWaves)  // two lanes, one vector store each
+        g_decode_timeline[2 * w + lane] = lane == 0 ? t_start : t_end;
+#endif
 }
 
 // Combine the partials of rows split over several work items.
@@ -1139,3 +1160,18 @@ hipError_t launch_decode_mfma(const DecodeArgs& a, hipStream_t stream)
 #endif  // FFKV_DEVICE_BODIES_ONLY
 
 }  // namespace ffkv
+
+#if FFKV_DECODE_TIMELINE && !defined(FFKV_DEVICE_BODIES_ONLY)
+// Timeline builds only (python -m firefly_amd.build --define FFKV_DECODE_TIMELINE=1 --out ...; bench.py --timeline):
+// clear != 0 zeroes the record, else up to max_waves (start, end) pairs of the last split-K launches are copied to
+// out (2 * max_waves values, 100 MHz clock ticks; waves that recorded nothing read 0).  Synchronous.
+extern "C" __attribute__((visibility("default"))) int ffkv_decode_timeline(uint64_t* out, int max_waves, int clear)
+{
+    const size_t n = static_cast<size_t>(max_waves < ffkv::kTimelineWaves ? max_waves : ffkv::kTimelineWaves);
+    void*        p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(ffkv::g_decode_timeline)) != hipSuccess) return -1;
+    if (clear != 0) return hipMemset(p, 0, sizeof(ffkv::g_decode_timeline)) == hipSuccess ? 0 : -1;
+    if (out == nullptr || max_waves <= 0) return -1;
+    return hipMemcpy(out, p, 2 * n * sizeof(uint64_t), hipMemcpyDeviceToHost) == hipSuccess ? 0 : -1;
+}
+#endif
