@@ -29,6 +29,11 @@ constexpr int kPfxWaves = 4;   // waves per workgroup: a decode head group, or a
 constexpr int kPfxRG = 2;      // row groups per wave of the prefix part
 static_assert(512 / kPfxRG == 64 * kPfxWaves, "prefix and decode workgroups are the same size");
 
+// The fused grid needs decode workgroups of kPfxWaves waves (a build with other FFKV_MFMA_MAX_WAVES* values
+// launches the two kernels instead).
+template <int CT>
+constexpr bool kPfxFits = kMfmaMaxWaves<CT, kPfxD> == kPfxWaves;
+
 template <int CT, int QT>
 struct PfxLds
 {
@@ -45,7 +50,7 @@ template <int CT, int QT>
 __global__ __launch_bounds__(64 * kPfxWaves) __attribute__((amdgpu_waves_per_eu(2, 8)))
 void paged_decode_pfx(DecodeArgs a, PrefillArgs p)
 {
-    static_assert(kMfmaMaxWaves<CT, kPfxD> == kPfxWaves, "decode workgroups of four waves");
+    static_assert(kPfxFits<CT>, "decode workgroups of four waves");
     using L = typename PfxLds<CT, QT>::L;
     __shared__ __align__(16) uint8_t s_lds[PfxLds<CT, QT>::BYTES];
     __shared__ int s_vover;
@@ -64,7 +69,10 @@ void paged_decode_pfx(DecodeArgs a, PrefillArgs p)
 template <int CT, int QT>
 const void* pfx_kernel()
 {
-    return reinterpret_cast<const void*>(paged_decode_pfx<CT, QT>);
+    if constexpr (kPfxFits<CT>)
+        return reinterpret_cast<const void*>(paged_decode_pfx<CT, QT>);
+    else
+        return nullptr;
 }
 
 const void* pfx_kernel_for(int cache_dtype, int qo_dtype)
@@ -77,11 +85,16 @@ const void* pfx_kernel_for(int cache_dtype, int qo_dtype)
 template <int CT, int QT>
 hipError_t launch_pfx(const DecodeArgs& a, const PrefillArgs& p, int gy, hipStream_t stream)
 {
-    hipLaunchKernelGGL((paged_decode_pfx<CT, QT>), dim3(static_cast<unsigned>(a.items), static_cast<unsigned>(gy)),
-                       dim3(64 * kPfxWaves), 0, stream, a, p);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    return launch_merge<QT, kPfxD>(a, stream);
+    if constexpr (kPfxFits<CT>)
+    {
+        hipLaunchKernelGGL((paged_decode_pfx<CT, QT>), dim3(static_cast<unsigned>(a.items), static_cast<unsigned>(gy)),
+                           dim3(64 * kPfxWaves), 0, stream, a, p);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        return launch_merge<QT, kPfxD>(a, stream);
+    }
+    else
+        return hipErrorInvalidConfiguration;  // not reached: decode_pfx_plan declines such builds
 }
 
 int env_int(const char* name, int dflt)
@@ -98,8 +111,10 @@ bool decode_pfx_plan(const DecodeArgs& a, int shared_pages, int max_chunks, Deco
     if (fused_on == 0 || a.head_dim != kPfxD || (a.cache_dtype != BF16 && a.cache_dtype != F16) || a.group > 16 ||
         shared_pages <= 0 || max_chunks <= 0 || a.num_kv_heads % kPfxWaves != 0)
         return false;
+    const void* kernel = pfx_kernel_for(a.cache_dtype, a.qo_dtype);
+    if (kernel == nullptr) return false;
     const int gy = a.num_kv_heads / kPfxWaves;  // one wave per KV head (group <= 16), four per workgroup
-    const int items = decode_mfma_items(pfx_kernel_for(a.cache_dtype, a.qo_dtype), 64 * kPfxWaves, gy);
+    const int items = decode_mfma_items(kernel, 64 * kPfxWaves, gy);
     if (items < 8) return false;
     // Prefix tasks: (kv head, chunk of pages) groups, padded to whole rounds of 8 XCDs, times blocks of 128 query
     // rows.  About one task for every fourth workgroup of the grid, at most max_chunks chunks (the workspace's
