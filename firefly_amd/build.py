@@ -11,6 +11,7 @@ the library this builds).
 from __future__ import annotations
 
 import argparse
+import hashlib
 import concurrent.futures as cf
 import os
 import shutil
@@ -61,11 +62,14 @@ def build_library(jobs: int = 8, defines: tuple[str, ...] = (), out: Path | None
     """Compile every source and link ``libffkv.so``.  Always rebuilds.
 
     ``defines`` (``NAME=VALUE`` strings) set the kernels' compile-time switches (``FFKV_*`` macros) for a variant
-    build, which is linked to ``out`` (its objects under ``_build/variant``) and leaves ``libffkv.so`` alone;
+    build, which is linked to ``out`` (its objects under ``_build/variant-<hash of the switches>``) and leaves
+    ``libffkv.so`` alone;
     ``bench.py --lib`` measures such a build beside the shipped one."""
     if defines and out is None:
         raise ValueError("a variant build (defines) needs its own output path")
-    build_dir = BUILD / "variant" if defines else BUILD
+    # each set of switches compiles into a folder of its own, so variant builds can run side by side
+    tag = hashlib.sha1(" ".join(sorted(defines)).encode()).hexdigest()[:12]
+    build_dir = BUILD / f"variant-{tag}" if defines else BUILD
     build_dir.mkdir(parents=True, exist_ok=True)
     target = Path(out) if out is not None else LIB
     target.parent.mkdir(parents=True, exist_ok=True)
