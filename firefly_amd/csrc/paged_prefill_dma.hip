@@ -85,6 +85,9 @@ constexpr int kXcds = 8;  // MI355X: workgroups are dealt to 8 XCDs (separate L2
 #ifndef FFKV_PREFILL_AHEAD
 #define FFKV_PREFILL_AHEAD 1  // with three or more stages: tiles converted in LDS one step ahead, behind the scores
 #endif
+#ifndef FFKV_PREFILL_L_MFMA
+#define FFKV_PREFILL_L_MFMA 1  // fp8 pages: the denominator of f16 P by a product with a tile of ones
+#endif
 #ifndef FFKV_PREFILL_C16
 #define FFKV_PREFILL_C16 1  // int8 pages at head_dim <= 128: tiles converted to f16 in LDS by the waves that load them
 #endif
@@ -326,6 +329,10 @@ __device__ __forceinline__ void prefill_wg(PrefillArgs a, int wg_index, uint8_t*
     // denominator sums the rounded P that the products take, two values per v_dot2_f32_f16, in place of one add
     // per p.  int8's P carries the keys' V scales, so its denominator sums p itself, as do bf16's hi + lo pairs.
     constexpr bool L_DOT = !(BF && !V16) && CT != I8;
+    // fp8 pages (operands converted as they are read): that denominator as one more product per 32 keys with a V^T
+    // tile of ones, whose every output holds the column's sum, in place of the dot products (C4-shaped fp8
+    // prefill 210.9 -> 206.7 us; bf16 and f16 pages gained nothing from it)
+    constexpr bool L_MFMA = FFKV_PREFILL_L_MFMA && R8;
 
     static_assert(PrefillLds<QT, D, CT, PFX, RG>::STAGE == 2 * C::TILEB + C::SCB, "stage layout");
     // s_vover: some accumulator is not finite after the f16 PV products (bf16 and int8 pages)
@@ -761,6 +768,7 @@ __device__ __forceinline__ void prefill_wg(PrefillArgs a, int wg_index, uint8_t*
     // result is the same softmax
     constexpr float kRerunShift = -12.0f;
     float       m_run[RG], l_run[RG];
+    f32x4       lacc[RG];  // L_MFMA: the denominator's product (every element holds the column's sum)
     float       m_thr[RG], m_neg[RG];  // m_run + thr_raw, and -m_run * c_log2 (0 before the first key)
     f32x4       acc[RG][NT];
 
@@ -893,6 +901,7 @@ __device__ __forceinline__ void prefill_wg(PrefillArgs a, int wg_index, uint8_t*
                 const bool  upd = mt > m_thr[gi];
                 const float alpha = upd ? __builtin_amdgcn_exp2f((m_run[gi] - mt) * c_log2) : 1.0f;  // 0 at first
                 l_run[gi] *= alpha;
+                if constexpr (L_MFMA && LD) lacc[gi] *= alpha;
 #pragma unroll
                 for (int n = 0; n < NT; ++n) acc[gi][n] *= alpha;
                 m_run[gi] = upd ? mt : m_run[gi];
@@ -977,7 +986,8 @@ __device__ __forceinline__ void prefill_wg(PrefillArgs a, int wg_index, uint8_t*
                         const h2 hp = __builtin_convertvector(v, h2);
                         ph[e] = __builtin_bit_cast(uint32_t, hp);
                         pl[e] = 0u;
-                        if constexpr (LD) l_run[gi] = __builtin_amdgcn_fdot2(hp, h2{1, 1}, l_run[gi], false);
+                        if constexpr (LD && !L_MFMA)
+                            l_run[gi] = __builtin_amdgcn_fdot2(hp, h2{1, 1}, l_run[gi], false);
                     }
                 }
                 phi[gi] = __builtin_bit_cast(XP, u32x4{ph[0], ph[1], ph[2], ph[3]});
@@ -998,6 +1008,13 @@ __device__ __forceinline__ void prefill_wg(PrefillArgs a, int wg_index, uint8_t*
                     if constexpr (PBF) acc[gi][n] = MP::mma32(vcur, plo[gi], acc[gi][n]);
                 }
                 vcur = vnxt;
+                if constexpr (LD && L_MFMA)
+                    if (n == 0)
+                    {
+                        const XP ones = __builtin_bit_cast(XP, u32x4{0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u});
+#pragma unroll
+                        for (int gi = 0; gi < RG; ++gi) lacc[gi] = MP::mma32(ones, phi[gi], lacc[gi]);
+                    }
             }
             mfma_priority<R8>(0);
         }
@@ -1105,6 +1122,7 @@ __device__ __forceinline__ void prefill_wg(PrefillArgs a, int wg_index, uint8_t*
             m_thr[gi] = kNegInf;
             m_neg[gi] = 0.0f;
             l_run[gi] = 0.0f;
+            lacc[gi] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int n = 0; n < NT; ++n) acc[gi][n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
         }
@@ -1190,7 +1208,7 @@ __device__ __forceinline__ void prefill_wg(PrefillArgs a, int wg_index, uint8_t*
 #pragma unroll
     for (int gi = 0; gi < RG; ++gi)
     {
-        const float l_tot = swap_sum(l_run[gi]);
+        const float l_tot = swap_sum(l_run[gi]) + lacc[gi][0];  // whichever of the two the pipeline filled
         if constexpr (PFX)
         {
             // partial of (row bq, head hq) over this chunk, in the decode merge's convention: max in the log2 domain
